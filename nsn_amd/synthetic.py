@@ -1,0 +1,92 @@
+"""Seeded synthetic K/V/query generators for the benchmark configurations.
+
+The reference publishes no K/V arrays for these shapes (its saved inputs are in
+release ZIPs that are not available offline), so every configuration is built
+from a stated generator:
+
+* ``kv_tokens``: a unit direction drawn from N(0, I_128) and normalised, times a
+  per-token norm drawn from lognormal(0, 1); ``round(0.02 * rows)`` rows chosen
+  by the same generator are scaled by 20 (outlier tokens).
+* ``heavy_tailed_tokens``: per-channel Student-t (df=3) values times lognormal
+  token norms (the 5-bit configuration).
+
+``numpy.random.default_rng(seed)`` drives the small CPU-sized cases.  The
+full-size cases draw on the GPU from ``torch.Generator(device='cuda')`` with the
+same seed (a different stream of numbers, same distribution), because
+generating half a billion fp16 values through numpy would dominate the run.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+DIM = 128
+
+
+def kv_tokens(rng, prefix, ntok, dim=DIM, outlier_frac=0.02, outlier_scale=20.0):
+    """fp16 array [*prefix, ntok, dim] (see module docstring)."""
+    shape = tuple(prefix) + (ntok, dim)
+    u = rng.standard_normal(shape)
+    u /= np.linalg.norm(u, axis=-1, keepdims=True)
+    nrm = rng.lognormal(0.0, 1.0, tuple(prefix) + (ntok, 1))
+    rows = int(np.prod(tuple(prefix) + (ntok,)))
+    k = int(round(outlier_frac * rows))
+    if k:
+        idx = rng.choice(rows, size=k, replace=False)
+        nrm.reshape(-1)[idx] *= outlier_scale
+    return (u * nrm).astype(np.float16)
+
+
+def heavy_tailed_tokens(rng, prefix, ntok, dim=DIM, df=3.0):
+    shape = tuple(prefix) + (ntok, dim)
+    x = rng.standard_t(df, shape)
+    x /= np.linalg.norm(x, axis=-1, keepdims=True)
+    nrm = rng.lognormal(0.0, 1.0, tuple(prefix) + (ntok, 1))
+    return (x * nrm).astype(np.float16)
+
+
+def config0(seed=0):
+    """C0: K and V fp16 [32 heads, 64 tokens, 128], seed 0 (K drawn first)."""
+    rng = np.random.default_rng(seed)
+    k = kv_tokens(rng, (32,), 64)
+    v = kv_tokens(rng, (32,), 64)
+    return k, v
+
+
+def ragged_lengths(seed, batch, lo, hi):
+    """Per-sequence context lengths uniform in [lo, hi] (inclusive)."""
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=batch).astype(np.int64)
+
+
+# ------------------------------------------------------------- device side
+
+def kv_tokens_torch(gen, shape, device, outlier_frac=0.02, outlier_scale=20.0, dtype=None):
+    """GPU version of ``kv_tokens``: fp16 tensor of ``shape`` [..., T, 128]."""
+    import torch
+    dtype = dtype or torch.float16
+    u = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    u = u / torch.linalg.vector_norm(u, dim=-1, keepdim=True)
+    nrm = torch.empty(shape[:-1] + (1,), device=device, dtype=torch.float32)
+    nrm.log_normal_(0.0, 1.0, generator=gen)
+    rows = nrm.numel()
+    k = int(round(outlier_frac * rows))
+    if k:
+        idx = torch.randperm(rows, generator=gen, device=device)[:k]
+        nrm.view(-1)[idx] *= outlier_scale
+    return (u * nrm).to(dtype)
+
+
+def heavy_tailed_torch(gen, shape, device, df=3.0, dtype=None):
+    """GPU Student-t(df) channels (as N / sqrt(chi2/df)) times lognormal norms."""
+    import torch
+    dtype = dtype or torch.float16
+    z = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    g = torch.zeros(shape, device=device, dtype=torch.float32)
+    for _ in range(int(df)):
+        e = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+        g += e * e
+    x = z / torch.sqrt(g / df)
+    x = x / torch.linalg.vector_norm(x, dim=-1, keepdim=True)
+    nrm = torch.empty(shape[:-1] + (1,), device=device, dtype=torch.float32)
+    nrm.log_normal_(0.0, 1.0, generator=gen)
+    return (x * nrm).to(dtype)
