@@ -1,0 +1,194 @@
+/*
+ * nsn_hip.h -- C ABI of libnsn_hip.so, the MI355X (gfx950) NSN packed-KV hot path.
+ *
+ * The reference (metaSATOKEN/nsn) exposes this path as Python module
+ * functions over Triton kernels and torch eager ops; each entry point below
+ * replaces one group of them (citations relative to the reference root).
+ * Conventions:
+ *   - every pointer is device memory owned by the caller; the library never
+ *     allocates; inputs are never written;
+ *   - all work is enqueued on `stream` (a hipStream_t); calls are asynchronous;
+ *   - data-dependent failures (nonfinite values, fp16 metadata overflow, code
+ *     range) are OR-ed into the caller's device status word `status` (int32,
+ *     NSN_ST_* bits) -- the caller reads it when it needs to raise;
+ *   - the return value reports argument / launch errors (NSN_OK == 0).
+ * Packed layout (the reference's, see loop_kv_pk01_cache.py:7-37):
+ *   block = 64 tokens x 128 channels of one (sequence, kv-head);
+ *   codes: LSB-first bitstream, code of (token t, channel c) at bits
+ *          [(t*128+c)*bits, +bits) of the block's 64*128*bits/8 bytes;
+ *   norm:  fp16 [64] per block; min, scale: fp16 [128] per block;
+ *   header: 12 bytes '<QHBB' = (token offset u64, 64 u16, bits u8, 0 u8).
+ */
+#ifndef NSN_HIP_H
+#define NSN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *nsn_stream_t; /* == hipStream_t */
+
+enum { NSN_DTYPE_F16 = 0, NSN_DTYPE_BF16 = 1, NSN_DTYPE_F32 = 2 };
+
+/* Order of the fp32 sum of squares in the encoder's token norm.  torch's CPU
+ * vector_norm uses 8 fma lanes (elements j, j+8, ...; lanes summed in order)
+ * for a contiguous row, and one fma chain when the row is strided. */
+enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
+
+/* Status-word bits. */
+#define NSN_ST_NONFINITE_INPUT 0x01   /* encode: nonfinite input            */
+#define NSN_ST_META_NONFINITE 0x02    /* encode: fp16 metadata overflow/NaN  */
+#define NSN_ST_META_UNDERFLOW 0x04    /* encode: nonzero norm/step -> fp16 0 */
+#define NSN_ST_CODE_RANGE 0x08        /* pack: code >= 2^bits                */
+#define NSN_ST_NONFINITE_RESTORE 0x10 /* restore: nonfinite reconstruction   */
+#define NSN_ST_NONFINITE_ATTN 0x20    /* attention: nonfinite score/weights  */
+#define NSN_ST_NONFINITE_OUTPUT 0x40  /* attention merge: nonfinite context  */
+#define NSN_ST_NONFINITE_SCAN 0x80    /* finite scan: nonfinite raw input    */
+
+/* Return codes. */
+#define NSN_OK 0
+#define NSN_EINVAL (-1)
+#define NSN_ELAUNCH (-2)
+
+/* Library version string. */
+const char *nsn_version(void);
+
+/*
+ * Encode 64x128 blocks: token norm, per-channel min/max over the block,
+ * round-half-even codes, LSB-first packing, fp16 metadata, headers.
+ * Replaces nsn_encode (experiments/ac08/source/loop_kv_pilot.py:195-213),
+ * pack3 (experiments/ac08/source/loop_kv_pk01_cache.py:7-16) and the header
+ * loop of encode_group (loop_kv_pk01_cache.py:31-37).
+ *   x: input rows of 128 elements (x_dtype), contiguous within a row; block
+ *      (o, i) starts at element o*x_outer_stride + (x_token_offset + 64*i)*128.
+ *      16-byte aligned.
+ *   Output block (o, i) lands at index ob = o*out_outer_blocks + out_block_offset + i
+ *   of codes [*, 64*128*bits/8], norms [*, 64], mins/scales [*, 128] (fp16
+ *   bits) and headers [*, 12] (nullable); its header token is
+ *   header_start_token + 64*i.
+ *   codes_unpacked (nullable): [n_outer*n_blocks, 64, 128] u8 codes.
+ *   zero_flat_scale: 1 = nsn_encode (codes forced to 0 where scale == 0),
+ *                    0 = nsn_int3_qdq (identical outputs for finite input).
+ */
+int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blocks,
+                      int64_t x_outer_stride, int64_t x_token_offset, int bits, int norm_order,
+                      int zero_flat_scale, uint8_t *codes, uint16_t *norms, uint16_t *mins,
+                      uint16_t *scales, uint8_t *headers, int64_t out_outer_blocks,
+                      int64_t out_block_offset, int64_t header_start_token,
+                      uint8_t *codes_unpacked, int32_t *status, nsn_stream_t stream);
+
+/*
+ * LSB-first bitstream of `count` codes (bits in {3,4,5}) -> (count*bits+7)/8 bytes.
+ * Replaces pack_codes (loop_kv_pilot.py:171-181) and pack3 (loop_kv_pk01_cache.py:7-16).
+ * Codes >= 2^bits set NSN_ST_CODE_RANGE.
+ */
+int nsn_pack_codes(const uint8_t *codes, int64_t count, int bits, uint8_t *out, int32_t *status,
+                   nsn_stream_t stream);
+
+/*
+ * Inverse of nsn_pack_codes.  Replaces unpack3 (loop_kv_pk01_cache.py:19-28),
+ * the PU01 kernel (experiments/ac08/source/loop_kv_pu01_kernel.py:32-52) and
+ * unpack_codes_reference (loop_kv_pilot.py:183-193).
+ */
+int nsn_unpack_codes(const uint8_t *payload, int64_t count, int bits, uint8_t *out,
+                     nsn_stream_t stream);
+
+/*
+ * Reconstruct blocks (nsn_decode arithmetic: d = m + s*q, y = n*(d/max(|d|,1e-12)),
+ * n==0 -> 0, RNE cast) and append a tail.
+ * Replaces nsn_decode (loop_kv_pilot.py:216-225), restore_group
+ * (loop_kv_pk01_cache.py:40-42, loop_kv_rf01_kernel.py:60-74,
+ * loop_kv_pu01_kernel.py:54-56) and the bridge restore_v/materialize
+ * (experiments/ac08/source/loop_kv_vf01_kernel.py:47-54,120-126).
+ *   codes: packed [n_outer, in_outer_blocks, 64*128*bits/8] (codes_are_unpacked=0)
+ *          or unpacked u8 [n_outer, in_outer_blocks, 64, 128] (codes_are_unpacked=1);
+ *   norms/mins/scales: [n_outer, in_outer_blocks, 64|128] fp16 bits;
+ *   out: [n_outer, out_outer_tokens, 128] out_dtype; tokens [0, 64*n_blocks)
+ *        restored, tokens [64*n_blocks, 64*n_blocks + tail_len) copied from
+ *        tail [n_outer, tail_outer_tokens, 128] tail_dtype (tail nullable when
+ *        tail_len == 0).
+ */
+int nsn_restore_blocks(const uint8_t *codes, int codes_are_unpacked, const uint16_t *norms,
+                       const uint16_t *mins, const uint16_t *scales, int64_t n_outer,
+                       int64_t n_blocks, int64_t in_outer_blocks, int bits, void *out,
+                       int out_dtype, int64_t out_outer_tokens, const void *tail,
+                       int tail_dtype, int64_t tail_len, int64_t tail_outer_tokens,
+                       int32_t *status, nsn_stream_t stream);
+
+/* K/V sources of the decode attention. */
+enum {
+    NSN_KV_PACKED = 0,  /* packed blocks for tokens < 64*blocks[b], then the tail buffer */
+    NSN_KV_SCORES = 1   /* (K side only) fp32 logits given: the AF01 FULL=False readout */
+};
+
+/* Attention kernels. */
+enum {
+    NSN_ATTN_REFERENCE = 0, /* exact-order: nsn_decode restore, K/V rounded to kv_round_dtype,
+                               fp32 QK / online softmax / PV (route-equal bridge and fused) */
+    NSN_ATTN_FAST = 1       /* factored MFMA kernel (codes on matrix cores); tolerance-equal */
+};
+
+typedef struct {
+    const uint8_t *codes;   /* [B, Hkv, block_cap, 64*128*bits/8] */
+    const uint16_t *norms;  /* [B, Hkv, block_cap, 64]  fp16 */
+    const uint16_t *mins;   /* [B, Hkv, block_cap, 128] fp16 */
+    const uint16_t *scales; /* [B, Hkv, block_cap, 128] fp16 */
+    const int32_t *blocks;  /* [B] packed blocks per sequence (nullable -> 0) */
+    int64_t block_cap;
+    const void *tail;       /* [B, Hkv, tail_cap, 128] tail_dtype: tokens 64*blocks[b] .. */
+    int tail_dtype;
+    int64_t tail_cap;
+} nsn_kv_side;
+
+typedef struct {
+    const void *q;          /* [B, Hq, 128] q_dtype */
+    int q_dtype;
+    int64_t batch, heads_q, heads_kv; /* heads_q = G * heads_kv; q-head h reads kv-head h / G */
+    float scale;            /* 1/sqrt(128) = 0.08838834764831845 */
+    const int32_t *seq_len; /* [B] tokens per sequence (>0) */
+    int max_seq_len;        /* >= every seq_len[b] */
+    int bits;               /* 3, 4 or 5 */
+    int k_mode;             /* NSN_KV_PACKED | NSN_KV_SCORES */
+    nsn_kv_side k, v;
+    const float *scores;    /* [B, Hq, scores_cap] fp32 (k_mode == NSN_KV_SCORES) */
+    int64_t scores_cap;
+    int kernel;             /* NSN_ATTN_REFERENCE | NSN_ATTN_FAST */
+    int kv_round_dtype;     /* reference kernel: dtype restored K/V are rounded to */
+    int split_tokens;       /* tokens per split (multiple of 64) */
+    int n_splits;           /* ceil(max_seq_len / split_tokens) */
+    float *partials;        /* workspace [B, Hq, n_splits, 132] fp32 */
+    float *ctx;             /* [B, Hq, 128] fp32 (nullable) */
+    void *out;              /* [B, Hq, 128] out_dtype */
+    int out_dtype;
+    int32_t *status;
+} nsn_attn_args;
+
+/*
+ * Single-query decode attention over packed K/V (+ tail), split over the
+ * context with a log-sum-exp merge.  Replaces the VF01 fused route
+ * (experiments/ac08/source/loop_kv_vf01_kernel.py:56-139), AF01 partial/merge
+ * (experiments/ac08/source/loop_kv_af01_kernel.py:13-111) and the GQA route
+ * (experiments/nb06/source/loop_kv_nb06_kernel.py:54-154).  A dense fp16/bf16
+ * K/V baseline is the same call with blocks == NULL.
+ */
+int nsn_decode_attention(const nsn_attn_args *args, nsn_stream_t stream);
+
+/* Workspace floats needed by nsn_decode_attention for the given shape. */
+int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits);
+
+/*
+ * NaN/Inf scan over up to 16 arrays; array i sets bit i of flags[0] (int32)
+ * and NSN_ST_NONFINITE_SCAN in status.  Replaces the grouped finite checks
+ * (experiments/ac08/source/loop_kv_vf01_checks.py:20-63,
+ * loop_kv_iv01_kernel.py:29-46).
+ */
+int nsn_finite_scan(int n_arrays, const void *const *ptrs, const int64_t *counts,
+                    const int *dtypes, int32_t *flags, int32_t *status, nsn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSN_HIP_H */

@@ -1,0 +1,82 @@
+"""ctypes binding of libnsn_hip.so (declared in include/nsn_hip.h).
+
+There is no CPU fallback: if the library is missing or no GPU is visible, the
+ops raise.  The library is built in-tree by ``python -m nsn_amd.build`` (or
+``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_build" / "libnsn_hip.so"
+
+# dtype / mode enums (include/nsn_hip.h)
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
+NORM_LANES8, NORM_SEQUENTIAL = 0, 1
+KV_PACKED, KV_SCORES = 0, 1
+ATTN_REFERENCE, ATTN_FAST = 0, 1
+
+ST_NONFINITE_INPUT = 0x01
+ST_META_NONFINITE = 0x02
+ST_META_UNDERFLOW = 0x04
+ST_CODE_RANGE = 0x08
+ST_NONFINITE_RESTORE = 0x10
+ST_NONFINITE_ATTN = 0x20
+ST_NONFINITE_OUTPUT = 0x40
+ST_NONFINITE_SCAN = 0x80
+
+NSN_OK, NSN_EINVAL, NSN_ELAUNCH = 0, -1, -2
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int
+I64 = ctypes.c_int64
+
+
+class KVSide(ctypes.Structure):
+    _fields_ = [("codes", P), ("norms", P), ("mins", P), ("scales", P), ("blocks", P),
+                ("block_cap", I64), ("tail", P), ("tail_dtype", I32), ("tail_cap", I64)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", P), ("q_dtype", I32), ("batch", I64), ("heads_q", I64), ("heads_kv", I64),
+                ("scale", ctypes.c_float), ("seq_len", P), ("max_seq_len", I32), ("bits", I32),
+                ("k_mode", I32), ("k", KVSide), ("v", KVSide), ("scores", P), ("scores_cap", I64),
+                ("kernel", I32), ("kv_round_dtype", I32), ("split_tokens", I32), ("n_splits", I32),
+                ("partials", P), ("ctx", P), ("out", P), ("out_dtype", I32), ("status", P)]
+
+
+# symbol -> (restype, argtypes); must cover every function include/nsn_hip.h declares
+SIGNATURES = {
+    "nsn_version": (ctypes.c_char_p, []),
+    "nsn_encode_blocks": (I32, [P, I32, I64, I64, I64, I64, I32, I32, I32, P, P, P, P, P, I64, I64, I64, P, P, P]),
+    "nsn_pack_codes": (I32, [P, I64, I32, P, P, P]),
+    "nsn_unpack_codes": (I32, [P, I64, I32, P, P]),
+    "nsn_restore_blocks": (I32, [P, I32, P, P, P, I64, I64, I64, I32, P, I32, I64, P, I32, I64, I64, P, P]),
+    "nsn_decode_attention": (I32, [ctypes.POINTER(AttnArgs), P]),
+    "nsn_attention_workspace_floats": (I64, [I64, I64, I32]),
+    "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"NSN HIP library not built ({LIB_PATH}); run `python -m nsn_amd.build`")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc, what):
+    if rc != NSN_OK:
+        kind = {NSN_EINVAL: "invalid arguments", NSN_ELAUNCH: "kernel launch failed"}.get(rc, str(rc))
+        raise RuntimeError(f"{what}: {kind}")

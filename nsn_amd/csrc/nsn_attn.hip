@@ -1,0 +1,437 @@
+// Single-query decode attention over NSN-packed K/V for gfx950.
+//
+// Work unit = (sequence b, kv-head, context split).  Each unit serves all
+// G = Hq/Hkv query heads of its kv-head, so every packed block is read and
+// reconstructed once per kv-head (the reference's GQA kernel reconstructs it
+// once per query head, experiments/nb06/source/loop_kv_nb06_kernel.py:56).
+// Each unit writes per-head softmax partials (running max, sum, weighted V);
+// a merge kernel combines the splits (log-sum-exp), as the reference's AF01
+// merge does (experiments/ac08/source/loop_kv_af01_kernel.py:70-82).
+//
+// This file holds the exact-order ("reference") kernel: K and V tiles are
+// reconstructed with nsn_decode's arithmetic (loop_kv_pilot.py:216-225),
+// rounded to the attention dtype as the reference's read_v does
+// (loop_kv_vf01_kernel.py:34), and QK / softmax / PV run in fp32 with
+// unfused multiply-add.  Because a restored tile and the same values read
+// back from HBM go through identical arithmetic, the bridge route (restore V
+// to HBM, then attend) and the fused route give bitwise-equal outputs -- the
+// reference's route-equality property (AC/verify_loop_kv_vf01.py:41-50).
+#include "nsn_common.hpp"
+
+namespace nsn {
+
+constexpr int kPartStride = 132;  // floats per (b, hq, split) partial: m, l, pad, pad, acc[128]
+constexpr int kMaxGroup = 16;
+
+struct SideParams {
+    const uint8_t *codes;
+    const uint16_t *norms, *mins, *scales;
+    const int32_t *blocks;
+    int64_t block_cap;
+    const void *tail;
+    int64_t tail_cap;
+};
+
+struct AttnParams {
+    const void *q;
+    int64_t heads_q, heads_kv;
+    int group;
+    float scale;
+    const int32_t *seq_len;
+    int split_tokens, n_splits;
+    SideParams k, v;
+    const float *scores;
+    int64_t scores_cap;
+    float *partials;
+    int32_t *status;
+};
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void *base, int64_t idx) {
+    return Elem<DT>::load(static_cast<const typename Elem<DT>::T *>(base)[idx]);
+}
+
+// Reconstruct packed block `blk` of row `row` (= b*Hkv + kvh) into tile[64][kXP]
+// as fp32 values already rounded to RDT.  Returns true if any value is nonfinite.
+template <int BITS, int RDT>
+__device__ bool restore_tile(const SideParams &sd, int64_t row, int64_t blk, float *tile, uint32_t *codes_s,
+                             float *m_s, float *s_s, float *n_s, double *rden_s) {
+    constexpr int kXP = kDim + 4;
+    const int tid = threadIdx.x;
+    const int64_t ib = row * sd.block_cap + blk;
+    if (tid < kDim) {
+        m_s[tid] = f16_bits_to_f32(sd.mins[ib * kDim + tid]);
+        s_s[tid] = f16_bits_to_f32(sd.scales[ib * kDim + tid]);
+    } else if (tid < kDim + kBlockTok) {
+        n_s[tid - kDim] = f16_bits_to_f32(sd.norms[ib * kBlockTok + tid - kDim]);
+    }
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(sd.codes + ib * packed_block_bytes(BITS)) + tid * BITS;
+        uint32_t w[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) w[k] = src[k];
+        constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = 4 * k + e, pos = i * BITS, d = pos >> 5, sh = pos & 31;
+                uint32_t v = w[d] >> sh;
+                if (sh + BITS > 32) v |= w[d + 1] << (32 - sh);
+                word |= (v & mask) << (8 * e);
+            }
+            codes_s[tid * 8 + k] = word;
+        }
+    }
+    __syncthreads();
+    {
+        const int r = tid >> 2, jp = (tid & 3) * 2;
+        const uint8_t *cr = reinterpret_cast<const uint8_t *>(codes_s) + r * kDim;
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int c = 8 * k + jp;
+            const float p0 = s_s[c] * static_cast<float>(cr[c]);
+            const float p1 = s_s[c + 1] * static_cast<float>(cr[c + 1]);
+            const float d0 = m_s[c] + p0, d1 = m_s[c + 1] + p1;
+            a0 = __builtin_fmaf(d0, d0, a0);
+            a1 = __builtin_fmaf(d1, d1, a1);
+        }
+        const float b0 = __shfl_down(a0, 1), b1 = __shfl_down(a1, 1);
+        const float c0 = __shfl_down(a0, 2), c1 = __shfl_down(a1, 2);
+        const float d0 = __shfl_down(a0, 3), d1 = __shfl_down(a1, 3);
+        if ((tid & 3) == 0) {
+            const float acc[8] = {a0, a1, b0, b1, c0, c1, d0, d1};
+            rden_s[r] = recip_rn(clamp_eps(sqrt_rn(lane8_sum(acc))));
+        }
+    }
+    __syncthreads();
+    bool bad = false;
+    const int cg = tid & 15, r0 = tid >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = r0 + 16 * j;
+        const uint8_t *cr = reinterpret_cast<const uint8_t *>(codes_s) + r * kDim;
+        const float n = n_s[r];
+        const double rd = rden_s[r];
+        float *dst = tile + r * kXP + 8 * cg;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int c = 8 * cg + e;
+            const float prod = s_s[c] * static_cast<float>(cr[c]);
+            const float d = m_s[c] + prod;
+            const float val = n * div_by_recip(d, rd);
+            float y = (n == 0.f) ? 0.f : val;
+            y = Elem<RDT>::load(Elem<RDT>::store(y));
+            bad |= !finite(y);
+            dst[e] = y;
+        }
+    }
+    return bad;
+}
+
+// Dense tile: tokens [t0, t0 + valid) of the tail buffer row, zero beyond.
+template <int TDT>
+__device__ bool dense_tile(const SideParams &sd, int64_t row, int64_t t0, int valid, float *tile) {
+    constexpr int kXP = kDim + 4;
+    const int tid = threadIdx.x;
+    const int cg = tid & 15, r0 = tid >> 4;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = r0 + 16 * j;
+        float *dst = tile + r * kXP + 8 * cg;
+        if (r < valid) {
+            const int64_t base = (row * sd.tail_cap + t0 + r) * kDim + 8 * cg;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                dst[e] = load_elem<TDT>(sd.tail, base + e);
+                bad |= !finite(dst[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dst[e] = 0.f;
+        }
+    }
+    return bad;
+}
+
+template <int BITS, int RDT, int TDT>
+__device__ bool load_tile(const SideParams &sd, int64_t row, int b, int64_t t0, int valid, float *tile,
+                          uint32_t *codes_s, float *m_s, float *s_s, float *n_s, double *rden_s) {
+    const int64_t nb = sd.blocks ? sd.blocks[b] : 0;
+    if (t0 < nb * kBlockTok)
+        return restore_tile<BITS, RDT>(sd, row, t0 / kBlockTok, tile, codes_s, m_s, s_s, n_s, rden_s);
+    return dense_tile<TDT>(sd, row, t0 - nb * kBlockTok, valid, tile);
+}
+
+template <int BITS, int QDT, int RDT, int TDT, bool SCORES>
+__global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
+    constexpr int kXP = kDim + 4;
+    __shared__ float tile[kBlockTok * kXP];
+    __shared__ uint32_t codes_s[kBlockTok * kDim / 4];
+    __shared__ float m_s[kDim], s_s[kDim], n_s[kBlockTok];
+    __shared__ double rden_s[kBlockTok];
+    __shared__ float q_s[kMaxGroup * kDim];
+    __shared__ float sc_s[kMaxGroup * kBlockTok];
+    __shared__ float run_m[kMaxGroup], run_l[kMaxGroup], alpha_s[kMaxGroup];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int G = p.group;
+    const int64_t row = static_cast<int64_t>(b) * p.heads_kv + kvh;
+    const int64_t T = p.seq_len[b];
+    const int64_t t_begin = static_cast<int64_t>(split) * p.split_tokens;
+    const int64_t t_end = t_begin + p.split_tokens < T ? t_begin + p.split_tokens : T;
+    const int64_t hq0 = static_cast<int64_t>(kvh) * G;
+
+    // thread -> accumulator slots: heads wave, wave+4, ...; channels 2*lane, 2*lane+1
+    float acc[kMaxGroup / 4][2];
+#pragma unroll
+    for (int k = 0; k < kMaxGroup / 4; ++k) acc[k][0] = acc[k][1] = 0.f;
+
+    for (int i = tid; i < G * kDim; i += 256) {
+        const int h = i / kDim, c = i - h * kDim;
+        q_s[i] = load_elem<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + c);
+    }
+    if (tid < G) { run_m[tid] = -INFINITY; run_l[tid] = 0.f; }
+    bool bad_attn = false, bad_restore = false;
+    __syncthreads();
+
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBlockTok) {
+        const int valid = static_cast<int>(t_end - t0 < kBlockTok ? t_end - t0 : kBlockTok);
+        // ---- scores [G][64] ----
+        if constexpr (SCORES) {
+            for (int i = tid; i < G * kBlockTok; i += 256) {
+                const int h = i / kBlockTok, t = i - h * kBlockTok;
+                float s = -INFINITY;
+                if (t < valid) {
+                    s = p.scores[(static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.scores_cap + t0 + t];
+                    bad_attn |= !finite(s);
+                }
+                sc_s[i] = s;
+            }
+        } else {
+            bad_restore |= load_tile<BITS, RDT, TDT>(p.k, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+            __syncthreads();
+            const int r = tid >> 2, qq = tid & 3;
+            for (int h = 0; h < G; ++h) {
+                float part = 0.f;
+                const float *kr = tile + r * kXP + 32 * qq;
+                const float *qh = q_s + h * kDim + 32 * qq;
+#pragma unroll 8
+                for (int c = 0; c < 32; ++c) {
+                    const float prod = kr[c] * qh[c];
+                    part = part + prod;
+                }
+                const float o1 = __shfl_down(part, 1), o2 = __shfl_down(part, 2), o3 = __shfl_down(part, 3);
+                if (qq == 0) {
+                    float s = ((part + o1) + o2) + o3;
+                    s = s * p.scale;
+                    if (r < valid) bad_attn |= !finite(s);
+                    sc_s[h * kBlockTok + r] = (r < valid) ? s : -INFINITY;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- online softmax per head: wave w handles heads w, w+4, ... ----
+        for (int h = wave; h < G; h += 4) {
+            const float s = sc_s[h * kBlockTok + lane];
+            float mx = s;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float o = __shfl_xor(mx, off);
+                mx = o > mx ? o : mx;
+            }
+            const float m_old = run_m[h];
+            const float m_new = m_old > mx ? m_old : mx;
+            const float pw = (lane < valid) ? expf(s - m_new) : 0.f;
+            float sum = pw;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) sum = sum + __shfl_xor(sum, off);
+            sc_s[h * kBlockTok + lane] = pw;
+            if (lane == 0) {
+                const float alpha = (m_old == -INFINITY) ? 0.f : expf(m_old - m_new);
+                alpha_s[h] = alpha;
+                run_m[h] = m_new;
+                run_l[h] = run_l[h] * alpha + sum;
+                if (!finite(sum) || !finite(m_new)) bad_attn = true;
+            }
+        }
+        __syncthreads();
+        // ---- V tile and P.V ----
+        bad_restore |= load_tile<BITS, RDT, TDT>(p.v, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kMaxGroup / 4; ++k) {
+            const int h = wave + 4 * k;
+            if (h < G) {
+                const float alpha = alpha_s[h];
+                float a0 = acc[k][0] * alpha, a1 = acc[k][1] * alpha;
+                const float *ph = sc_s + h * kBlockTok;
+                for (int t = 0; t < valid; ++t) {
+                    const float w = ph[t];
+                    const float2 vv = *reinterpret_cast<const float2 *>(tile + t * kXP + 2 * lane);
+                    const float p0 = w * vv.x, p1 = w * vv.y;
+                    a0 = a0 + p0;
+                    a1 = a1 + p1;
+                }
+                acc[k][0] = a0;
+                acc[k][1] = a1;
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- partials ----
+#pragma unroll
+    for (int k = 0; k < kMaxGroup / 4; ++k) {
+        const int h = wave + 4 * k;
+        if (h < G) {
+            float *dst = p.partials + ((static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.n_splits + split) * kPartStride;
+            if (lane == 0) { dst[0] = run_m[h]; dst[1] = run_l[h]; dst[2] = 0.f; dst[3] = 0.f; }
+            *reinterpret_cast<float2 *>(dst + 4 + 2 * lane) = make_float2(acc[k][0], acc[k][1]);
+            bad_attn |= !finite(acc[k][0]) || !finite(acc[k][1]);
+        }
+    }
+    int st = (bad_attn ? NSN_ST_NONFINITE_ATTN : 0) | (bad_restore ? NSN_ST_NONFINITE_RESTORE : 0);
+    if (__any(st != 0)) {
+        if (st) raise_status(p.status, st);
+    }
+}
+
+// Merge splits: one 128-thread block per (b, hq).
+template <int ODT>
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *partials, int n_splits, float *ctx, void *out,
+                                                         int32_t *status) {
+    const int64_t bh = blockIdx.x;
+    const int c = threadIdx.x;
+    const float *base = partials + bh * n_splits * kPartStride;
+    float L = -INFINITY;
+    for (int s = 0; s < n_splits; ++s) {
+        const float m = base[s * kPartStride];
+        L = m > L ? m : L;
+    }
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < n_splits; ++s) {
+        const float m = base[s * kPartStride];
+        const float a = (m == -INFINITY) ? 0.f : expf(m - L);
+        const float zp = base[s * kPartStride + 1] * a;
+        const float up = base[s * kPartStride + 4 + c] * a;
+        den = den + zp;
+        num = num + up;
+    }
+    const float cx = num / den;
+    const typename Elem<ODT>::T ov = Elem<ODT>::store(cx);
+    if (ctx) ctx[bh * kDim + c] = cx;
+    static_cast<typename Elem<ODT>::T *>(out)[bh * kDim + c] = ov;
+    const bool bad = !finite(cx) || !finite(Elem<ODT>::load(ov)) || !(den > 0.f);
+    if (bad) raise_status(status, NSN_ST_NONFINITE_OUTPUT);
+}
+
+}  // namespace nsn
+
+using namespace nsn;
+
+namespace {
+
+bool side_ok(const nsn_kv_side &s, int bits) {
+    (void)bits;
+    if (s.blocks && (!s.codes || !s.norms || !s.mins || !s.scales)) return false;
+    if (s.codes && (reinterpret_cast<uintptr_t>(s.codes) & 15u)) return false;
+    return true;
+}
+
+SideParams to_side(const nsn_kv_side &s) {
+    return SideParams{s.codes, s.norms, s.mins, s.scales, s.blocks, s.block_cap, s.tail, s.tail_cap};
+}
+
+template <int BITS, int QDT, int RDT, int TDT>
+int launch_reference_scores(bool scores, dim3 grid, hipStream_t st, const AttnParams &p) {
+    if (scores) hipLaunchKernelGGL((attn_reference_kernel<BITS, QDT, RDT, TDT, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_reference_kernel<BITS, QDT, RDT, TDT, false>), grid, dim3(256), 0, st, p);
+    return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
+}
+
+template <int BITS, int QDT, int RDT>
+int dispatch_tail(int tdt, bool scores, dim3 grid, hipStream_t st, const AttnParams &p) {
+    if (tdt == NSN_DTYPE_F16) return launch_reference_scores<BITS, QDT, RDT, NSN_DTYPE_F16>(scores, grid, st, p);
+    if (tdt == NSN_DTYPE_BF16) return launch_reference_scores<BITS, QDT, RDT, NSN_DTYPE_BF16>(scores, grid, st, p);
+    return NSN_EINVAL;
+}
+
+template <int BITS, int QDT>
+int dispatch_round(int rdt, int tdt, bool scores, dim3 grid, hipStream_t st, const AttnParams &p) {
+    if (rdt == NSN_DTYPE_F16) return dispatch_tail<BITS, QDT, NSN_DTYPE_F16>(tdt, scores, grid, st, p);
+    if (rdt == NSN_DTYPE_BF16) return dispatch_tail<BITS, QDT, NSN_DTYPE_BF16>(tdt, scores, grid, st, p);
+    return dispatch_tail<BITS, QDT, NSN_DTYPE_F32>(tdt, scores, grid, st, p);
+}
+
+template <int BITS>
+int dispatch_q(int qdt, int rdt, int tdt, bool scores, dim3 grid, hipStream_t st, const AttnParams &p) {
+    if (qdt == NSN_DTYPE_BF16) return dispatch_round<BITS, NSN_DTYPE_BF16>(rdt, tdt, scores, grid, st, p);
+    if (qdt == NSN_DTYPE_F16) return dispatch_round<BITS, NSN_DTYPE_F16>(rdt, tdt, scores, grid, st, p);
+    return dispatch_round<BITS, NSN_DTYPE_F32>(rdt, tdt, scores, grid, st, p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits) {
+    return batch * heads_q * static_cast<int64_t>(n_splits) * kPartStride;
+}
+
+int nsn_decode_attention(const nsn_attn_args *a, nsn_stream_t stream) {
+    if (!a) return NSN_EINVAL;
+    if (a->batch <= 0 || a->heads_kv <= 0 || a->heads_q <= 0 || a->heads_q % a->heads_kv) return NSN_EINVAL;
+    const int64_t G = a->heads_q / a->heads_kv;
+    if (G > kMaxGroup) return NSN_EINVAL;
+    if (a->bits != 3 && a->bits != 4 && a->bits != 5) return NSN_EINVAL;
+    if (!a->q || !a->seq_len || !a->partials || !a->out) return NSN_EINVAL;
+    if (a->split_tokens <= 0 || a->split_tokens % kBlockTok || a->n_splits <= 0) return NSN_EINVAL;
+    if (static_cast<int64_t>(a->n_splits) * a->split_tokens < a->max_seq_len) return NSN_EINVAL;
+    const bool scores = a->k_mode == NSN_KV_SCORES;
+    if (!scores && a->k_mode != NSN_KV_PACKED) return NSN_EINVAL;
+    if (scores && !a->scores) return NSN_EINVAL;
+    if (!scores && (!side_ok(a->k, a->bits) || a->k.tail_dtype != a->v.tail_dtype)) return NSN_EINVAL;
+    if (!side_ok(a->v, a->bits)) return NSN_EINVAL;
+    if (a->out_dtype != NSN_DTYPE_BF16 && a->out_dtype != NSN_DTYPE_F16 && a->out_dtype != NSN_DTYPE_F32) return NSN_EINVAL;
+    if (a->batch > 65535 || a->heads_kv > 65535) return NSN_EINVAL;
+
+    AttnParams p{};
+    p.q = a->q;
+    p.heads_q = a->heads_q;
+    p.heads_kv = a->heads_kv;
+    p.group = static_cast<int>(G);
+    p.scale = a->scale;
+    p.seq_len = a->seq_len;
+    p.split_tokens = a->split_tokens;
+    p.n_splits = a->n_splits;
+    p.k = to_side(a->k);
+    p.v = to_side(a->v);
+    p.scores = a->scores;
+    p.scores_cap = a->scores_cap;
+    p.partials = a->partials;
+    p.status = a->status;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(a->n_splits), static_cast<unsigned>(a->heads_kv),
+                    static_cast<unsigned>(a->batch));
+    int rc;
+    if (a->kernel != NSN_ATTN_REFERENCE) return NSN_EINVAL;
+    if (a->bits == 3) rc = dispatch_q<3>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
+    else if (a->bits == 4) rc = dispatch_q<4>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
+    else rc = dispatch_q<5>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
+    if (rc != NSN_OK) return rc;
+    const dim3 mgrid(static_cast<unsigned>(a->batch * a->heads_q));
+    if (a->out_dtype == NSN_DTYPE_BF16)
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
+    else if (a->out_dtype == NSN_DTYPE_F16)
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
+    else
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
+    return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,369 @@
+"""Decode-attention readout over packed K/V: the reference's L3 call surface.
+
+Mirrors (paths relative to the reference root):
+  * VF01 fused / bridge routes: ``restore_v``, ``launch``, ``pipeline``
+    (experiments/ac08/source/loop_kv_vf01_kernel.py:117-158);
+  * AF01 attention with materialised V or given scores: ``af_launch``
+    (experiments/ac08/source/loop_kv_af01_kernel.py:100-111);
+  * the grouped input checks ``structural`` / ``finite``
+    (experiments/ac08/source/loop_kv_vf01_checks.py:5-63,
+    loop_kv_qk01_kernel.py:66-78, loop_kv_rf01_kernel.py:49-58);
+  * the GQA route (experiments/nb06/source/loop_kv_nb06_kernel.py:142-191):
+    ``launch`` serves any Hq = G*Hkv -- query head h reads kv head h // G.
+The reference requires batch 1; ``decode_attention`` is the batched, ragged
+form the benchmark configurations need (one call for B sequences).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _dev, _lib, codec
+from .errors import IntegrityError, NumericalFailure, require
+
+SCALE = 0.08838834764831845   # 1/sqrt(128), loop_kv_vf01_kernel.py:90
+BLOCK, DIM = 64, 128
+PART_STRIDE = 132
+LAST_STAGE = "idle"
+
+KERNELS = {"reference": _lib.ATTN_REFERENCE, "fast": _lib.ATTN_FAST}
+
+
+@dataclass
+class PackedKV:
+    """One side (K or V) of a batched packed cache.
+
+    codes  u8  [B, Hkv, cap, 64*128*bits/8]     norm f16 [B, Hkv, cap, 64(,1)]
+    min    f16 [B, Hkv, cap, (1,)128]           scale f16 [B, Hkv, cap, (1,)128]
+    blocks i32 [B]  packed blocks of each sequence (tokens 0 .. 64*blocks-1)
+    tail   f16/bf16 [B, Hkv, tail_cap, 128]  tokens 64*blocks[b] .. seq_len[b]-1
+    """
+    codes: Optional[torch.Tensor]
+    norm: Optional[torch.Tensor]
+    min: Optional[torch.Tensor]
+    scale: Optional[torch.Tensor]
+    blocks: Optional[torch.Tensor]
+    tail: Optional[torch.Tensor]
+    bits: int = 3
+
+    @property
+    def heads(self):
+        return (self.codes if self.codes is not None else self.tail).shape[1]
+
+    def side(self):
+        s = _lib.KVSide()
+        if self.codes is not None:
+            s.codes = self.codes.data_ptr()
+            s.norms = self.norm.data_ptr()
+            s.mins = self.min.data_ptr()
+            s.scales = self.scale.data_ptr()
+            s.blocks = self.blocks.data_ptr()
+            s.block_cap = self.codes.shape[2]
+        if self.tail is not None:
+            s.tail = self.tail.data_ptr()
+            s.tail_dtype = _dev.dtype_code(self.tail.dtype)
+            s.tail_cap = self.tail.shape[2]
+        else:
+            s.tail_dtype = _lib.DTYPE_F16
+        return s
+
+    def validate(self, batch, heads):
+        if self.codes is not None:
+            nbytes = BLOCK * DIM * self.bits // 8
+            require(self.codes.dtype == torch.uint8 and self.codes.is_contiguous() and self.codes.ndim == 4
+                    and tuple(self.codes.shape[:2]) == (batch, heads) and self.codes.shape[3] == nbytes,
+                    "Packed codes layout")
+            cap = self.codes.shape[2]
+            for t, last in ((self.norm, BLOCK), (self.min, DIM), (self.scale, DIM)):
+                require(t.dtype == torch.float16 and t.is_contiguous() and t.numel() == batch * heads * cap * last,
+                        "Packed metadata layout")
+            require(self.blocks is not None and self.blocks.dtype == torch.int32 and self.blocks.numel() == batch,
+                    "Packed block counts")
+        if self.tail is not None:
+            require(self.tail.dtype in (torch.float16, torch.bfloat16) and self.tail.is_contiguous()
+                    and self.tail.ndim == 4 and tuple(self.tail.shape[:2]) == (batch, heads)
+                    and self.tail.shape[3] == DIM, "Tail shape/type")
+
+
+def default_split(batch, heads_kv, max_len, target_units=1024, min_split=256):
+    """Split the context so that batch*heads_kv*splits covers the 256 CUs several times."""
+    want = max(1, math.ceil(target_units / max(1, batch * heads_kv)))
+    split = max(min_split, math.ceil(max_len / want / BLOCK) * BLOCK)
+    split = min(split, math.ceil(max_len / BLOCK) * BLOCK)
+    return max(BLOCK, split), max(1, math.ceil(max_len / max(BLOCK, split)))
+
+
+def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
+                     kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
+                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None):
+    """Batched single-query decode attention.
+
+    q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
+    ctx [B,Hq,128] fp32).  ``scores`` [B, Hq, cap] fp32 replaces K (the AF01
+    FULL=False readout).  ``check`` syncs and raises NumericalFailure on any
+    nonfinite intermediate/output.
+    """
+    _dev.require_gpu(q, seq_len)
+    require(q.ndim == 3 and q.shape[2] == DIM and q.is_contiguous(), "Query shape/type")
+    B, Hq = q.shape[:2]
+    Hkv = v.heads
+    require(Hq % Hkv == 0 and Hq // Hkv <= 16, "GQA group")
+    require(seq_len.dtype == torch.int32 and seq_len.numel() == B and seq_len.is_cuda, "Sequence lengths")
+    v.validate(B, Hkv)
+    if scores is None:
+        require(k is not None, "K cache required")
+        k.validate(B, Hkv)
+        require(k.bits == v.bits, "K/V bit widths differ")
+        if k.tail is not None and v.tail is not None:
+            require(k.tail.dtype == v.tail.dtype, "K/V tail dtypes differ")
+    else:
+        require(scores.dtype == torch.float32 and scores.is_contiguous() and scores.ndim == 3
+                and tuple(scores.shape[:2]) == (B, Hq), "Score shape/type")
+    if max_seq_len is None or check:
+        _validate_lengths(seq_len, k if scores is None else None, v, scores, max_seq_len)
+    if max_seq_len is None:
+        max_seq_len = int(seq_len.max().item())
+    if split_tokens is None:
+        split_tokens, n_splits = default_split(B, Hkv, max_seq_len)
+    else:
+        n_splits = max(1, math.ceil(max_seq_len / split_tokens))
+    if kv_round_dtype is None:
+        tdt = v.tail.dtype if v.tail is not None else torch.bfloat16
+        kv_round_dtype = tdt
+    dev = q.device
+    need = B * Hq * n_splits * PART_STRIDE
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty((B, Hq, DIM), dtype=out_dtype, device=dev)
+    if ctx is None:
+        ctx = torch.empty((B, Hq, DIM), dtype=torch.float32, device=dev)
+    st = status if status is not None else _dev.new_status(dev)
+    a = _lib.AttnArgs()
+    a.q = q.data_ptr()
+    a.q_dtype = _dev.dtype_code(q.dtype)
+    a.batch, a.heads_q, a.heads_kv = B, Hq, Hkv
+    a.scale = scale
+    a.seq_len = seq_len.data_ptr()
+    a.max_seq_len = max_seq_len
+    a.bits = v.bits
+    a.k_mode = _lib.KV_SCORES if scores is not None else _lib.KV_PACKED
+    if scores is None:
+        a.k = k.side()
+    else:
+        a.scores = scores.data_ptr()
+        a.scores_cap = scores.shape[2]
+    a.v = v.side()
+    a.kernel = KERNELS[kernel]
+    a.kv_round_dtype = _dev.dtype_code(kv_round_dtype)
+    a.split_tokens = split_tokens
+    a.n_splits = n_splits
+    a.partials = workspace.data_ptr()
+    a.ctx = ctx.data_ptr()
+    a.out = out.data_ptr()
+    a.out_dtype = _dev.dtype_code(out_dtype)
+    a.status = st.data_ptr()
+    rc = _lib.lib().nsn_decode_attention(a, _dev.stream())
+    _lib.check(rc, "nsn_decode_attention")
+    if check and status is None:
+        s = _dev.read_status(st)
+        if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):
+            raise NumericalFailure("Nonfinite fused attention intermediate/output")
+    return out, ctx
+
+
+def _validate_lengths(seq_len, k, v, scores, max_seq_len):
+    """Host check (one device->host copy) that every token the kernels will
+    touch lies inside the caller's buffers: 0 < seq_len[b] <= max_seq_len,
+    blocks[b] <= block capacity, 0 <= seq_len[b] - 64*blocks[b] <= tail capacity,
+    seq_len[b] <= score capacity."""
+    L = seq_len.cpu().numpy().astype(np.int64)
+    require(np.all(L > 0), "Empty sequence")
+    if max_seq_len is not None:
+        require(np.all(L <= max_seq_len), "Sequence longer than max_seq_len")
+    for side in (k, v):
+        if side is None:
+            continue
+        nb = side.blocks.cpu().numpy().astype(np.int64) if side.codes is not None else np.zeros_like(L)
+        cap = side.codes.shape[2] if side.codes is not None else 0
+        tcap = side.tail.shape[2] if side.tail is not None else 0
+        require(np.all(nb >= 0) and np.all(nb <= cap), "Packed block count exceeds capacity")
+        rest = L - BLOCK * nb
+        require(np.all(rest >= 0) and np.all(rest <= tcap), "Tail exceeds capacity / packed past length")
+    if scores is not None:
+        require(np.all(L <= scores.shape[2]), "Score length")
+
+
+# --------------------------------------------------- reference (b == 1) surface
+
+def _group_side(g, tail, bits=None):
+    """Reference group dict (+ tail [1,H,L,128]) -> PackedKV for batch 1."""
+    dev = tail.device
+    if g is None:
+        return PackedKV(None, None, None, None, None, tail.contiguous(), bits or 3)
+    codes = g["codes"]
+    n = codes.shape[2]
+    b = (codes.shape[3] * 8) // (BLOCK * DIM)
+    return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2],
+                    torch.full((1,), n, dtype=torch.int32, device=dev), tail.contiguous(), b)
+
+
+def _length(g, tail):
+    return (0 if g is None else g["codes"].shape[2] * BLOCK) + tail.shape[2]
+
+
+def _shape_check(g, h):
+    codes = g["codes"]
+    require(codes.ndim == 4 and codes.dtype == torch.uint8 and codes.is_contiguous()
+            and codes.shape[-1] in (3072, 4096, 5120), "RF01 packed layout")
+    b, gh, n, _ = codes.shape
+    require(b > 0 and gh > 0 and n > 0, "RF01 nonempty shape")
+    shapes = [(b, gh, n, 64, 1), (b, gh, n, 1, 128), (b, gh, n, 1, 128)]
+    require(len(g["metas"]) == 3 and all(tuple(a.shape) == sh and a.dtype == torch.float16 and a.is_contiguous()
+                                         and a.device == codes.device for a, sh in zip(g["metas"], shapes)),
+            "RF01 metadata layout")
+    require(b == 1 and gh == h, "Packed head/device mismatch")
+    return n
+
+
+def _qshape(g, tail, q):
+    require(tail.ndim == 4 and tail.shape[0] == 1 and tail.shape[-1] == 128
+            and tail.dtype in (torch.bfloat16, torch.float16) and tail.is_contiguous(), "Tail shape/type")
+    h = tail.shape[1]
+    require(h > 0 and q.ndim == 4 and q.shape[0] == 1 and q.shape[2:] == (1, 128) and q.shape[1] % h == 0
+            and q.dtype in (torch.bfloat16, torch.float16) and q.is_contiguous(), "Query shape/type")
+    require(q.device == tail.device and tail.is_cuda, "CUDA only; no fallback")
+    compressed = 0 if g is None else _shape_check(g, h) * 64
+    require(tail.shape[-2] + compressed > 0, "Empty sequence")
+    return h, compressed, compressed + tail.shape[-2]
+
+
+def structural(g, kt, q, vg, vt):
+    """Layout contract (loop_kv_vf01_checks.py:5-12): raises IntegrityError."""
+    k = _qshape(g, kt, q)
+    v = _qshape(vg, vt, q)
+    require(k == v, "K/V lengths differ")
+    for group in (g, vg):
+        if group is not None:
+            hd = group.get("headers")
+            b, nh, n, _ = group["codes"].shape
+            require(hd is not None and hd.dtype == torch.uint8 and hd.is_contiguous()
+                    and tuple(hd.shape) == (b, nh, n, 12) and hd.device == q.device, "Header layout")
+    return k[2]
+
+
+def finite(g, kt, q, vg, vt):
+    """One grouped NaN/Inf scan over q, tails and metadata (loop_kv_vf01_checks.py:55-63)."""
+    arrays = [q, kt] + ([] if g is None else list(g["metas"])) + [vt] + ([] if vg is None else list(vg["metas"]))
+    ptrs = (ctypes_array("c_void_p", [a.data_ptr() for a in arrays]))
+    counts = ctypes_array("c_int64", [a.numel() for a in arrays])
+    dts = ctypes_array("c_int", [_dev.dtype_code(a.dtype) for a in arrays])
+    flags = torch.zeros(1, dtype=torch.int32, device=q.device)
+    st = _dev.new_status(q.device)
+    rc = _lib.lib().nsn_finite_scan(len(arrays), ptrs, counts, dts, flags.data_ptr(), st.data_ptr(), _dev.stream())
+    _lib.check(rc, "nsn_finite_scan")
+    if _dev.read_status(st):
+        raise NumericalFailure("VF01 nonfinite raw input")
+
+
+def ctypes_array(kind, values):
+    import ctypes
+    t = getattr(ctypes, kind) * len(values)
+    return t(*values)
+
+
+def restore_v(g, tail):
+    """Bridge: write the full reconstructed V [1,H,T,128] to HBM (loop_kv_vf01_kernel.py:120-126)."""
+    h = tail.shape[1]
+    if g is None:
+        return tail.contiguous().clone()
+    codes = g["codes"]
+    b, gh, n, nbytes = codes.shape
+    bits = nbytes * 8 // (BLOCK * DIM)
+    out = codec.restore(codes.reshape(b * gh, n, nbytes), g["metas"], bits, tail.dtype, tail=tail.reshape(h, -1, DIM))
+    return out.reshape(1, h, -1, DIM)
+
+
+def launch(g, kt, q, vg, vt, trace=False, kernel="reference"):
+    """Fused packed-K/V readout (loop_kv_vf01_kernel.py:128-139; GQA: loop_kv_nb06_kernel.py:142-154).
+
+    Returns (out [1,1,Hq,128] bf16, context [1,Hq,1,128] fp32, score, v): score
+    and v are only produced with ``trace`` (computed from the exactly restored
+    K/V; the fused kernel itself keeps neither).
+    """
+    Hq = q.shape[1]
+    T = _length(g, kt)
+    ks, vs = _group_side(g, kt), _group_side(vg, vt)
+    seq = torch.full((1,), T, dtype=torch.int32, device=q.device)
+    out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
+                                kv_round_dtype=kt.dtype)
+    score = vtr = None
+    if trace:
+        kk = restore_v(g, kt).float()
+        vtr = restore_v(vg, vt)
+        G = Hq // kt.shape[1]
+        score = (torch.einsum("hd,htd->ht", q.reshape(Hq, DIM).float(), kk[0].repeat_interleave(G, 0)) * SCALE)[None]
+    return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM), score, vtr
+
+
+def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
+    """AF01 attention (loop_kv_af01_kernel.py:100-111).
+
+    full=True: K from the packed group + tail, V given dense [1,H,T,128];
+    full=False: softmax readout of the given fp32 scores [1,Hq,T] over V.
+    Returns (out [1,1,Hq,128], context [1,Hq,1,128]).
+    """
+    Hq = q.shape[1]
+    T = v.shape[2]
+    vs = PackedKV(None, None, None, None, None, v.contiguous(), 3)
+    seq = torch.full((1,), T, dtype=torch.int32, device=v.device)
+    if full:
+        out, ctx = decode_attention(q.reshape(1, Hq, DIM), _group_side(g, tail), vs, seq, max_seq_len=T,
+                                    kernel=kernel, kv_round_dtype=v.dtype)
+    else:
+        require(score is not None and tuple(score.shape) == (1, Hq, T), "Score shape/type")
+        out, ctx = decode_attention(q.reshape(1, Hq, DIM), None, vs, seq, max_seq_len=T, scores=score.contiguous(),
+                                    kernel=kernel, kv_round_dtype=v.dtype)
+    return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM)
+
+
+def pipeline(arm, data, trace=False):
+    """Checked route selection (loop_kv_vf01_kernel.py:141-158, loop_kv_nb06_kernel.py:175-191).
+
+    Arms: 'V_FUSED' / 'GQA_FUSED' (fused), 'TILE_MATERIALIZE' (bridge: V
+    restored to HBM then attention), 'RF01_MATERIALIZE' (V from restore_group
+    + cat).  Stages recorded in LAST_STAGE as the reference does.
+    """
+    global LAST_STAGE
+    g, kt, q, vg, vt = data
+    LAST_STAGE = "structural"
+    structural(g, kt, q, vg, vt)
+    LAST_STAGE = "input_finite"
+    finite(g, kt, q, vg, vt)
+    if arm in ("V_FUSED", "GQA_FUSED"):
+        LAST_STAGE = "attention"
+        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace)
+    elif arm in ("TILE_MATERIALIZE", "RF01_MATERIALIZE"):
+        LAST_STAGE = "restore"
+        if arm == "TILE_MATERIALIZE":
+            v = restore_v(vg, vt)
+        else:
+            v = vt if vg is None else torch.cat((codec.restore_group(vg, vt.dtype), vt), dim=-2)
+        require(v.dtype == vt.dtype and v.is_contiguous() and tuple(v.shape) == (1, vt.shape[1], _length(vg, vt), 128),
+                "V shape/type")
+        if not bool(torch.isfinite(v).all()):
+            raise NumericalFailure("Nonfinite V")
+        LAST_STAGE = "attention"
+        out, ctx = af_launch(g, kt, q, v, full=True)
+        score = None
+    else:
+        raise IntegrityError("Unknown VF01 arm")
+    LAST_STAGE = "output"
+    if not bool(torch.isfinite(out).all()):
+        raise NumericalFailure("Nonfinite VF01 output")
+    LAST_STAGE = "returned"
+    return (out, ctx, score, v) if trace else out

@@ -65,7 +65,7 @@ def heavy_tailed_blocks():
 # ---------------------------------------------------------------- VF01 fixtures
 
 def _bf16_bits(a):
-    a = np.asarray(a, dtype=np.float32)
+    a = np.ascontiguousarray(a, dtype=np.float32)
     u = a.view(np.uint32).astype(np.uint64)
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
@@ -85,7 +85,7 @@ def query_bits(kind, h, index=0):
         a = np.zeros(shape, np.float32)
     else:
         raise ValueError(kind)
-    return _bf16_bits(a)
+    return np.ascontiguousarray(_bf16_bits(a))
 
 
 def pack3_bits(codes):

@@ -1,0 +1,225 @@
+"""GPU parity of the decode readout through the C-ABI.
+
+Expected values come from the oracle: K/V restored by the C restatement of
+nsn_decode, rounded to the attention dtype, then float64 softmax attention.
+Tolerance (north star): |ctx - ref| <= 2e-3 + 1e-2 * |ref| elementwise.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nsn_amd import cache, codec, kernels
+from nsn_amd.errors import NumericalFailure
+from oracle import oracle as O
+from tests.golden import inputs as gi
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def within(got, ref, atol=ATOL, rtol=RTOL):
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    ok = np.all(err <= atol + rtol * np.abs(ref))
+    return ok, float(err.max())
+
+
+def oracle_restore(x16, length, bits, round_dtype):
+    """Oracle view of one sequence: x16 [H, T, 128] fp16 -> fp32 [H, length, 128]
+    as the kernel sees it (packed prefix restored + rounded, tail as stored)."""
+    H = x16.shape[0]
+    C = (length // 64) * 64
+    parts = []
+    if C:
+        blocks = x16[:, :C].astype(np.float32).reshape(H, C // 64, 64, 128)
+        q, n, m, s, err = O.nsn_encode(blocks, bits)
+        assert err == 0
+        y = O.nsn_decode_f32(q, n, m, s).reshape(H, C, 128)
+        bitsr = O.cast_bits(y, round_dtype)
+        parts.append(O.from_bf16_bits(bitsr) if round_dtype == "bfloat16" else O.from_f16_bits(bitsr))
+    if length > C:
+        parts.append(x16[:, C:length].astype(np.float32))
+    return np.concatenate(parts, axis=1)
+
+
+def make_case(seed, B, Hq, Hkv, lengths, bits=3, gen="kv"):
+    rng = np.random.default_rng(seed)
+    T = max(lengths)
+    if gen == "kv":
+        from nsn_amd import synthetic
+        k = synthetic.kv_tokens(rng, (B, Hkv), T)
+        v = synthetic.kv_tokens(rng, (B, Hkv), T)
+    else:
+        from nsn_amd import synthetic
+        k = synthetic.heavy_tailed_tokens(rng, (B, Hkv), T)
+        v = synthetic.heavy_tailed_tokens(rng, (B, Hkv), T)
+    q = rng.standard_normal((B, Hq, 128)).astype(np.float32)
+    qb = torch.from_numpy(q).to(torch.bfloat16)
+    kk, seq = cache.pack_sequences(torch.from_numpy(k).to(DEV), lengths, bits=bits)
+    vv, _ = cache.pack_sequences(torch.from_numpy(v).to(DEV), lengths, bits=bits)
+    return k, v, qb, kk, vv, seq
+
+
+def oracle_ctx(k, v, qb, lengths, bits, round_dtype="float16"):
+    B, Hq = qb.shape[:2]
+    out = np.zeros((B, Hq, 128))
+    q = qb.float().numpy()
+    for b, L in enumerate(lengths):
+        kr = oracle_restore(k[b], L, bits, round_dtype)
+        vr = oracle_restore(v[b], L, bits, round_dtype)
+        c, _ = O.decode_attention64(q[b:b + 1], kr[None], vr[None])
+        out[b] = c[0]
+    return out
+
+
+@pytest.mark.parametrize("kernel", ["reference"])
+@pytest.mark.parametrize("B,Hq,Hkv,lengths", [
+    (1, 4, 4, [200]),              # MHA, 3 blocks + 8 tail
+    (2, 8, 2, [1000, 333]),        # GQA 4:1, ragged
+    (3, 6, 1, [64, 65, 17]),       # GQA 6:1, exact block / block+1 / tail only
+])
+def test_decode_vs_oracle(kernel, B, Hq, Hkv, lengths):
+    k, v, qb, kk, vv, seq = make_case(1, B, Hq, Hkv, lengths)
+    out, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel=kernel, kv_round_dtype=torch.float16)
+    ref = oracle_ctx(k, v, qb, lengths, 3)
+    ok, err = within(ctx.cpu().numpy(), ref)
+    assert ok, err
+    # the bf16 output is the RNE cast of the fp32 context
+    assert torch.equal(out.cpu(), ctx.cpu().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("kernel", ["reference"])
+def test_5bit_decode_vs_oracle(kernel):
+    lengths = [640, 200]
+    k, v, qb, kk, vv, seq = make_case(3, 2, 8, 2, lengths, bits=5, gen="heavy")
+    _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel=kernel, kv_round_dtype=torch.float16)
+    ok, err = within(ctx.cpu().numpy(), oracle_ctx(k, v, qb, lengths, 5))
+    assert ok, err
+
+
+def test_split_invariance():
+    lengths = [1500, 900]
+    k, v, qb, kk, vv, seq = make_case(5, 2, 8, 2, lengths)
+    outs = []
+    for split in (64, 256, 1536):
+        _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, split_tokens=split, kv_round_dtype=torch.float16)
+        outs.append(ctx.cpu().numpy())
+    for o in outs[1:]:
+        assert np.allclose(o, outs[0], atol=1e-5, rtol=1e-5)
+
+
+def test_gqa_equals_repeated_mha():
+    """Invariant: q-head h of a GQA call equals an MHA call on kv-head h // G."""
+    lengths = [300]
+    k, v, qb, kk, vv, seq = make_case(9, 1, 8, 2, lengths)
+    _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kv_round_dtype=torch.float16)
+    krep = np.repeat(k, 4, axis=1)
+    vrep = np.repeat(v, 4, axis=1)
+    km, _ = cache.pack_sequences(torch.from_numpy(krep).to(DEV), lengths)
+    vm, _ = cache.pack_sequences(torch.from_numpy(vrep).to(DEV), lengths)
+    _, ctx_m = kernels.decode_attention(qb.to(DEV), km, vm, seq, kv_round_dtype=torch.float16)
+    assert torch.equal(ctx.cpu(), ctx_m.cpu())
+
+
+def _fixture_data(f):
+    a = gi.vf01_fixture(f["compressed"], f["length"], f["pattern"])
+    bf = lambda x: torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV)
+    g = vg = None
+    if f["compressed"]:
+        g = {"codes": torch.from_numpy(a["k_codes"]).to(DEV), "headers": torch.from_numpy(a["k_headers"]).to(DEV),
+             "metas": tuple(torch.from_numpy(a[f"k_meta{i}"]).to(DEV) for i in range(3))}
+        vg = {"codes": torch.from_numpy(a["v_codes"]).to(DEV), "headers": torch.from_numpy(a["v_headers"]).to(DEV),
+              "metas": tuple(torch.from_numpy(a[f"v_meta{i}"]).to(DEV) for i in range(3))}
+    return a, (g, bf(a["k_tail"]), bf(a["q"]), vg, bf(a["v_tail"]))
+
+
+def _fixture_oracle(a, f):
+    """fp64 attention over the oracle-restored (bf16-rounded) K/V of a VF01 fixture."""
+    c, T = f["compressed"], f["length"]
+    out = []
+    for side in ("k", "v"):
+        tail = O.from_bf16_bits(a[side + "_tail"])[0]
+        if c:
+            n = c // 64
+            q = O.unpack_codes(a[side + "_codes"].reshape(-1), 2 * c * 128, 3).reshape(2, n, 64, 128)
+            n16 = a[side + "_meta0"].view(np.uint16).reshape(2, n, 64, 1)
+            m16 = a[side + "_meta1"].view(np.uint16).reshape(2, n, 1, 128)
+            s16 = a[side + "_meta2"].view(np.uint16).reshape(2, n, 1, 128)
+            y = O.from_bf16_bits(O.nsn_decode(q, n16, m16, s16, "bfloat16")).reshape(2, c, 128)
+            tail = np.concatenate([y, tail], axis=1)
+        out.append(tail)
+    q = O.from_bf16_bits(a["q"]).reshape(1, 2, 128)
+    ctx, _ = O.decode_attention64(q, out[0][None], out[1][None])
+    return ctx[0]
+
+
+def test_vf01_normal_fixtures_fused_equals_bridge_and_oracle():
+    """The reference's 16 normal fixtures (loop_kv_vf01_contract.py:81-96): the fused
+    and bridge routes must be bitwise equal (AC/verify_loop_kv_vf01.py:41-50) and
+    match the fp64 oracle."""
+    import json
+    from pathlib import Path
+    rec = json.loads((Path(__file__).parent / "golden" / "vf01_input_hashes.json").read_text())
+    for f in rec["fixtures"]:
+        a, data = _fixture_data(f)
+        out_f, ctx_f, _, v_f = kernels.pipeline("V_FUSED", data, trace=True)
+        out_b, ctx_b, _, v_b = kernels.pipeline("TILE_MATERIALIZE", data, trace=True)
+        out_r = kernels.pipeline("RF01_MATERIALIZE", data)
+        assert torch.equal(out_f.view(torch.int16), out_b.view(torch.int16)), f["id"]
+        assert torch.equal(ctx_f.view(torch.int32), ctx_b.view(torch.int32)), f["id"]
+        assert torch.equal(out_f.view(torch.int16), out_r.view(torch.int16)), f["id"]
+        assert torch.equal(v_f.view(torch.int16), v_b.view(torch.int16)), f["id"]
+        ref = _fixture_oracle(a, f)
+        ok, err = within(ctx_f.cpu().numpy().reshape(2, 128), ref, atol=1e-5, rtol=1e-5)
+        assert ok, (f["id"], err)
+
+
+def test_score_input_readout_config1():
+    """C1: B=1, 32q/8kv, 64 packed blocks + 37-token fp16 tail; logits N(0,1)*4."""
+    rng = np.random.default_rng(1)
+    from nsn_amd import synthetic
+    T = 4096 + 37
+    v = synthetic.kv_tokens(rng, (1, 8), T)
+    scores = (rng.standard_normal((1, 32, T)) * 4).astype(np.float32)
+    vv, seq = cache.pack_sequences(torch.from_numpy(v).to(DEV), [T])
+    qdummy = torch.zeros(1, 32, 128, dtype=torch.bfloat16, device=DEV)
+    _, ctx = kernels.decode_attention(qdummy, None, vv, seq, scores=torch.from_numpy(scores).to(DEV),
+                                      kv_round_dtype=torch.float16)
+    vr = oracle_restore(v[0], T, 3, "float16")
+    ref = O.readout64(scores, vr[None], groups=4)
+    ok, err = within(ctx.cpu().numpy(), ref)
+    assert ok, err
+    # bridge: V restored to HBM, then the same readout -> bitwise equal
+    vfull = codec.restore(vv.codes[0], (vv.norm[0], vv.min[0], vv.scale[0]), 3, torch.float16,
+                          tail=vv.tail[0, :, :37])
+    vd = kernels.PackedKV(None, None, None, None, None, vfull[None].contiguous(), 3)
+    _, ctx_b = kernels.decode_attention(qdummy, None, vd, seq, scores=torch.from_numpy(scores).to(DEV),
+                                        kv_round_dtype=torch.float16)
+    assert torch.equal(ctx.cpu(), ctx_b.cpu())
+
+
+def test_negative_fixtures_rejected_at_reference_stage():
+    """NaN/Inf inputs stop at 'input_finite'; overflowing scores at 'attention'
+    (loop_kv_vf01_contract.py:98-120)."""
+    f = {"compressed": 64, "length": 65, "pattern": "mixed_codes"}
+    a, (g, kt, q, vg, vt) = _fixture_data(f)
+    q2 = q.clone()
+    q2.view(-1)[0] = float("nan")
+    with pytest.raises(NumericalFailure):
+        kernels.pipeline("V_FUSED", (g, kt, q2, vg, vt))
+    assert kernels.LAST_STAGE == "input_finite"
+    vg2 = dict(vg)
+    m = vg["metas"][0].clone()
+    m.view(-1)[-1] = float("inf")
+    vg2["metas"] = (m, vg["metas"][1], vg["metas"][2])
+    with pytest.raises(NumericalFailure):
+        kernels.pipeline("V_FUSED", (g, kt, q, vg2, vt))
+    assert kernels.LAST_STAGE == "input_finite"
+    # score overflow: q = K tail = 2**120 (tail only, T=17)
+    big = torch.full((1, 2, 1, 128), 2.0 ** 120, dtype=torch.bfloat16, device=DEV)
+    tail = torch.full((1, 2, 17, 128), 2.0 ** 120, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NumericalFailure):
+        kernels.pipeline("V_FUSED", (None, tail, big, None, tail.clone()))
+    assert kernels.LAST_STAGE == "attention"

@@ -1,0 +1,120 @@
+"""CPU-side tests: the C-ABI library loads and exports what include/nsn_hip.h
+declares, host-side contracts (structural checks, byte accounting, split
+heuristics), and that the product path neither imports the oracle nor falls
+back to the CPU."""
+import ast
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nsn_amd import _lib, kernels, primitives
+from nsn_amd.errors import IntegrityError
+from tests.golden import inputs as gi
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_functions():
+    text = (ROOT / "include" / "nsn_hip.h").read_text()
+    return set(re.findall(r"^\s*(?:const char \*|int64_t |int )\s*(nsn_\w+)\s*\(", text, re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    declared = header_functions()
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    lib = _lib.lib()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.nsn_version().startswith(b"nsn_hip")
+
+
+def test_library_rejects_bad_arguments_without_gpu_work():
+    lib = _lib.lib()
+    # invalid bits / dtype / null pointers are rejected on the host before any launch
+    assert lib.nsn_pack_codes(None, 10, 7, None, None, None) == _lib.NSN_EINVAL
+    assert lib.nsn_unpack_codes(None, 10, 2, None, None) == _lib.NSN_EINVAL
+    assert lib.nsn_encode_blocks(None, 9, 1, 1, 0, 0, 3, 0, 1, None, None, None, None, None, 1, 0, 0,
+                                 None, None, None) == _lib.NSN_EINVAL
+    assert lib.nsn_decode_attention(None, None) == _lib.NSN_EINVAL
+    a = _lib.AttnArgs()
+    a.batch, a.heads_q, a.heads_kv, a.bits = 1, 6, 4, 3          # 6 % 4 != 0
+    assert lib.nsn_decode_attention(a, None) == _lib.NSN_EINVAL
+    assert lib.nsn_attention_workspace_floats(16, 32, 8) == 16 * 32 * 8 * 132
+    # zero-size work is a no-op
+    assert lib.nsn_pack_codes(None, 0, 3, None, None, None) == _lib.NSN_OK
+
+
+def test_planned_bytes_matches_reference_accounting():
+    # loop_kv_pilot.py:407 and the paper's 3,724 B block (3072 + 640 + 12)
+    assert primitives.planned_bytes((1, 1, 64, 128), 64, 4) == {"codes": 4096, "metadata": 640, "native": 0, "block_headers": 12}
+    p = primitives.planned_bytes((1, 1, 64, 128), 64, 3)
+    assert p["codes"] + p["metadata"] + p["block_headers"] == 3724
+    with pytest.raises(IntegrityError):
+        primitives.planned_bytes((1, 1, 64, 128), 65, 3)
+
+
+def test_default_split_covers_context():
+    for B, H, L in [(16, 8, 32768), (1, 8, 4133), (64, 4, 8192), (1, 1, 17)]:
+        split, n = kernels.default_split(B, H, L)
+        assert split % 64 == 0 and split * n >= L and split * (n - 1) < L
+
+
+def _cpu_fixture(kind):
+    """The reference's negative fixtures that fail structural checks (loop_kv_vf01_contract.py:98-120)."""
+    a = gi.vf01_fixture(64, 65, "mixed_codes")
+    t = lambda x, dt=torch.bfloat16: torch.from_numpy(x.view(np.int16)).view(dt) if x.dtype == np.uint16 else torch.from_numpy(x)
+    q = t(a["q"])
+    kt, vt = t(a["k_tail"]), t(a["v_tail"])
+    g = {"codes": torch.from_numpy(a["k_codes"]), "metas": tuple(torch.from_numpy(a[f"k_meta{i}"]) for i in range(3)),
+         "headers": torch.from_numpy(a["k_headers"])}
+    vg = {"codes": torch.from_numpy(a["v_codes"]), "metas": tuple(torch.from_numpy(a[f"v_meta{i}"]) for i in range(3)),
+          "headers": torch.from_numpy(a["v_headers"])}
+    if kind == "q_shape":
+        q = q[..., :127].contiguous()
+    elif kind == "q_dtype":
+        q = q.float()
+    elif kind == "v_codes_short":
+        vg["codes"] = vg["codes"][..., :-1].contiguous()
+    elif kind == "v_meta_shape":
+        vg["metas"] = (vg["metas"][0], vg["metas"][1][..., :127].contiguous(), vg["metas"][2])
+    elif kind == "kv_length_mismatch":
+        vt = torch.cat([vt, vt], 2)
+    elif kind == "v_tail_noncontiguous":
+        vt = vt.transpose(-1, -2).contiguous().transpose(-1, -2)
+    elif kind == "k_codes_dtype":
+        g["codes"] = g["codes"].to(torch.int16)
+    elif kind == "empty_sequence":
+        g = vg = None
+        kt, vt = kt[:, :, :0], vt[:, :, :0]
+    elif kind == "cpu_tensors":
+        pass
+    return g, kt, q, vg, vt
+
+
+@pytest.mark.parametrize("kind", ["q_shape", "q_dtype", "v_codes_short", "v_meta_shape", "kv_length_mismatch",
+                                  "v_tail_noncontiguous", "k_codes_dtype", "empty_sequence", "cpu_tensors"])
+def test_structural_rejections(kind):
+    data = _cpu_fixture(kind)
+    with pytest.raises(IntegrityError):
+        kernels.structural(*data)
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 64, 128)
+    with pytest.raises(IntegrityError):
+        primitives.nsn_encode(x, 3)
+    with pytest.raises(IntegrityError):
+        primitives.pack_codes(torch.zeros(8, dtype=torch.uint8), 3)
+
+
+def test_product_path_never_imports_the_oracle():
+    for path in (ROOT / "nsn_amd").rglob("*.py"):
+        tree = ast.parse(path.read_text())
+        for node in ast.walk(tree):
+            if isinstance(node, ast.Import):
+                assert not any(a.name.startswith("oracle") for a in node.names), path
+            if isinstance(node, ast.ImportFrom):
+                assert not (node.module or "").startswith("oracle"), path
