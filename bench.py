@@ -1,0 +1,270 @@
+"""Benchmark of the NSN packed-KV decode hot path on one MI355X.
+
+Workload ("C2"): batch 16, 32 query / 8 KV heads,
+head_dim 128, bf16 queries N(0,1), ragged context lengths uniform in
+[16384, 32768] (numpy default_rng(2)), K and V from the outlier-token
+generator (lognormal norms, 2% x20), packed as INT3 blocks of 64 tokens plus
+an fp16 tail of < 64 tokens.  Synthetic data generated on the GPU
+(torch.Generator seed 2); inputs are resident in HBM before timing.
+
+A step = one fused decode-attention call for the whole batch (split kernel +
+merge).  Printed: one JSON line (driver contract) with ``value`` = us/step,
+the roofline of the dominant (split) kernel, encode tokens/s, the on-GPU
+bridge and fp16-KV comparators, and the CPU oracle baseline.
+
+    python bench.py [--steps 20] [--warmup 5] [--kernel fast|reference]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+B, HQ, HKV, D = 16, 32, 8, 128
+LMIN, LMAX = 16384, 32768
+METRIC = "fused INT3-KV decode-attn µs/step + HBM GB/s (B=16, ctx 32K); encode tok/s"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--kernel", default="fast", choices=["fast", "reference"])
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--no-baselines", action="store_true", help="skip the bridge / fp16 comparators")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup, stream):
+    """Average ms per call of fn() over `steps` back-to-back calls (HIP events on `stream`)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def algorithmic_bytes(lengths, bits):
+    """Bytes the split kernel must move per step: packed K and V (codes + fp16
+    norm/min/scale = bits*16 + 10 B per token per kv-head), fp16 tails
+    (256 B/token/kv-head) and the bf16 queries.  Headers are not read."""
+    per_tok = bits * 16 + 10
+    kv = 0
+    for L in lengths:
+        C = (L // 64) * 64
+        kv += HKV * 2 * (C * per_tok + (L - C) * 256)
+    q = B * HQ * D * 2
+    return int(kv + q)
+
+
+def cpu_baseline(kk, vv, q, lengths, seconds):
+    """Oracle bridge readout for sequence 0 (restore K and V with the C
+    restatement of nsn_decode, then fp32 softmax(qK^T/sqrt(d))V in numpy), one
+    thread, repeated for about `seconds`; scaled to the whole batch."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import oracle as O
+
+    L0 = int(lengths[0])
+    C0 = (L0 // 64) * 64
+    nb = C0 // 64
+    host = {}
+    for name, side in (("k", kk), ("v", vv)):
+        host[name] = dict(codes=side.codes[0, :, :nb].cpu().numpy(), n=side.norm[0, :, :nb].cpu().numpy().view(np.uint16),
+                          m=side.min[0, :, :nb].cpu().numpy().view(np.uint16), s=side.scale[0, :, :nb].cpu().numpy().view(np.uint16),
+                          tail=side.tail[0, :, : L0 - C0].float().cpu().numpy())
+    qh = q[0].float().cpu().numpy()
+
+    def once():
+        kvr = []
+        for name in ("k", "v"):
+            h = host[name]
+            y = O.restore_blocks_f32(h["codes"], h["n"], h["m"], h["s"], 3)          # [8, nb, 64, 128]
+            y = O.from_f16_bits(O.f16_bits(y)).reshape(HKV, C0, D)
+            kvr.append(np.concatenate([y, h["tail"]], axis=1))
+        k, v = kvr
+        G = HQ // HKV
+        out = np.empty((HQ, D), np.float32)
+        for h in range(HQ):
+            s = (k[h // G] @ qh[h]) * np.float32(1 / math.sqrt(D))
+            p = np.exp(s - s.max())
+            out[h] = (p @ v[h // G]) / p.sum()
+        return out
+
+    with threadpool_limits(limits=1):
+        once()
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            once()
+            n += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = (time.perf_counter() - t0) / n
+    scale = float(sum(lengths)) / L0
+    return dict(value=round(dt * scale * 1e6, 1), unit="µs/step", cores=1, kind="port",
+                sample=f"oracle bridge readout (C nsn_decode restore of K and V + numpy fp32 attention) of "
+                       f"sequence 0 ({L0} tokens, 8 kv / 32 q heads), 1 thread, {n} repeats of "
+                       f"{dt * 1e3:.0f} ms, scaled by total/sample tokens = {scale:.2f}")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
+              "described in DESIGN.md and no figure at several GPUs is produced.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from nsn_amd import _dev, _lib, cache, codec, kernels, synthetic
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    lengths = [int(x) for x in synthetic.ragged_lengths(2, B, LMIN, LMAX)]
+    gen = torch.Generator(device=dev).manual_seed(2)
+    log(f"[bench] generating C2 K/V on the GPU: B={B} Hkv={HKV} Lmax={LMAX} (lengths {min(lengths)}..{max(lengths)})")
+    k = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
+    v = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
+    q = torch.randn((B, HQ, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+    # ---- encode throughput: all 64-token blocks of K (B*Hkv rows x 512 blocks) in one launch
+    nblk = LMAX // 64
+    codes = torch.empty((B * HKV, nblk, 3072), dtype=torch.uint8, device=dev)
+    nrm = torch.empty((B * HKV, nblk, 64), dtype=torch.float16, device=dev)
+    mn = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
+    sc = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
+    st = _dev.new_status(dev)
+    lib = _lib.lib()
+
+    def encode_all():
+        rc = lib.nsn_encode_blocks(k.data_ptr(), _lib.DTYPE_F16, B * HKV, nblk, LMAX * D, 0, 3, _lib.NORM_LANES8, 1,
+                                   codes.data_ptr(), nrm.data_ptr(), mn.data_ptr(), sc.data_ptr(), None, None, nblk, 0, 0,
+                                   None, st.data_ptr(), stream.cuda_stream)
+        assert rc == 0
+    enc_ms = timed(encode_all, 10, 2, stream)
+    enc_tokens = B * HKV * LMAX
+    enc_tok_s = enc_tokens / (enc_ms * 1e-3)
+    enc_gbs = enc_tokens * 314 / (enc_ms * 1e-3) / 1e9
+    log(f"[bench] encode: {enc_ms * 1e3:.1f} us per launch ({enc_tokens} token-heads), {enc_tok_s / 1e9:.2f} G tok/s, "
+        f"{enc_gbs:.0f} GB/s algorithmic (314 B/token)")
+    del codes, nrm, mn, sc
+
+    # ---- packed ragged caches (setup, untimed)
+    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
+    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+    max_len = max(lengths)
+    split, n_splits = kernels.default_split(B, HKV, max_len)
+    ws = torch.empty(B * HQ * n_splits * kernels.PART_STRIDE, dtype=torch.float32, device=dev)
+    out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
+    ctx = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+    status = _dev.new_status(dev)
+    # validated, checked call first (syncs, raises on any error)
+    kernels.decode_attention(q, kk, vv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+                             workspace=ws, out=out, ctx=ctx)
+
+    def step(merge=True):
+        kernels.decode_attention(q, kk, vv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+                                 workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=merge)
+
+    log(f"[bench] decode: kernel={args.kernel} split={split} tokens x {n_splits} splits, "
+        f"{B * HKV * n_splits} work units; warmup {args.warmup}, steps {args.steps}")
+    ms_step = timed(step, args.steps, args.warmup, stream)
+    ms_split = timed(lambda: step(merge=False), args.steps, 2, stream)
+    st_val = _dev.read_status(status)
+    assert st_val == 0, f"status word {st_val:#x}"
+    nbytes = algorithmic_bytes(lengths, 3)
+    achieved = nbytes / (ms_split * 1e-3) / 1e9
+    log(f"[bench] step {ms_step * 1e3:.1f} us, split kernel {ms_split * 1e3:.1f} us, "
+        f"{nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+
+    # parity spot check of this step against the exact-order kernel (untimed)
+    if args.kernel != "reference":
+        # exact-order kernel with fp32 reconstructions (no rounding of K/V): the fp32 reference math
+        _, ref_ctx = kernels.decode_attention(q, kk, vv, seq, max_seq_len=max_len, kernel="reference",
+                                              kv_round_dtype=torch.float32)
+        err = (ctx - ref_ctx).abs()
+        tol = 2e-3 + 1e-2 * ref_ctx.abs()
+        log(f"[bench] parity vs exact-order kernel: max abs {float(err.max()):.2e}, within tol: {bool((err <= tol).all())}")
+
+    result = {
+        "metric": METRIC, "value": round(ms_step * 1e3, 2), "unit": "µs/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (GPU torch.Generator seed 2; lengths numpy rng 2)",
+        "config": {"workload": "C2: fused packed-INT3 K+V decode attention, B=16, 32q/8kv heads, d=128, "
+                               "ragged ctx U[16K,32K], fp16 tail < 64", "batch": B, "heads_q": HQ, "heads_kv": HKV,
+                   "head_dim": D, "ctx_min": LMIN, "ctx_max": LMAX, "bits": 3, "kernel": args.kernel,
+                   "split_tokens": split, "n_splits": n_splits},
+        "hbm_gbs": round(achieved, 1),
+        "encode_tok_s": round(enc_tok_s, 1),
+        "encode_gbs": round(enc_gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
+                     "kernel_us": round(ms_split * 1e3, 2)},
+    }
+
+    if not args.no_baselines:
+        # bridge: V restored to HBM (fp16), then attention reading packed K + dense V
+        vfull = torch.empty((B, HKV, max_len, D), dtype=torch.float16, device=dev)
+
+        cap = vv.codes.shape[2]
+
+        def restore_all():
+            for b in range(B):
+                L = int(lengths[b])
+                nb = L // 64
+                rc = lib.nsn_restore_blocks(
+                    vv.codes[b].data_ptr(), 0, vv.norm[b].data_ptr(), vv.min[b].data_ptr(), vv.scale[b].data_ptr(),
+                    HKV, nb, cap, 3, vfull[b].data_ptr(), _lib.DTYPE_F16, max_len, vv.tail[b].data_ptr(),
+                    _lib.DTYPE_F16, L - nb * 64, vv.tail.shape[2], status.data_ptr(), stream.cuda_stream)
+                assert rc == 0
+        vd = kernels.PackedKV(None, None, None, None, None, None, vfull, 3)
+
+        def bridge():
+            restore_all()
+            kernels.decode_attention(q, kk, vd, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+                                     workspace=ws, out=out, ctx=ctx, status=status, check=False)
+        ms_bridge = timed(bridge, max(3, args.steps // 4), 1, stream)
+        del vfull
+        # fp16-KV decode: the same kernel over dense fp16 K and V
+        kd = kernels.PackedKV(None, None, None, None, None, None, k, 3)
+        vdn = kernels.PackedKV(None, None, None, None, None, None, v, 3)
+
+        def dense():
+            kernels.decode_attention(q, kd, vdn, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+                                     workspace=ws, out=out, ctx=ctx, status=status, check=False)
+        ms_dense = timed(dense, max(3, args.steps // 4), 1, stream)
+        result["comparators"] = {"bridge_us": round(ms_bridge * 1e3, 1), "fp16_kv_us": round(ms_dense * 1e3, 1)}
+        log(f"[bench] bridge {ms_bridge * 1e3:.1f} us/step, fp16-KV {ms_dense * 1e3:.1f} us/step")
+
+    if not args.no_cpu:
+        log(f"[bench] CPU oracle baseline (~{args.cpu_seconds:.0f} s) ...")
+        result["cpu_baseline"] = cpu_baseline(kk, vv, q, lengths, args.cpu_seconds)
+        log(f"[bench] CPU baseline {result['cpu_baseline']['value']:.0f} us/step (scaled)")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -68,6 +68,7 @@ const char *nsn_version(void);
  *   of codes [*, 64*128*bits/8], norms [*, 64], mins/scales [*, 128] (fp16
  *   bits) and headers [*, 12] (nullable); its header token is
  *   header_start_token + 64*i.
+ *   factors (nullable): [*, 64] fp32 decode factors (see nsn_block_factors).
  *   codes_unpacked (nullable): [n_outer*n_blocks, 64, 128] u8 codes.
  *   zero_flat_scale: 1 = nsn_encode (codes forced to 0 where scale == 0),
  *                    0 = nsn_int3_qdq (identical outputs for finite input).
@@ -75,7 +76,7 @@ const char *nsn_version(void);
 int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blocks,
                       int64_t x_outer_stride, int64_t x_token_offset, int bits, int norm_order,
                       int zero_flat_scale, uint8_t *codes, uint16_t *norms, uint16_t *mins,
-                      uint16_t *scales, uint8_t *headers, int64_t out_outer_blocks,
+                      uint16_t *scales, uint8_t *headers, float *factors, int64_t out_outer_blocks,
                       int64_t out_block_offset, int64_t header_start_token,
                       uint8_t *codes_unpacked, int32_t *status, nsn_stream_t stream);
 
@@ -117,6 +118,20 @@ int nsn_restore_blocks(const uint8_t *codes, int codes_are_unpacked, const uint1
                        int tail_dtype, int64_t tail_len, int64_t tail_outer_tokens,
                        int32_t *status, nsn_stream_t stream);
 
+/*
+ * Per-token decode factors f_t = n_t / max(|m + s*q_t|, 1e-12) of packed blocks
+ * (fp16 metadata as fp32; the norm in nsn_decode's order), so that the restored
+ * row is f_t * (m + s*q_t).  A block's factors never change once it is encoded,
+ * so decode attention reads them instead of renormalising every token on every
+ * step.  No counterpart in the reference (it renormalises inside each read,
+ * experiments/ac08/source/loop_kv_vf01_kernel.py:28-34).
+ *   codes/norms/mins/scales: [n_outer, in_outer_blocks, ...] as nsn_restore_blocks;
+ *   factors: [n_outer, in_outer_blocks, 64] fp32.
+ */
+int nsn_block_factors(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins,
+                      const uint16_t *scales, int64_t n_outer, int64_t n_blocks,
+                      int64_t in_outer_blocks, int bits, float *factors, nsn_stream_t stream);
+
 /* K/V sources of the decode attention. */
 enum {
     NSN_KV_PACKED = 0,  /* packed blocks for tokens < 64*blocks[b], then the tail buffer */
@@ -135,6 +150,7 @@ typedef struct {
     const uint16_t *norms;  /* [B, Hkv, block_cap, 64]  fp16 */
     const uint16_t *mins;   /* [B, Hkv, block_cap, 128] fp16 */
     const uint16_t *scales; /* [B, Hkv, block_cap, 128] fp16 */
+    const float *factors;   /* [B, Hkv, block_cap, 64] fp32 decode factors (NSN_ATTN_FAST) */
     const int32_t *blocks;  /* [B] packed blocks per sequence (nullable -> 0) */
     int64_t block_cap;
     const void *tail;       /* [B, Hkv, tail_cap, 128] tail_dtype: tokens 64*blocks[b] .. */
@@ -163,6 +179,7 @@ typedef struct {
     void *out;              /* [B, Hq, 128] out_dtype */
     int out_dtype;
     int32_t *status;
+    int merge;              /* 1: also run the split merge; 0: partials only */
 } nsn_attn_args;
 
 /*
@@ -174,6 +191,15 @@ typedef struct {
  * K/V baseline is the same call with blocks == NULL.
  */
 int nsn_decode_attention(const nsn_attn_args *args, nsn_stream_t stream);
+
+/*
+ * Log-sum-exp merge of the per-split partials written by nsn_decode_attention
+ * (with merge == 0): ctx = sum_s u_s e^(m_s - M) / sum_s z_s e^(m_s - M),
+ * out = RNE cast of ctx.  Replaces the AF01 merge kernel
+ * (experiments/ac08/source/loop_kv_af01_kernel.py:70-82).
+ */
+int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, int n_splits, float *ctx,
+                        void *out, int out_dtype, int32_t *status, nsn_stream_t stream);
 
 /* Workspace floats needed by nsn_decode_attention for the given shape. */
 int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits);

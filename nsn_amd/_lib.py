@@ -34,7 +34,7 @@ I64 = ctypes.c_int64
 
 
 class KVSide(ctypes.Structure):
-    _fields_ = [("codes", P), ("norms", P), ("mins", P), ("scales", P), ("blocks", P),
+    _fields_ = [("codes", P), ("norms", P), ("mins", P), ("scales", P), ("factors", P), ("blocks", P),
                 ("block_cap", I64), ("tail", P), ("tail_dtype", I32), ("tail_cap", I64)]
 
 
@@ -43,17 +43,20 @@ class AttnArgs(ctypes.Structure):
                 ("scale", ctypes.c_float), ("seq_len", P), ("max_seq_len", I32), ("bits", I32),
                 ("k_mode", I32), ("k", KVSide), ("v", KVSide), ("scores", P), ("scores_cap", I64),
                 ("kernel", I32), ("kv_round_dtype", I32), ("split_tokens", I32), ("n_splits", I32),
-                ("partials", P), ("ctx", P), ("out", P), ("out_dtype", I32), ("status", P)]
+                ("partials", P), ("ctx", P), ("out", P), ("out_dtype", I32), ("status", P),
+                ("merge", I32)]
 
 
 # symbol -> (restype, argtypes); must cover every function include/nsn_hip.h declares
 SIGNATURES = {
     "nsn_version": (ctypes.c_char_p, []),
-    "nsn_encode_blocks": (I32, [P, I32, I64, I64, I64, I64, I32, I32, I32, P, P, P, P, P, I64, I64, I64, P, P, P]),
+    "nsn_encode_blocks": (I32, [P, I32, I64, I64, I64, I64, I32, I32, I32, P, P, P, P, P, P, I64, I64, I64, P, P, P]),
+    "nsn_block_factors": (I32, [P, P, P, P, I64, I64, I64, I32, P, P]),
     "nsn_pack_codes": (I32, [P, I64, I32, P, P, P]),
     "nsn_unpack_codes": (I32, [P, I64, I32, P, P]),
     "nsn_restore_blocks": (I32, [P, I32, P, P, P, I64, I64, I64, I32, P, I32, I64, P, I32, I64, I64, P, P]),
     "nsn_decode_attention": (I32, [ctypes.POINTER(AttnArgs), P]),
+    "nsn_attention_merge": (I32, [P, I64, I64, I32, P, P, I32, P, P]),
     "nsn_attention_workspace_floats": (I64, [I64, I64, I32]),
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
 }

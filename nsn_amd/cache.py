@@ -26,6 +26,7 @@ def alloc_packed(batch, heads, block_cap, tail_cap, bits, tail_dtype, device):
         norm=torch.empty((batch, heads, block_cap, BLOCK), dtype=torch.float16, device=device),
         min=torch.empty((batch, heads, block_cap, DIM), dtype=torch.float16, device=device),
         scale=torch.empty((batch, heads, block_cap, DIM), dtype=torch.float16, device=device),
+        factor=torch.zeros((batch, heads, block_cap, BLOCK), dtype=torch.float32, device=device),
         blocks=torch.zeros(batch, dtype=torch.int32, device=device),
         tail=torch.zeros((batch, heads, max(1, tail_cap), DIM), dtype=tail_dtype, device=device),
         bits=bits)
@@ -54,7 +55,7 @@ def pack_sequences(x, lengths, bits=3, tail_dtype=None, status=None):
             rc = lib.nsn_encode_blocks(
                 xc[b].data_ptr(), _dev.dtype_code(xc.dtype), H, nblk[b], Tcap * DIM, 0, bits, order, 1,
                 kv.codes[b].data_ptr(), kv.norm[b].data_ptr(), kv.min[b].data_ptr(), kv.scale[b].data_ptr(),
-                None, cap, 0, 0, None, st.data_ptr(), _dev.stream())
+                None, kv.factor[b].data_ptr(), cap, 0, 0, None, st.data_ptr(), _dev.stream())
             _lib.check(rc, "nsn_encode_blocks")
         t0 = nblk[b] * BLOCK
         if lengths[b] > t0:

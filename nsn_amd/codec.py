@@ -57,7 +57,7 @@ def encode_group(x, start, bits=3, status=None, check=True):
     if rows and n:
         rc = _lib.lib().nsn_encode_blocks(
             xc.data_ptr(), _dev.dtype_code(xc.dtype), rows, n, n * BLOCK * DIM, 0, bits, order, 1,
-            codes.data_ptr(), norm.data_ptr(), mn.data_ptr(), sc.data_ptr(), hdr.data_ptr(), n, 0, start,
+            codes.data_ptr(), norm.data_ptr(), mn.data_ptr(), sc.data_ptr(), hdr.data_ptr(), None, n, 0, start,
             None, st.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_encode_blocks")
     if check and status is None:

@@ -419,18 +419,37 @@ int nsn_decode_attention(const nsn_attn_args *a, nsn_stream_t stream) {
     const dim3 grid(static_cast<unsigned>(a->n_splits), static_cast<unsigned>(a->heads_kv),
                     static_cast<unsigned>(a->batch));
     int rc;
+    if (a->kernel == NSN_ATTN_FAST) {
+        rc = launch_attn_fast(a, st);
+        if (rc != NSN_OK) return rc;
+        if (!a->merge) return NSN_OK;
+        return nsn_attention_merge(a->partials, a->batch, a->heads_q, a->n_splits, a->ctx, a->out, a->out_dtype,
+                                   a->status, stream);
+    }
     if (a->kernel != NSN_ATTN_REFERENCE) return NSN_EINVAL;
     if (a->bits == 3) rc = dispatch_q<3>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
     else if (a->bits == 4) rc = dispatch_q<4>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
     else rc = dispatch_q<5>(a->q_dtype, a->kv_round_dtype, a->v.tail_dtype, scores, grid, st, p);
     if (rc != NSN_OK) return rc;
-    const dim3 mgrid(static_cast<unsigned>(a->batch * a->heads_q));
-    if (a->out_dtype == NSN_DTYPE_BF16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
-    else if (a->out_dtype == NSN_DTYPE_F16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
+    if (!a->merge) return NSN_OK;
+    return nsn_attention_merge(a->partials, a->batch, a->heads_q, a->n_splits, a->ctx, a->out, a->out_dtype,
+                               a->status, stream);
+}
+
+int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, int n_splits, float *ctx, void *out,
+                        int out_dtype, int32_t *status, nsn_stream_t stream) {
+    if (!partials || !out || batch <= 0 || heads_q <= 0 || n_splits <= 0) return NSN_EINVAL;
+    if (batch * heads_q > 0x7fffffff) return NSN_EINVAL;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 mgrid(static_cast<unsigned>(batch * heads_q));
+    if (out_dtype == NSN_DTYPE_BF16)
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
+    else if (out_dtype == NSN_DTYPE_F16)
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
+    else if (out_dtype == NSN_DTYPE_F32)
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
     else
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(128), 0, st, a->partials, a->n_splits, a->ctx, a->out, a->status);
+        return NSN_EINVAL;
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }
 

@@ -29,6 +29,7 @@ struct EncodeParams {
     uint8_t *codes;
     uint16_t *norms, *mins, *scales;
     uint8_t *headers;
+    float *factors;
     int64_t out_outer_blocks, out_block_offset, header_start_token;
     uint8_t *codes_unpacked;
     int32_t *status;
@@ -95,6 +96,37 @@ __device__ __forceinline__ void unpack32(const uint32_t (&w)[BITS], uint32_t (&c
     }
 }
 
+// Decode factors f_t = n_t / max(|d_t|, 1e-12) with d_t = m + s*q (fp16 metadata
+// as fp32, unfused multiply/add, torch's 8-lane norm order) for the 64 rows of
+// a block whose u8 codes are in LDS.  f_t * d_t is the row nsn_decode returns
+// (up to the final rounding), so the decode kernels can renormalise a packed
+// token with one multiply.  Writes f_t for t = tid/4 from lanes tid%4 == 0.
+__device__ __forceinline__ void block_factors_lds(const uint8_t *codes_s, const float *m16f, const float *s16f,
+                                                  const float *n16f, float *factors) {
+    const int tid = threadIdx.x;
+    const int r = tid >> 2, jp = (tid & 3) * 2;
+    const uint8_t *cr = codes_s + r * kDim;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int c = 8 * k + jp;
+        const float p0 = s16f[c] * static_cast<float>(cr[c]);
+        const float p1 = s16f[c + 1] * static_cast<float>(cr[c + 1]);
+        const float d0 = m16f[c] + p0, d1 = m16f[c + 1] + p1;
+        a0 = __builtin_fmaf(d0, d0, a0);
+        a1 = __builtin_fmaf(d1, d1, a1);
+    }
+    const float b0 = __shfl_down(a0, 1), b1 = __shfl_down(a1, 1);
+    const float c0 = __shfl_down(a0, 2), c1 = __shfl_down(a1, 2);
+    const float d0 = __shfl_down(a0, 3), d1 = __shfl_down(a1, 3);
+    if ((tid & 3) == 0) {
+        const float acc[8] = {a0, a1, b0, b1, c0, c1, d0, d1};
+        const float den = clamp_eps(sqrt_rn(lane8_sum(acc)));
+        const float n = n16f[r];
+        factors[r] = (n == 0.f) ? 0.f : div_by_recip(n, recip_rn(den));
+    }
+}
+
 template <int DT, int BITS, int ORDER>
 __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     using T = typename Elem<DT>::T;
@@ -106,6 +138,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     __shared__ float m_s[kDim], s_s[kDim];
     __shared__ double rs_s[kDim];
     __shared__ uint32_t codes_s[kBlockTok * kDim / 4];
+    __shared__ float mh_s[kDim], sh_s[kDim], nh_s[kBlockTok];
     __shared__ int bad_s;
 
     const int tid = threadIdx.x;
@@ -208,6 +241,8 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
         p.mins[ob * kDim + tid] = hm;
         p.scales[ob * kDim + tid] = hs;
+        mh_s[tid] = f16_bits_to_f32(hm);
+        sh_s[tid] = f16_bits_to_f32(hs);
         if ((hm & 0x7c00u) == 0x7c00u || (hs & 0x7c00u) == 0x7c00u) meta_flags |= NSN_ST_META_NONFINITE;
         if (s != 0.f && (hs & 0x7fffu) == 0) meta_flags |= NSN_ST_META_UNDERFLOW;
     } else if (tid < kDim + kBlockTok) {
@@ -215,6 +250,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         const float n = nrm_s[t];
         const uint16_t hn = f32_to_f16_bits(n);
         p.norms[ob * kBlockTok + t] = hn;
+        nh_s[t] = f16_bits_to_f32(hn);
         if ((hn & 0x7c00u) == 0x7c00u) meta_flags |= NSN_ST_META_NONFINITE;
         if (n != 0.f && (hn & 0x7fffu) == 0) meta_flags |= NSN_ST_META_UNDERFLOW;
     }
@@ -261,6 +297,8 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
             du[1] = make_uint4(codes_s[g * 8 + 4], codes_s[g * 8 + 5], codes_s[g * 8 + 6], codes_s[g * 8 + 7]);
         }
     }
+    if (p.factors)
+        block_factors_lds(reinterpret_cast<const uint8_t *>(codes_s), mh_s, sh_s, nh_s, p.factors + ob * kBlockTok);
     if (tid == 0 && p.headers) {
         const uint64_t tok = static_cast<uint64_t>(p.header_start_token + i * kBlockTok);
         uint32_t *h = reinterpret_cast<uint32_t *>(p.headers + ob * 12);
@@ -483,6 +521,39 @@ __global__ __launch_bounds__(256) void restore_kernel(RestoreParams p) {
 }
 
 // =====================================================================
+// Decode factors of existing packed blocks (one 256-thread group per block).
+// =====================================================================
+
+template <int BITS>
+__global__ __launch_bounds__(256) void factor_kernel(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins,
+                                                     const uint16_t *scales, int64_t n_blocks, int64_t in_outer_blocks,
+                                                     float *factors) {
+    __shared__ float m_s[kDim], s_s[kDim], n_s[kBlockTok];
+    __shared__ uint32_t codes_s[kBlockTok * kDim / 4];
+    const int tid = threadIdx.x;
+    const int64_t o = blockIdx.x / n_blocks, i = blockIdx.x - o * n_blocks;
+    const int64_t ib = o * in_outer_blocks + i;
+    if (tid < kDim) {
+        m_s[tid] = f16_bits_to_f32(mins[ib * kDim + tid]);
+        s_s[tid] = f16_bits_to_f32(scales[ib * kDim + tid]);
+    } else if (tid < kDim + kBlockTok) {
+        n_s[tid - kDim] = f16_bits_to_f32(norms[ib * kBlockTok + tid - kDim]);
+    }
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(codes + ib * packed_block_bytes(BITS)) + tid * BITS;
+        uint32_t w[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) w[k] = src[k];
+        uint32_t c[32];
+        unpack32<BITS>(w, c);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) codes_s[tid * 8 + k] = c[4 * k] | (c[4 * k + 1] << 8) | (c[4 * k + 2] << 16) | (c[4 * k + 3] << 24);
+    }
+    __syncthreads();
+    block_factors_lds(reinterpret_cast<const uint8_t *>(codes_s), m_s, s_s, n_s, factors + ib * kBlockTok);
+}
+
+// =====================================================================
 // Finite scan over up to 16 arrays.
 // =====================================================================
 
@@ -565,7 +636,7 @@ const char *nsn_version(void) { return "nsn_hip 0.1 gfx950"; }
 
 int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blocks, int64_t x_outer_stride,
                       int64_t x_token_offset, int bits, int norm_order, int zero_flat_scale, uint8_t *codes,
-                      uint16_t *norms, uint16_t *mins, uint16_t *scales, uint8_t *headers,
+                      uint16_t *norms, uint16_t *mins, uint16_t *scales, uint8_t *headers, float *factors,
                       int64_t out_outer_blocks, int64_t out_block_offset, int64_t header_start_token,
                       uint8_t *codes_unpacked, int32_t *status, nsn_stream_t stream) {
     if (n_outer < 0 || n_blocks < 0 || !bits_ok(bits) || !dtype_ok(x_dtype)) return NSN_EINVAL;
@@ -576,11 +647,12 @@ int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blo
     if (!aligned(x, 16) || (x_outer_stride * esize) % 16 || (x_token_offset * kDim * esize) % 16) return NSN_EINVAL;
     if (!aligned(codes, 16) || !aligned(norms, 2) || !aligned(mins, 2) || !aligned(scales, 2)) return NSN_EINVAL;
     if (headers && !aligned(headers, 4)) return NSN_EINVAL;
+    if (factors && !aligned(factors, 4)) return NSN_EINVAL;
     if (codes_unpacked && !aligned(codes_unpacked, 16)) return NSN_EINVAL;
     if (out_outer_blocks < out_block_offset + n_blocks) return NSN_EINVAL;
     const int64_t total = n_outer * n_blocks;
     if (total > 0x7fffffff) return NSN_EINVAL;
-    EncodeParams p{x, n_blocks, x_outer_stride, x_token_offset, codes, norms, mins, scales, headers,
+    EncodeParams p{x, n_blocks, x_outer_stride, x_token_offset, codes, norms, mins, scales, headers, factors,
                    out_outer_blocks, out_block_offset, header_start_token, codes_unpacked, status,
                    zero_flat_scale};
     const dim3 grid(static_cast<unsigned>(total));
@@ -649,6 +721,21 @@ int nsn_restore_blocks(const uint8_t *codes, int codes_are_unpacked, const uint1
     if (bits == 3) restore_dispatch_out<3>(out_dtype, tail_dtype, grid, s, p);
     else if (bits == 4) restore_dispatch_out<4>(out_dtype, tail_dtype, grid, s, p);
     else restore_dispatch_out<5>(out_dtype, tail_dtype, grid, s, p);
+    return launch_status();
+}
+
+int nsn_block_factors(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins, const uint16_t *scales,
+                      int64_t n_outer, int64_t n_blocks, int64_t in_outer_blocks, int bits, float *factors,
+                      nsn_stream_t stream) {
+    if (n_outer < 0 || n_blocks < 0 || !bits_ok(bits) || in_outer_blocks < n_blocks) return NSN_EINVAL;
+    if (n_outer == 0 || n_blocks == 0) return NSN_OK;
+    if (!codes || !norms || !mins || !scales || !factors || !aligned(codes, 16)) return NSN_EINVAL;
+    if (n_outer * n_blocks > 0x7fffffff) return NSN_EINVAL;
+    const dim3 grid(static_cast<unsigned>(n_outer * n_blocks));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (bits == 3) hipLaunchKernelGGL(factor_kernel<3>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
+    else if (bits == 4) hipLaunchKernelGGL(factor_kernel<4>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
+    else hipLaunchKernelGGL(factor_kernel<5>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
     return launch_status();
 }
 

@@ -101,6 +101,9 @@ __device__ __forceinline__ float lane8_sum(const float (&acc)[8]) {
     return s;
 }
 
+// Fast (MFMA) decode attention launcher, defined in nsn_fast.hip.
+int launch_attn_fast(const nsn_attn_args *a, hipStream_t st);
+
 // ------------------------------------------------------------ status word
 
 __device__ __forceinline__ void raise_status(int32_t* status, int bits) {

@@ -39,6 +39,7 @@ class PackedKV:
 
     codes  u8  [B, Hkv, cap, 64*128*bits/8]     norm f16 [B, Hkv, cap, 64(,1)]
     min    f16 [B, Hkv, cap, (1,)128]           scale f16 [B, Hkv, cap, (1,)128]
+    factor f32 [B, Hkv, cap, 64]  decode factors n/|m+s*q| (fast kernel; see nsn_block_factors)
     blocks i32 [B]  packed blocks of each sequence (tokens 0 .. 64*blocks-1)
     tail   f16/bf16 [B, Hkv, tail_cap, 128]  tokens 64*blocks[b] .. seq_len[b]-1
     """
@@ -46,6 +47,7 @@ class PackedKV:
     norm: Optional[torch.Tensor]
     min: Optional[torch.Tensor]
     scale: Optional[torch.Tensor]
+    factor: Optional[torch.Tensor]
     blocks: Optional[torch.Tensor]
     tail: Optional[torch.Tensor]
     bits: int = 3
@@ -61,6 +63,8 @@ class PackedKV:
             s.norms = self.norm.data_ptr()
             s.mins = self.min.data_ptr()
             s.scales = self.scale.data_ptr()
+            if self.factor is not None:
+                s.factors = self.factor.data_ptr()
             s.blocks = self.blocks.data_ptr()
             s.block_cap = self.codes.shape[2]
         if self.tail is not None:
@@ -83,13 +87,16 @@ class PackedKV:
                         "Packed metadata layout")
             require(self.blocks is not None and self.blocks.dtype == torch.int32 and self.blocks.numel() == batch,
                     "Packed block counts")
+            if self.factor is not None:
+                require(self.factor.dtype == torch.float32 and self.factor.is_contiguous()
+                        and self.factor.numel() == batch * heads * cap * BLOCK, "Decode factor layout")
         if self.tail is not None:
             require(self.tail.dtype in (torch.float16, torch.bfloat16) and self.tail.is_contiguous()
                     and self.tail.ndim == 4 and tuple(self.tail.shape[:2]) == (batch, heads)
                     and self.tail.shape[3] == DIM, "Tail shape/type")
 
 
-def default_split(batch, heads_kv, max_len, target_units=1024, min_split=256):
+def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
     """Split the context so that batch*heads_kv*splits covers the 256 CUs several times."""
     want = max(1, math.ceil(target_units / max(1, batch * heads_kv)))
     split = max(min_split, math.ceil(max_len / want / BLOCK) * BLOCK)
@@ -99,7 +106,7 @@ def default_split(batch, heads_kv, max_len, target_units=1024, min_split=256):
 
 def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
                      kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
-                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None):
+                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True):
     """Batched single-query decode attention.
 
     q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
@@ -114,6 +121,11 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     require(Hq % Hkv == 0 and Hq // Hkv <= 16, "GQA group")
     require(seq_len.dtype == torch.int32 and seq_len.numel() == B and seq_len.is_cuda, "Sequence lengths")
     v.validate(B, Hkv)
+    if kernel == "fast":
+        for side in ((v,) if scores is not None else (k, v)):
+            require(side.codes is None or side.factor is not None, "Fast kernel needs decode factors")
+            require(side.tail is None or side.tail.dtype == torch.float16, "Fast kernel reads fp16 tails")
+        require(v.bits in (3, 5), "Fast kernel supports 3- and 5-bit codes")
     if scores is None:
         require(k is not None, "K cache required")
         k.validate(B, Hkv)
@@ -167,6 +179,7 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     a.out = out.data_ptr()
     a.out_dtype = _dev.dtype_code(out_dtype)
     a.status = st.data_ptr()
+    a.merge = 1 if merge else 0
     rc = _lib.lib().nsn_decode_attention(a, _dev.stream())
     _lib.check(rc, "nsn_decode_attention")
     if check and status is None:
@@ -200,15 +213,29 @@ def _validate_lengths(seq_len, k, v, scores, max_seq_len):
 
 # --------------------------------------------------- reference (b == 1) surface
 
-def _group_side(g, tail, bits=None):
+def block_factors(codes, norm, mn, sc, bits):
+    """Decode factors n/|m+s*q| of packed blocks codes [rows, n, nbytes] -> fp32 [rows, n, 64]."""
+    rows, n, _ = codes.shape
+    out = torch.empty((rows, n, BLOCK), dtype=torch.float32, device=codes.device)
+    norm, mn, sc = (t.contiguous() for t in (norm, mn, sc))
+    rc = _lib.lib().nsn_block_factors(codes.contiguous().data_ptr(), norm.data_ptr(), mn.data_ptr(), sc.data_ptr(),
+                                      rows, n, n, bits, out.data_ptr(), _dev.stream())
+    _lib.check(rc, "nsn_block_factors")
+    return out
+
+
+def _group_side(g, tail, bits=None, factors=False):
     """Reference group dict (+ tail [1,H,L,128]) -> PackedKV for batch 1."""
     dev = tail.device
     if g is None:
-        return PackedKV(None, None, None, None, None, tail.contiguous(), bits or 3)
+        return PackedKV(None, None, None, None, None, None, tail.contiguous(), bits or 3)
     codes = g["codes"]
-    n = codes.shape[2]
-    b = (codes.shape[3] * 8) // (BLOCK * DIM)
-    return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2],
+    b_, h, n, nbytes = codes.shape
+    b = (nbytes * 8) // (BLOCK * DIM)
+    f = None
+    if factors:
+        f = block_factors(codes.reshape(b_ * h, n, nbytes), *g["metas"], b).reshape(b_, h, n, BLOCK)
+    return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2], f,
                     torch.full((1,), n, dtype=torch.int32, device=dev), tail.contiguous(), b)
 
 
@@ -297,7 +324,8 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference"):
     """
     Hq = q.shape[1]
     T = _length(g, kt)
-    ks, vs = _group_side(g, kt), _group_side(vg, vt)
+    fast = kernel == "fast"
+    ks, vs = _group_side(g, kt, factors=fast), _group_side(vg, vt, factors=fast)
     seq = torch.full((1,), T, dtype=torch.int32, device=q.device)
     out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
                                 kv_round_dtype=kt.dtype)
@@ -319,10 +347,11 @@ def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
     """
     Hq = q.shape[1]
     T = v.shape[2]
-    vs = PackedKV(None, None, None, None, None, v.contiguous(), 3)
+    vs = PackedKV(None, None, None, None, None, None, v.contiguous(), 3)
     seq = torch.full((1,), T, dtype=torch.int32, device=v.device)
     if full:
-        out, ctx = decode_attention(q.reshape(1, Hq, DIM), _group_side(g, tail), vs, seq, max_seq_len=T,
+        out, ctx = decode_attention(q.reshape(1, Hq, DIM), _group_side(g, tail, factors=kernel == "fast"), vs, seq,
+                                    max_seq_len=T,
                                     kernel=kernel, kv_round_dtype=v.dtype)
     else:
         require(score is not None and tuple(score.shape) == (1, Hq, T), "Score shape/type")

@@ -61,7 +61,7 @@ def encode_blocks(x, bits, *, zero_flat_scale=True, want_unpacked=True, want_hea
     if nb:
         rc = _lib.lib().nsn_encode_blocks(
             xc.data_ptr(), _dev.dtype_code(xc.dtype), 1, nb, 0, 0, bits, order, 1 if zero_flat_scale else 0,
-            codes.data_ptr(), n.data_ptr(), m.data_ptr(), s.data_ptr(), _dev.ptr(hdr), nb, 0, start,
+            codes.data_ptr(), n.data_ptr(), m.data_ptr(), s.data_ptr(), _dev.ptr(hdr), None, nb, 0, start,
             _dev.ptr(q), st.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_encode_blocks")
     if check and status is None:

@@ -189,6 +189,23 @@ def nsn_decode_f32(q, n16, m16, s16):
     return y
 
 
+def decode_factors(q, n16, m16, s16):
+    """f_t = n_t / max(|m + s*q_t|, 1e-12) in fp32 (the norm in nsn_decode's
+    order, unfused m + s*q, IEEE division; 0 where n == 0): the per-token factor
+    that turns m + s*q_t into the row nsn_decode reconstructs (before rounding).
+    Pinned by tests/test_oracle.py against nsn_decode itself."""
+    q = np.ascontiguousarray(q, np.uint8)
+    lead = q.shape[:-2]
+    m = from_f16_bits(m16).reshape(lead + (1, DIM))
+    s = from_f16_bits(s16).reshape(lead + (1, DIM))
+    n = from_f16_bits(n16).reshape(lead + (BLOCK,))
+    d = (m + (s * q.astype(np.float32)).astype(np.float32)).astype(np.float32)
+    den = vector_norm(d)
+    den = np.where(den > EPS, den, EPS).astype(np.float32)
+    f = (n / den).astype(np.float32)
+    return np.where(n == 0, np.float32(0), f).astype(np.float32)
+
+
 def nsn_decode(q, n16, m16, s16, dtype):
     """``nsn_decode(q, metas, dtype)``; returns raw bits of ``dtype``."""
     return cast_bits(nsn_decode_f32(q, n16, m16, s16), dtype)

@@ -37,8 +37,11 @@ def oracle_restore(x16, length, bits, round_dtype):
         q, n, m, s, err = O.nsn_encode(blocks, bits)
         assert err == 0
         y = O.nsn_decode_f32(q, n, m, s).reshape(H, C, 128)
-        bitsr = O.cast_bits(y, round_dtype)
-        parts.append(O.from_bf16_bits(bitsr) if round_dtype == "bfloat16" else O.from_f16_bits(bitsr))
+        if round_dtype == "float32":          # the fast kernel keeps fp32 reconstructions
+            parts.append(y)
+        else:
+            bitsr = O.cast_bits(y, round_dtype)
+            parts.append(O.from_bf16_bits(bitsr) if round_dtype == "bfloat16" else O.from_f16_bits(bitsr))
     if length > C:
         parts.append(x16[:, C:length].astype(np.float32))
     return np.concatenate(parts, axis=1)
@@ -74,37 +77,40 @@ def oracle_ctx(k, v, qb, lengths, bits, round_dtype="float16"):
     return out
 
 
-@pytest.mark.parametrize("kernel", ["reference"])
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
 @pytest.mark.parametrize("B,Hq,Hkv,lengths", [
     (1, 4, 4, [200]),              # MHA, 3 blocks + 8 tail
     (2, 8, 2, [1000, 333]),        # GQA 4:1, ragged
     (3, 6, 1, [64, 65, 17]),       # GQA 6:1, exact block / block+1 / tail only
+    (2, 16, 2, [700, 130]),        # GQA 8:1
 ])
 def test_decode_vs_oracle(kernel, B, Hq, Hkv, lengths):
     k, v, qb, kk, vv, seq = make_case(1, B, Hq, Hkv, lengths)
     out, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel=kernel, kv_round_dtype=torch.float16)
-    ref = oracle_ctx(k, v, qb, lengths, 3)
+    ref = oracle_ctx(k, v, qb, lengths, 3, "float16" if kernel == "reference" else "float32")
     ok, err = within(ctx.cpu().numpy(), ref)
     assert ok, err
     # the bf16 output is the RNE cast of the fp32 context
     assert torch.equal(out.cpu(), ctx.cpu().to(torch.bfloat16))
 
 
-@pytest.mark.parametrize("kernel", ["reference"])
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
 def test_5bit_decode_vs_oracle(kernel):
     lengths = [640, 200]
     k, v, qb, kk, vv, seq = make_case(3, 2, 8, 2, lengths, bits=5, gen="heavy")
     _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel=kernel, kv_round_dtype=torch.float16)
-    ok, err = within(ctx.cpu().numpy(), oracle_ctx(k, v, qb, lengths, 5))
+    ok, err = within(ctx.cpu().numpy(), oracle_ctx(k, v, qb, lengths, 5, "float16" if kernel == "reference" else "float32"))
     assert ok, err
 
 
-def test_split_invariance():
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+def test_split_invariance(kernel):
     lengths = [1500, 900]
     k, v, qb, kk, vv, seq = make_case(5, 2, 8, 2, lengths)
     outs = []
     for split in (64, 256, 1536):
-        _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, split_tokens=split, kv_round_dtype=torch.float16)
+        _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, split_tokens=split, kv_round_dtype=torch.float16,
+                                          kernel=kernel)
         outs.append(ctx.cpu().numpy())
     for o in outs[1:]:
         assert np.allclose(o, outs[0], atol=1e-5, rtol=1e-5)
@@ -176,7 +182,8 @@ def test_vf01_normal_fixtures_fused_equals_bridge_and_oracle():
         assert ok, (f["id"], err)
 
 
-def test_score_input_readout_config1():
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+def test_score_input_readout_config1(kernel):
     """C1: B=1, 32q/8kv, 64 packed blocks + 37-token fp16 tail; logits N(0,1)*4."""
     rng = np.random.default_rng(1)
     from nsn_amd import synthetic
@@ -186,18 +193,72 @@ def test_score_input_readout_config1():
     vv, seq = cache.pack_sequences(torch.from_numpy(v).to(DEV), [T])
     qdummy = torch.zeros(1, 32, 128, dtype=torch.bfloat16, device=DEV)
     _, ctx = kernels.decode_attention(qdummy, None, vv, seq, scores=torch.from_numpy(scores).to(DEV),
-                                      kv_round_dtype=torch.float16)
-    vr = oracle_restore(v[0], T, 3, "float16")
+                                      kv_round_dtype=torch.float16, kernel=kernel)
+    vr = oracle_restore(v[0], T, 3, "float16" if kernel == "reference" else "float32")
     ref = O.readout64(scores, vr[None], groups=4)
     ok, err = within(ctx.cpu().numpy(), ref)
     assert ok, err
     # bridge: V restored to HBM, then the same readout -> bitwise equal
     vfull = codec.restore(vv.codes[0], (vv.norm[0], vv.min[0], vv.scale[0]), 3, torch.float16,
                           tail=vv.tail[0, :, :37])
-    vd = kernels.PackedKV(None, None, None, None, None, vfull[None].contiguous(), 3)
+    vd = kernels.PackedKV(None, None, None, None, None, None, vfull[None].contiguous(), 3)
     _, ctx_b = kernels.decode_attention(qdummy, None, vd, seq, scores=torch.from_numpy(scores).to(DEV),
-                                        kv_round_dtype=torch.float16)
-    assert torch.equal(ctx.cpu(), ctx_b.cpu())
+                                        kv_round_dtype=torch.float16, kernel=kernel)
+    if kernel == "reference":
+        assert torch.equal(ctx.cpu(), ctx_b.cpu())
+    else:
+        ok, err = within(ctx_b.cpu().numpy(), ref)
+        assert ok, err
+
+
+@pytest.mark.parametrize("mode", ["dense", "bridge"])
+def test_fast_dense_and_bridge_vs_oracle(mode):
+    """fp16-KV baseline (no packed blocks) and the bridge (packed K, restored V)."""
+    lengths = [1000, 333]
+    k, v, qb, kk, vv, seq = make_case(11, 2, 8, 2, lengths)
+    if mode == "dense":
+        kd = kernels.PackedKV(None, None, None, None, None, None, torch.from_numpy(k).to(DEV), 3)
+        vd = kernels.PackedKV(None, None, None, None, None, None, torch.from_numpy(v).to(DEV), 3)
+        _, ctx = kernels.decode_attention(qb.to(DEV), kd, vd, seq, kernel="fast")
+        ref = np.zeros((2, 8, 128))
+        for b, L in enumerate(lengths):
+            c, _ = O.decode_attention64(qb.float().numpy()[b:b + 1], k[b:b + 1, :, :L].astype(np.float32),
+                                        v[b:b + 1, :, :L].astype(np.float32))
+            ref[b] = c[0]
+    else:
+        vfull = torch.zeros((2, 2, 1000, 128), dtype=torch.float16, device=DEV)
+        for b, L in enumerate(lengths):
+            nb = L // 64
+            vfull[b, :, :L] = codec.restore(vv.codes[b, :, :nb].contiguous(), (vv.norm[b, :, :nb], vv.min[b, :, :nb],
+                                            vv.scale[b, :, :nb]), 3, torch.float16, tail=vv.tail[b, :, :L - nb * 64])
+        vd = kernels.PackedKV(None, None, None, None, None, None, vfull, 3)
+        _, ctx = kernels.decode_attention(qb.to(DEV), kk, vd, seq, kernel="fast")
+        # K packed (fp32 reconstruction in-kernel) and V restored to fp16 in HBM
+        ref = np.zeros((2, 8, 128))
+        for b, L in enumerate(lengths):
+            kr = oracle_restore(k[b], L, 3, "float32")
+            vr = oracle_restore(v[b], L, 3, "float16")
+            c, _ = O.decode_attention64(qb.float().numpy()[b:b + 1], kr[None], vr[None])
+            ref[b] = c[0]
+    ok, err = within(ctx.cpu().numpy(), ref)
+    assert ok, err
+
+
+def test_fast_matches_reference_launch_surface():
+    """The reference-shaped launch() with the fast kernel (fp16 tails) agrees with the exact-order kernel."""
+    rng = np.random.default_rng(12)
+    from nsn_amd import synthetic
+    x = synthetic.kv_tokens(rng, (2, 8), 64 * 5 + 21)
+    k16 = torch.from_numpy(x[0]).to(DEV)[None]
+    v16 = torch.from_numpy(x[1]).to(DEV)[None]
+    g = codec.encode_group(k16[:, :, :320].reshape(1, 8, 5, 64, 128).contiguous(), 0)
+    vg = codec.encode_group(v16[:, :, :320].reshape(1, 8, 5, 64, 128).contiguous(), 0)
+    kt, vt = k16[:, :, 320:].contiguous(), v16[:, :, 320:].contiguous()
+    q = torch.from_numpy(rng.standard_normal((1, 32, 1, 128)).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    _, c_ref, _, _ = kernels.launch(g, kt, q, vg, vt, kernel="reference")
+    _, c_fast, _, _ = kernels.launch(g, kt, q, vg, vt, kernel="fast")
+    ok, err = within(c_fast.cpu().numpy(), c_ref.cpu().numpy().astype(np.float64))
+    assert ok, err
 
 
 def test_negative_fixtures_rejected_at_reference_stage():

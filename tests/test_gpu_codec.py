@@ -157,6 +157,25 @@ def test_pack3_kats_and_exhaustive_byte_pairs(golden):
     assert np.array_equal(got, O.unpack_bits_numpy(packed, n, 3))
 
 
+@pytest.mark.parametrize("bits", [3, 5])
+def test_decode_factors_vs_oracle(bits):
+    from nsn_amd import cache
+    rng = np.random.default_rng(40 + bits)
+    x = (rng.standard_normal((2, 3, 320, 128)) * rng.lognormal(0, 1, (2, 3, 320, 1))).astype(np.float16)
+    x[0, 1, 70] = 0
+    kv, _ = cache.pack_sequences(torch.from_numpy(x).to(DEV), [320, 300], bits=bits)
+    for b, L in enumerate((320, 300)):
+        nb = L // 64
+        q_o, n_o, m_o, s_o, _ = O.nsn_encode(x[b, :, :nb * 64].astype(np.float32).reshape(3, nb, 64, 128), bits)
+        want = O.decode_factors(q_o, n_o, m_o, s_o)
+        got = kv.factor[b, :, :nb].cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        # standalone factor kernel on the same packed blocks
+        f2 = kernels.block_factors(kv.codes[b, :, :nb].contiguous(), kv.norm[b, :, :nb], kv.min[b, :, :nb],
+                                   kv.scale[b, :, :nb], bits).cpu().numpy()
+        assert np.array_equal(f2.view(np.uint32), want.view(np.uint32))
+
+
 def test_code_range_rejected():
     with pytest.raises(IntegrityError):
         codec.pack3(torch.tensor([1, 2, 8], dtype=torch.uint8, device=DEV))

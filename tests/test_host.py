@@ -36,7 +36,7 @@ def test_library_rejects_bad_arguments_without_gpu_work():
     # invalid bits / dtype / null pointers are rejected on the host before any launch
     assert lib.nsn_pack_codes(None, 10, 7, None, None, None) == _lib.NSN_EINVAL
     assert lib.nsn_unpack_codes(None, 10, 2, None, None) == _lib.NSN_EINVAL
-    assert lib.nsn_encode_blocks(None, 9, 1, 1, 0, 0, 3, 0, 1, None, None, None, None, None, 1, 0, 0,
+    assert lib.nsn_encode_blocks(None, 9, 1, 1, 0, 0, 3, 0, 1, None, None, None, None, None, None, 1, 0, 0,
                                  None, None, None) == _lib.NSN_EINVAL
     assert lib.nsn_decode_attention(None, None) == _lib.NSN_EINVAL
     a = _lib.AttnArgs()

@@ -169,6 +169,25 @@ def test_group_codec_and_real_blocks(golden):
         assert np.array_equal(y.reshape(-1), G[key + "restored"].reshape(-1)), name
 
 
+def test_decode_factors_reproduce_nsn_decode():
+    """f_t * (m + s*q) equals nsn_decode's n * ((m + s*q) / den) to within 2 ulp,
+    and exactly where the reference's quotient is exact (zero rows, n == 0)."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((8, 64, 128)) * rng.lognormal(0, 1, (8, 64, 1))).astype(np.float32)
+    x[0, 3] = 0.0
+    q, n16, m16, s16, err = O.nsn_encode(x, 3)
+    assert err == 0
+    f = O.decode_factors(q, n16, m16, s16)
+    assert f[0, 3] == 0.0
+    y = O.nsn_decode_f32(q, n16, m16, s16)
+    d = (O.from_f16_bits(m16) + (O.from_f16_bits(s16) * q.astype(np.float32)).astype(np.float32)).astype(np.float32)
+    approx = (f[..., None] * d).astype(np.float32)
+    ulp = np.spacing(np.abs(y).astype(np.float32))
+    assert np.all(np.abs(approx - y) <= 2 * ulp + 1e-30)
+    # planted mistake: dropping the norm (f = n) is far off
+    assert not np.allclose(O.from_f16_bits(n16).reshape(8, 64, 1) * d, y, rtol=1e-3)
+
+
 # ------------------------------------------------------------ encoder errors
 
 def test_encode_error_conditions():
