@@ -13,10 +13,26 @@ the roofline of the dominant (split) kernel, encode tokens/s, the on-GPU
 bridge and fp16-KV comparators, and the CPU oracle baseline.
 
     python bench.py [--steps 20] [--warmup 5] [--kernel fast|reference]
+
+Profiling (the commands behind the committed summaries under profiles/):
+
+    rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --profile
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o fetch -- python3 bench.py --profile
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o write -- python3 bench.py --profile
+    python3 bench.py --summarize OUT      # writes profiles/attn_fast_c2.{md,json}
+
+``--profile`` runs one 1 GiB device-to-device copy (the counter calibration:
+a plain copy kernel of known size) and then ``--steps`` decode steps.  The
+HBM traffic per split-kernel launch is FETCH_SIZE and WRITE_SIZE (KiB per
+dispatch) scaled by bytes-moved / counter-reading of that copy.  The normal
+run reports it as ``roofline.traffic`` when profiles/attn_fast_c2.json was
+measured on the current kernel source (sha256 of nsn_amd/csrc/nsn_fast.hip).
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import hashlib
 import json
 import math
 import os
@@ -42,6 +58,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-baselines", action="store_true", help="skip the bridge / fp16 comparators")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
+    p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
     return p.parse_args()
 
 
@@ -129,24 +147,163 @@ def cpu_baseline(kk, vv, q, lengths, seconds):
                        f"{dt * 1e3:.0f} ms, scaled by total/sample tokens = {scale:.2f}")
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
-              "described in DESIGN.md and no figure at several GPUs is produced.", file=sys.stderr)
-        sys.exit(2)
-    import numpy as np
-    import torch
-    from nsn_amd import _dev, _lib, cache, codec, kernels, synthetic
+PROFILE_JSON = ROOT / "profiles" / "attn_fast_c2.json"
+PROFILE_MD = ROOT / "profiles" / "attn_fast_c2.md"
+FAST_SOURCE = ROOT / "nsn_amd" / "csrc" / "nsn_fast.hip"
+CALIB_BYTES = 1 << 30
+SPLIT_KERNEL = "nsn::fast::attn_fast_kernel<3, 1, false, 4>"
+MERGE_KERNEL = "nsn::attn_merge_kernel<1>"
+CALIB_KERNEL = "__amd_rocclr_copyBuffer"
 
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
+
+def source_sha():
+    return hashlib.sha256(FAST_SOURCE.read_bytes()).hexdigest()
+
+
+def _rows(path_glob):
+    files = sorted(Path(path_glob[0]).glob(path_glob[1]))
+    if not files:
+        raise SystemExit(f"no {path_glob[1]} under {path_glob[0]}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _counter(dirname, counter):
+    """Per-dispatch readings (KiB) of one counter for the split kernel, the
+    merge kernel and the calibration copy (the only copy dispatch with a grid
+    of 64K threads or more; the other copies in the run move a few bytes)."""
+    out = {"split": [], "merge": [], "calib": []}
+    for r in _rows((dirname, "**/*counter_collection.csv")):
+        if r["Counter_Name"] != counter:
+            continue
+        name, val = r["Kernel_Name"], float(r["Counter_Value"])
+        if SPLIT_KERNEL in name:
+            out["split"].append(val)
+        elif MERGE_KERNEL in name:
+            out["merge"].append(val)
+        elif name.startswith(CALIB_KERNEL) and int(r["Grid_Size"]) >= 65536:
+            out["calib"].append(val)
+    return out
+
+
+def summarize(d):
+    """Write profiles/attn_fast_c2.{md,json} from rocprofv3 CSV output under d
+    (subdirectories kt/, fetch/, write/ made by the commands in the module docstring)."""
+    d = Path(d)
+    stats = _rows((d / "kt", "**/*kernel_stats.csv"))
+    fetch = _counter(d / "fetch", "FETCH_SIZE")
+    write = _counter(d / "write", "WRITE_SIZE")
+    for nm, c in (("FETCH_SIZE", fetch), ("WRITE_SIZE", write)):
+        if not (c["split"] and c["calib"]):
+            raise SystemExit(f"{nm}: split kernel or calibration copy missing")
+    mean = lambda xs: sum(xs) / len(xs)
+    f_scale = CALIB_BYTES / (mean(fetch["calib"]) * 1024)   # bytes moved per counted byte, reads
+    w_scale = CALIB_BYTES / (mean(write["calib"]) * 1024)   # the same for writes
+    split_read = mean(fetch["split"]) * 1024 * f_scale
+    split_write = mean(write["split"]) * 1024 * w_scale
+    lens = [int(x) for x in __import__("nsn_amd.synthetic", fromlist=["x"]).ragged_lengths(2, B, LMIN, LMAX)]
+    alg = algorithmic_bytes(lens, 3)
+    top = sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]
+    top += [r for r in stats if (SPLIT_KERNEL in r["Name"] or MERGE_KERNEL in r["Name"]) and r not in top]
+    split_avg = next(float(r["AverageNs"]) for r in stats if SPLIT_KERNEL in r["Name"]) / 1e3
+    fig = {"kernel": SPLIT_KERNEL, "source_sha256": source_sha(), "workload": "C2",
+           "split_avg_us": round(split_avg, 2), "fetch_kib": round(mean(fetch["split"]), 1),
+           "write_kib": round(mean(write["split"]), 1), "fetch_scale": round(f_scale, 4),
+           "write_scale": round(w_scale, 4), "read_bytes": int(split_read), "write_bytes": int(split_write),
+           "traffic": int(split_read + split_write), "algorithmic_bytes": alg}
+    PROFILE_JSON.write_text(json.dumps(fig, indent=1) + "\n")
+    L = ["# attn_fast_kernel on C2 (B=16, 32q/8kv, ctx U[16K,32K], INT3 + fp16 tail)", "",
+         "Commands (run from the repository root on one MI355X, `OUT` = an output folder):", "", "```"]
+    L += [ln.strip() for ln in __doc__.split("Profiling")[1].split("``--profile``")[0].strip().splitlines()[1:] if ln.strip()]
+    L += ["```", "", "`python3 bench.py --profile`: one 1 GiB copy (calibration), then "
+          "decode steps over the C2 cache (split kernel + merge per step).", "",
+          "## Kernel trace (rocprofv3 --kernel-trace --stats)", "",
+          "Top kernels by total time (the set-up kernels generate and pack the synthetic cache), "
+          "then the split and merge kernels of the decode step.", "",
+          "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for r in top:
+        L.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                 f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
+    L += ["", "## HBM traffic per dispatch (rocprofv3 --pmc, one counter per pass)", "",
+          "| dispatch | FETCH_SIZE KiB | WRITE_SIZE KiB |", "|---|---|---|",
+          f"| calibration copy, {CALIB_BYTES >> 20} MiB read + written | {mean(fetch['calib']):.0f} | {mean(write['calib']):.0f} |",
+          f"| split kernel (mean of {len(fetch['split'])}) | {mean(fetch['split']):.0f} | {mean(write['split']):.0f} |"]
+    if fetch["merge"]:
+        L.append(f"| merge kernel | {mean(fetch['merge']):.0f} | {mean(write['merge']):.0f} |")
+    L += ["", f"Scale factors from the copy (bytes moved per counted byte): reads x{f_scale:.3f}, "
+          f"writes x{w_scale:.3f}.", "",
+          f"Split kernel: {split_read / 1e6:.1f} MB read + {split_write / 1e6:.1f} MB written = "
+          f"**{fig['traffic'] / 1e6:.1f} MB** per launch, against {alg / 1e6:.1f} MB algorithmic "
+          f"(ratio {fig['traffic'] / alg:.3f}); average duration {split_avg:.1f} us under the profiler "
+          f"-> {alg / split_avg / 1e3:.0f} GB/s algorithmic.", "",
+          f"Kernel source sha256: `{fig['source_sha256']}`", ""]
+    PROFILE_MD.write_text("\n".join(L))
+    print("\n".join(L))
+
+
+def measured_traffic():
+    """HBM bytes per split-kernel launch from the committed profile, if it was
+    measured on this kernel source; else None."""
+    try:
+        fig = json.loads(PROFILE_JSON.read_text())
+    except (OSError, ValueError):
+        return None
+    return fig["traffic"] if fig.get("source_sha256") == source_sha() else None
+
+
+def make_workload(dev):
+    import torch
+    from nsn_amd import cache, synthetic
     lengths = [int(x) for x in synthetic.ragged_lengths(2, B, LMIN, LMAX)]
     gen = torch.Generator(device=dev).manual_seed(2)
     log(f"[bench] generating C2 K/V on the GPU: B={B} Hkv={HKV} Lmax={LMAX} (lengths {min(lengths)}..{max(lengths)})")
     k = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
     v = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
     q = torch.randn((B, HQ, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return lengths, k, v, q
+
+
+def profile_run(args):
+    """Calibration copy, then `steps` decode steps of the C2 workload."""
+    import torch
+    from nsn_amd import cache, kernels
+    dev = torch.device("cuda:0")
+    lengths, k, v, q = make_workload(dev)
+    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
+    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+    del k, v
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    max_len = max(lengths)
+    for i in range(args.steps):
+        kernels.decode_attention(q, kk, vv, seq, kernel=args.kernel, max_seq_len=max_len, check=(i == 0))
+    torch.cuda.synchronize()
+    log(f"[bench] profile run done: {args.steps} steps")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
+              "described in DESIGN.md and no figure at several GPUs is produced.", file=sys.stderr)
+        sys.exit(2)
+    if args.summarize:
+        summarize(args.summarize)
+        return
+    if args.profile:
+        profile_run(args)
+        return
+    import numpy as np
+    import torch
+    from nsn_amd import _dev, _lib, cache, codec, kernels, synthetic
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    lengths, k, v, q = make_workload(dev)
 
     # ---- encode throughput: all 64-token blocks of K (B*Hkv rows x 512 blocks) in one launch
     nblk = LMAX // 64
@@ -220,7 +377,8 @@ def main():
         "encode_tok_s": round(enc_tok_s, 1),
         "encode_gbs": round(enc_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic() if args.kernel == "fast" else None,
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
                      "kernel_us": round(ms_split * 1e3, 2)},
     }
