@@ -301,32 +301,50 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
     }
 }
 
-// Merge splits: one 128-thread block per (b, hq).
+// Merge splits: one 256-thread block (4 waves) per (b, hq).  Wave w sums
+// splits w, w+4, ... (all its loads in flight together), lane c owns channels
+// 2c, 2c+1; the four wave partials are combined in LDS.
 template <int ODT>
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float *partials, int n_splits, float *ctx, void *out,
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, int n_splits, float *ctx, void *out,
                                                          int32_t *status) {
+    __shared__ float red_z[4];
+    __shared__ float2 red_u[4][64];
     const int64_t bh = blockIdx.x;
-    const int c = threadIdx.x;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const float *base = partials + bh * n_splits * kPartStride;
     float L = -INFINITY;
-    for (int s = 0; s < n_splits; ++s) {
-        const float m = base[s * kPartStride];
-        L = m > L ? m : L;
-    }
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < n_splits; ++s) {
-        const float m = base[s * kPartStride];
+    for (int s = lane; s < n_splits; s += 64) L = fmaxf(L, base[static_cast<int64_t>(s) * kPartStride]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L = fmaxf(L, __shfl_xor(L, off));
+    float z = 0.f, u0 = 0.f, u1 = 0.f;
+#pragma unroll 4
+    for (int s = w; s < n_splits; s += 4) {
+        const float *ps = base + static_cast<int64_t>(s) * kPartStride;
+        const float m = ps[0];
         const float a = (m == -INFINITY) ? 0.f : expf(m - L);
-        const float zp = base[s * kPartStride + 1] * a;
-        const float up = base[s * kPartStride + 4 + c] * a;
-        den = den + zp;
-        num = num + up;
+        z = z + ps[1] * a;
+        const float2 u = *reinterpret_cast<const float2 *>(ps + 4 + 2 * lane);
+        u0 = u0 + u.x * a;
+        u1 = u1 + u.y * a;
     }
-    const float cx = num / den;
-    const typename Elem<ODT>::T ov = Elem<ODT>::store(cx);
-    if (ctx) ctx[bh * kDim + c] = cx;
-    static_cast<typename Elem<ODT>::T *>(out)[bh * kDim + c] = ov;
-    const bool bad = !finite(cx) || !finite(Elem<ODT>::load(ov)) || !(den > 0.f);
+    if (lane == 0) red_z[w] = z;
+    red_u[w][lane] = make_float2(u0, u1);
+    __syncthreads();
+    if (w != 0) return;
+    const float den = (red_z[0] + red_z[1]) + (red_z[2] + red_z[3]);
+    const float n0 = (red_u[0][lane].x + red_u[1][lane].x) + (red_u[2][lane].x + red_u[3][lane].x);
+    const float n1 = (red_u[0][lane].y + red_u[1][lane].y) + (red_u[2][lane].y + red_u[3][lane].y);
+    const float cx0 = n0 / den, cx1 = n1 / den;
+    const typename Elem<ODT>::T o0 = Elem<ODT>::store(cx0), o1 = Elem<ODT>::store(cx1);
+    const int64_t c = bh * kDim + 2 * lane;
+    if (ctx) {
+        ctx[c] = cx0;
+        ctx[c + 1] = cx1;
+    }
+    static_cast<typename Elem<ODT>::T *>(out)[c] = o0;
+    static_cast<typename Elem<ODT>::T *>(out)[c + 1] = o1;
+    const bool bad = !finite(cx0) || !finite(cx1) || !finite(Elem<ODT>::load(o0)) || !finite(Elem<ODT>::load(o1)) ||
+                     !(den > 0.f);
     if (bad) raise_status(status, NSN_ST_NONFINITE_OUTPUT);
 }
 
@@ -443,11 +461,11 @@ int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, i
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 mgrid(static_cast<unsigned>(batch * heads_q));
     if (out_dtype == NSN_DTYPE_BF16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
     else if (out_dtype == NSN_DTYPE_F16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
     else if (out_dtype == NSN_DTYPE_F32)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(128), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
     else
         return NSN_EINVAL;
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;

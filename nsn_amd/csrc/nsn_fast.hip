@@ -1,23 +1,27 @@
 // Fast single-query decode attention over NSN-packed K/V for gfx950 (MFMA).
 //
 // Same work decomposition and partial format as the exact-order kernel in
-// nsn_attn.hip (work unit = sequence x kv-head x context split, all G query
-// heads of the kv-head served by one pass over its blocks; log-sum-exp merge
-// of the splits).  One wave per work unit; per 64-token packed block:
+// nsn_attn.hip: work unit = sequence x kv-head x context split; all G query
+// heads of the kv-head are served by one pass over its blocks; the splits are
+// merged with a log-sum-exp merge.  One wave per work unit.  Per 64-token
+// packed block:
 //
 //   scores   S[h,t] = scale * f_K[t] * (q_h.m_K + sum_c (q_h[c] s_K[c]) z_K[t,c])
-//            The contraction over channels runs on v_mfma_f32_16x16x32_f16:
-//            B = raw codes z as fp16 subnormals (z * 2^-24, exact), A = the
-//            coefficient rows q_h (.) s_K split into fp16 hi + lo parts.
+//            The channel contraction runs on v_mfma_f32_16x16x32_f16.  B holds
+//            the raw 3-bit codes, masked in place inside 16-bit halves: a code
+//            at bit k of its half is the fp16 subnormal z * 2^(k-24), exact.
+//            A holds the coefficient rows q_h (.) s_K * 2^-k, split into fp16
+//            hi + lo (error-free product on packed fp16 FMA).
 //   softmax  online (running max / sum per head), exp2 with log2(e) folded.
-//   output   acc[h,c] += s_V[c] * sum_t p'[h,t] z_V[t,c] + m_V[c] * sum_t p'[h,t]
-//            with p' = p * f_V.  The V codes are transposed (tokens onto the
-//            contraction axis) by an MFMA against an identity fragment, then
-//            P' (fp16 hi/lo rows) x Z_V runs on MFMA.
+//            One 16-lane row of the wave per query head.
+//   output   acc[h,c] += s_V[c] * F * sum_t p'[h,t] z_V[t,c] + m_V[c] * sum_t p[h,t] f_V[t]
+//            with p' = p f_V / F as fp16 hi + lo rows (F = block max of f_V).  V codes are
+//            loaded channel-major (a lane owns 8 channels of 16 tokens), so
+//            the tokens already sit on the contraction axis of the B operand.
 //
 // f_K, f_V are the per-token decode factors n / |m + s*z| of each packed block
-// (nsn_block_factors): constant once a block is encoded, so they are read, not
-// recomputed.  Reconstruction therefore equals nsn_decode's up to rounding
+// (nsn_block_factors).  They are constant once a block is encoded, so they are
+// read, not recomputed.  Reconstruction equals nsn_decode's up to rounding
 // (loop_kv_pilot.py:216-225); results match the fp64 oracle within the stated
 // tolerance, not bit for bit.  Tokens past the packed prefix (the fp16 tail,
 // or a fully dense fp16 K/V for the fp16 baseline) take the same MFMA path
@@ -32,119 +36,122 @@ namespace nsn {
 namespace fast {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __fp16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPartStride = 132;
 constexpr int kMaxGroup = 8;
-constexpr float kTwo24 = 16777216.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kPScale = 16384.f;   // softmax weights enter the PV product as p * 2^14
 
 __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
-
+// v_perm_b32: byte i of the result = byte sel[i] of {hi:lo} (0..3 = lo, 4..7 = hi, 0x0c = 0).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+__device__ __forceinline__ half2v as_h2(uint32_t x) { return __builtin_bit_cast(half2v, x); }
+__device__ __forceinline__ uint32_t as_u(half2v x) { return __builtin_bit_cast(uint32_t, x); }
 // Two fp32 -> packed fp16 pair, round toward zero (v_cvt_pkrtz_f16_f32).
 __device__ __forceinline__ uint32_t pkrtz(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
-__device__ __forceinline__ float lo_f32(uint32_t p) { return static_cast<float>(__builtin_bit_cast(half2_t, p)[0]); }
-__device__ __forceinline__ float hi_f32(uint32_t p) { return static_cast<float>(__builtin_bit_cast(half2_t, p)[1]); }
+__device__ __forceinline__ float lo_f32(uint32_t p) { return static_cast<float>(__builtin_bit_cast(fp16x2, p)[0]); }
+__device__ __forceinline__ float hi_f32(uint32_t p) { return static_cast<float>(__builtin_bit_cast(fp16x2, p)[1]); }
+__device__ __forceinline__ float f16lo(uint32_t p) { return static_cast<float>(__builtin_bit_cast(half2v, p)[0]); }
+__device__ __forceinline__ float f16hi(uint32_t p) { return static_cast<float>(__builtin_bit_cast(half2v, p)[1]); }
 
-// Split 8 fp32 values into fp16 hi (round toward zero) and lo = rn(x - hi):
-// hi + lo carries ~22 significant bits.
-__device__ __forceinline__ void split_hilo(const float (&x)[8], u32x4 &hi, u32x4 &lo) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t h = pkrtz(x[2 * k], x[2 * k + 1]);
-        const float r0 = x[2 * k] - lo_f32(h), r1 = x[2 * k + 1] - hi_f32(h);
-        hi[k] = h;
-        lo[k] = pkrtz(r0, r1);
-    }
+// fp32 pair -> fp16 hi (toward zero) + fp16 lo = rn(x - hi): ~22 significant bits.
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = pkrtz(a, b);
+    lo = pkrtz(a - lo_f32(hi), b - hi_f32(hi));
+}
+
+// The 16-bit half of dword `S[a/2]` holding element a, paired with element b
+// (a -> low half, b -> high half), for compile-time a, b.
+__device__ __forceinline__ uint32_t half_pair(const uint32_t (&S)[4], int a, int b) {
+    if (a / 2 == b / 2 && (a & 1) == 0 && (b & 1) == 1) return S[a / 2];
+    const uint32_t s0 = (a & 1) ? 0x0302u : 0x0100u;
+    const uint32_t s1 = (b & 1) ? 0x0706u : 0x0504u;
+    return perm(S[b / 2], S[a / 2], s0 | (s1 << 16));
 }
 
 // ---------------------------------------------------------------------------
-// Channel order of the MFMA contraction.  A lane owns a 32-channel chunk of
-// one token (chunk = lane / 16); its codes are unpacked into 16 dwords
-// D[j] = code(lo_j) | code(hi_j) << 16 (two fp16 subnormals), pair j covering
-// local channels (j, j+16) -- or (j+16, j) for j = 6..9 at 3 bits, where that
-// order is the cheaper one to extract.  K-step kk feeds D[4kk .. 4kk+3].
+// Code layouts.  A lane's B operand for one MFMA K-step is 8 codes as fp16
+// halves e = 0..7 (dword e/2, half e%2).
+//
+// K side: the lane owns one token and a 32-channel chunk; K-step kk takes the
+// chunk's channels 8kk .. 8kk+7 (3 bytes at 3 bits), element e = channel
+// chE[e], its code left at bit kE[e] of the half (value z * 2^(kE-24)).
+// V side: the lane owns channels 8*row .. 8*row+7 of 16 tokens; tile m is
+// channel 8*row + m, its code at bit kV[m] of every half.
 // ---------------------------------------------------------------------------
-template <int BITS>
-__host__ __device__ constexpr bool pair_reversed(int j) { return BITS == 3 && j >= 6 && j <= 9; }
-template <int BITS>
-__host__ __device__ constexpr int pi_channel(int kk, int e) {   // local channel of fragment element e
-    const int j = 4 * kk + e / 2;
-    const bool second = (e & 1) != pair_reversed<BITS>(j);
-    return second ? j + 16 : j;
-}
+template <int BITS> struct Layout;
+template <> struct Layout<3> {
+    static constexpr int chE[8] = {0, 3, 1, 4, 2, 5, 6, 7};
+    static constexpr int kE[8] = {0, 1, 3, 4, 6, 7, 2, 5};
+    static constexpr int kV[8] = {0, 3, 6, 1, 4, 7, 2, 5};
+};
+template <> struct Layout<5> {
+    static constexpr int chE[8] = {0, 1, 2, 3, 4, 5, 6, 7};
+    static constexpr int kE[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    static constexpr int kV[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+};
 
-__device__ __forceinline__ uint32_t bfi16(uint32_t lo_src, uint32_t hi_src) {   // low half of a, high half of b
-    return (lo_src & 0xffffu) | (hi_src & 0xffff0000u);
+// 3-bit K chunk (u0, u1, u2 = 12 bytes, 32 codes) -> 4 K-step B operands.
+// Group kk spans bytes g0 g1 g2 = 3kk .. 3kk+2.  P = (g0 g1 | g1 g2) holds the
+// 16-bit windows starting at g0 and g1; Q = (g2 | g2).  Every code then sits
+// at bit 0..7 of one window and is isolated by a single AND.
+__device__ __forceinline__ void kgroup3(uint32_t P, uint32_t Q, u32x4 &B) {
+    B[0] = P & 0x000E0007u;   // ch0 @0 | ch3 @1
+    B[1] = P & 0x00700038u;   // ch1 @3 | ch4 @4
+    B[2] = P & 0x038001C0u;   // ch2 @6 | ch5 @7
+    B[3] = Q & 0x00E0001Cu;   // ch6 @2 | ch7 @5
 }
-__device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t s) {
-    return __builtin_amdgcn_alignbit(hi, lo, s);
+__device__ __forceinline__ void kunpack(const uint32_t (&u)[3], u32x4 (&B)[4]) {
+    kgroup3(perm(u[0], u[0], 0x02010100u), perm(u[0], u[0], 0x0C020C02u), B[0]);
+    kgroup3(perm(u[1], u[0], 0x05040403u), perm(u[1], u[0], 0x0C050C05u), B[1]);
+    kgroup3(perm(u[2], u[1], 0x04030302u), perm(u[2], u[1], 0x0C040C04u), B[2]);
+    kgroup3(perm(u[2], u[2], 0x03020201u), perm(u[2], u[2], 0x0C030C03u), B[3]);
 }
-
-// 3-bit chunk: 96 bits (u0, u1, u2), code j at bits 3j .. 3j+2.
-__device__ __forceinline__ void unpack3(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t (&D)[16]) {
-    constexpr uint32_t M = 0x00070007u;
-    const uint32_t x = bfi16(u0, u1);
-    D[0] = x & M;
-    D[1] = (x >> 3) & M;
-    D[2] = (x >> 6) & M;
-    D[3] = (x >> 9) & M;
-    D[4] = (x >> 12) & M;
-    D[5] = ((u0 >> 15) & 7u) | ((alignbit(u2, u1, 31) & 7u) << 16);
-    const uint32_t y = bfi16(u2, u0);
-    D[6] = (y >> 2) & M;
-    D[7] = (y >> 5) & M;
-    D[8] = (y >> 8) & M;
-    D[9] = (y >> 11) & M;
-    D[10] = (alignbit(u1, u0, 30) & 7u) | (((u2 >> 14) & 7u) << 16);
-    const uint32_t z = bfi16(u1, u2);
-    D[11] = (z >> 1) & M;
-    D[12] = (z >> 4) & M;
-    D[13] = (z >> 7) & M;
-    D[14] = (z >> 10) & M;
-    D[15] = (z >> 13) & M;
-}
-
-// Generic chunk of 32 codes at BITS bits (BITS dwords).
+// Generic width: code j of the chunk at bits [j*BITS, +BITS) of u[].
 template <int BITS>
 __device__ __forceinline__ uint32_t code_at(const uint32_t (&u)[BITS], int i) {
     const int pos = i * BITS, w = pos >> 5, sh = pos & 31;
     uint32_t v;
     if (sh + BITS <= 32) v = u[w] >> sh;
-    else v = alignbit(u[w + 1], u[w], sh);
+    else v = __builtin_amdgcn_alignbit(u[w + 1], u[w], sh);
     return v & ((1u << BITS) - 1u);
 }
-
-template <int BITS>
-__device__ __forceinline__ void unpack_chunk(const uint32_t (&u)[BITS], uint32_t (&D)[16]) {
-    if constexpr (BITS == 3) {
-        unpack3(u[0], u[1], u[2], D);
-    } else {
+__device__ __forceinline__ void kunpack(const uint32_t (&u)[5], u32x4 (&B)[4]) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int a = pair_reversed<BITS>(j) ? j + 16 : j, b = pair_reversed<BITS>(j) ? j : j + 16;
-            D[j] = code_at<BITS>(u, a) | (code_at<BITS>(u, b) << 16);
-        }
-    }
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            B[kk][i] = code_at<5>(u, 8 * kk + 2 * i) | (code_at<5>(u, 8 * kk + 2 * i + 1) << 16);
 }
 
-// Dense fp16 chunk (32 halves in natural order, as 16 dwords) -> pair order.
-template <int BITS>
-__device__ __forceinline__ void pair_dense(const uint32_t (&h)[16], uint32_t (&D)[16]) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int a = pair_reversed<BITS>(j) ? j + 16 : j, b = pair_reversed<BITS>(j) ? j : j + 16;
-        const uint32_t ha = (a & 1) ? (h[a >> 1] >> 16) : (h[a >> 1] & 0xffffu);
-        const uint32_t hb = (b & 1) ? (h[b >> 1] & 0xffff0000u) : (h[b >> 1] << 16);
-        D[j] = ha | hb;
-    }
+// V: 16 token words w[t] (the lane's BITS*8 code bits of token t, aligned to
+// bit 0; w1 = bits 32..63) -> per tile m, per token pair k: code(2k) | code(2k+1) << 16.
+__device__ __forceinline__ void vpair3(uint32_t wa, uint32_t wb, uint32_t (&D)[8]) {
+    const uint32_t X = perm(wb, wa, 0x05040100u), Y = perm(wb, wa, 0x06050201u), Z = perm(wb, wa, 0x0C060C02u);
+    D[0] = X & 0x00070007u;
+    D[1] = X & 0x00380038u;
+    D[2] = X & 0x01C001C0u;
+    D[3] = Y & 0x000E000Eu;
+    D[4] = Y & 0x00700070u;
+    D[5] = Y & 0x03800380u;
+    D[6] = Z & 0x001C001Cu;
+    D[7] = Z & 0x00E000E0u;
+}
+__device__ __forceinline__ uint32_t vcode5(uint32_t w0, uint32_t w1, int m) {
+    if (m < 6) return __builtin_amdgcn_ubfe(w0, 5 * m, 5);
+    if (m == 6) return __builtin_amdgcn_alignbit(w1, w0, 30) & 31u;
+    return (w1 >> 3) & 31u;
 }
 
 template <int QDT>
@@ -204,77 +211,69 @@ __device__ __forceinline__ float red16_sum(float x) {
 // global loads stay in flight.
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Load the lane's 32-channel fp16 chunk of one dense token (64 bytes).
-__device__ __forceinline__ void load_dense_chunk(const uint16_t *row, int grp, uint32_t (&h)[16]) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(row + 32 * grp);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint4 v = src[k];
-        h[4 * k] = v.x; h[4 * k + 1] = v.y; h[4 * k + 2] = v.z; h[4 * k + 3] = v.w;
-    }
+__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ uint2 ld8_a4(const uint32_t *p) {   // 8 bytes at a 4-byte aligned address
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
 }
 
 // K-side data of a packed block (needed first; issued one block ahead).
 template <int BITS>
 struct KLoads {
-    uint32_t kc[4][BITS];   // K codes: token 16*nt + row, chunk grp
-    uint2 ks[2], km[2];     // K scale / min at the coefficient-prep channels (two runs of 4)
-    float fk[4];            // K decode factors at tokens 16*nt + row
+    uint32_t kc[4][BITS];   // codes: token 16*nt + row, chunk grp
+    uint4 ks, km;           // scale / min at the coefficient-prep channels (8 fp16 each)
+    float fk[4];            // decode factors at tokens 16*nt + row
 };
-// V-side data (needed after the scores; issued when the block starts).
+// V-side data (issued when the block starts).
 template <int BITS>
 struct VLoads {
-    uint32_t vc[4][BITS];   // V codes
-    float fv[4];            // V decode factors
-    uint32_t vsm[8];        // V scale | min << 16 at the output channels cch[n2]
+    uint2 vc[2][8];         // code dword pairs: token 32*kk2 + 8*grp + e, channels 8*row ..
+    uint4 vs, vm;           // scale / min at channels 8*row .. 8*row+7
+    float fv[4];            // decode factors at tokens 16*nt + row
 };
 
 template <int BITS>
-__device__ __forceinline__ void issue_k_loads(const FastParams &p, int64_t ibk, int row, int grp, int wch,
+__device__ __forceinline__ void issue_k_loads(const FastParams &p, int64_t ibk, int row, int grp, int pch,
                                               KLoads<BITS> &f) {
     constexpr int NB = packed_block_bytes(BITS);
-    {
-        const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.k.codes + ibk * NB);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-            for (int w = 0; w < BITS; ++w) f.kc[nt][w] = cb[(16 * nt + row) * (4 * BITS) + grp * BITS + w];
-        const uint16_t *sb = p.k.scales + ibk * kDim + wch;
-        const uint16_t *mb = p.k.mins + ibk * kDim + wch;
-        f.ks[0] = *reinterpret_cast<const uint2 *>(sb);
-        f.ks[1] = *reinterpret_cast<const uint2 *>(sb + 16);
-        f.km[0] = *reinterpret_cast<const uint2 *>(mb);
-        f.km[1] = *reinterpret_cast<const uint2 *>(mb + 16);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) f.fk[nt] = p.k.factors[ibk * kBlockTok + 16 * nt + row];
-    }
-}
-
-template <int BITS>
-__device__ __forceinline__ void issue_v_loads(const FastParams &p, int64_t ibv, int row, int grp, const int (&cch)[8],
-                                              VLoads<BITS> &f) {
-    constexpr int NB = packed_block_bytes(BITS);
-    const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.v.codes + ibv * NB);
+    const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.k.codes + ibk * NB);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int w = 0; w < BITS; ++w) f.vc[nt][w] = cb[(16 * nt + row) * (4 * BITS) + grp * BITS + w];
+        for (int w = 0; w < BITS; ++w) f.kc[nt][w] = cb[(16 * nt + row) * (4 * BITS) + grp * BITS + w];
+    f.ks = ld16(p.k.scales + ibk * kDim + pch);
+    f.km = ld16(p.k.mins + ibk * kDim + pch);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) f.fk[nt] = p.k.factors[ibk * kBlockTok + 16 * nt + row];
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_v_loads(const FastParams &p, int64_t ibv, int row, int grp, int vdw,
+                                              VLoads<BITS> &f) {
+    constexpr int NB = packed_block_bytes(BITS);
+    const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.v.codes + ibv * NB) + vdw;
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; ++kk2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f.vc[kk2][e] = ld8_a4(cb + (32 * kk2 + 8 * grp + e) * (4 * BITS));
+    f.vs = ld16(p.v.scales + ibv * kDim + 8 * row);
+    f.vm = ld16(p.v.mins + ibv * kDim + 8 * row);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) f.fv[nt] = p.v.factors[ibv * kBlockTok + 16 * nt + row];
-#pragma unroll
-    for (int n2 = 0; n2 < 8; ++n2)
-        f.vsm[n2] = static_cast<uint32_t>(p.v.scales[ibv * kDim + cch[n2]]) |
-                    (static_cast<uint32_t>(p.v.mins[ibv * kDim + cch[n2]]) << 16);
 }
 
 template <int BITS, int QDT, bool SCORES, int GRP>
-__global__ __launch_bounds__(64) void attn_fast_kernel(FastParams p) {
-    constexpr int NJ = GRP > 4 ? 2 : 1;  // coefficient-prep heads per lane (GRP >= group)
-    const int G = p.group;                 // query heads per kv-head
-    // A-operand fragments: [set 0 = packed coefficients (q.s), set 1 = dense (q)][row][chunk][kstep]
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
+    using LY = Layout<BITS>;
+    constexpr int NJ = GRP > 4 ? 2 : 1;   // query heads per 16-lane row (head grp + 4j)
+    const int G = p.group;                // query heads per kv-head (<= GRP)
+    // A operands.  K side: row 4*(h%4) + 2*(h/4) + part holds head h's hi (part 0)
+    // or lo (part 1) coefficients; set 0 = packed-K coefficients (rebuilt per
+    // block), set 1 = the dense query (tails).  [row][chunk][kstep].
     __shared__ u32x4 afrag_s[2][16][4][4];
-    __shared__ float pbuf[kMaxGroup][kBlockTok];
-    __shared__ float qm_s[kMaxGroup];
+    // P' rows of the PV product (same row map as the K side: hi, lo), fp16 per token.
+    __shared__ uint32_t pbuf[16][32];
 
     const int l = threadIdx.x;
     const int row = l & 15, grp = l >> 4;
@@ -284,65 +283,89 @@ __global__ __launch_bounds__(64) void attn_fast_kernel(FastParams p) {
     const int64_t t_begin = static_cast<int64_t>(split) * p.split_tokens;
     const int64_t t_end = t_begin + p.split_tokens < T ? t_begin + p.split_tokens : T;
     const int64_t hq0 = static_cast<int64_t>(kvh) * G;
-    const float sc2 = p.scale * kLog2e;
 
-    // coefficient-prep role: head (l>>4) [+4], chunk (l>>2)&3, kstep l&3 -> 8 channels
+    // unused A rows stay zero
+#pragma unroll
+    for (int i = 0; i < 8; ++i) reinterpret_cast<u32x4 *>(&afrag_s[0][0][0][0])[l + 64 * i] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) reinterpret_cast<u32x4 *>(&pbuf[0][0])[l + 64 * i] = u32x4{0u, 0u, 0u, 0u};
+    lds_sync();
+
+    // ---- query preparation.  Prep role of lane l: head grp + 4j, channels
+    // pch .. pch+7 with pch = 32*wgq + 8*wkk (chunk wgq, K-step wkk).
     const int wgq = (l >> 2) & 3, wkk = l & 3;
-    const int wch = 32 * wgq + 4 * wkk;      // first channel of the lane's two runs of 4
-    float qv[NJ][8];
+    const int pch = 32 * wgq + 8 * wkk;
+    float c1[NJ];                 // score scale: scale * log2(e) * 2^-sigma_h
+    uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): for q.m
+    uint32_t qkh[NJ][4], qkl[NJ][4];   // the same * 2^-kE: the coefficient rows
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int h = grp + 4 * j;
+        const bool valid = h < G;
+        float qv[8];
+        float mx = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            qv[j][e] = (h < G) ? load_q<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + 32 * wgq +
-                                                       pi_channel<BITS>(wkk, e))
-                               : 0.f;
-    }
+        for (int c = 0; c < 8; ++c) {
+            qv[c] = valid ? load_q<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + pch + c) : 0.f;
+            mx = fmaxf(mx, fabsf(qv[c]));
+        }
+        mx = red16_max(mx);
+        // sigma: max|q| * 2^sigma in [2^13, 2^14), so every coefficient |q s| < 2^14 * 2/7 stays fp16
+        int e2 = 0;
+        (void)frexpf(mx, &e2);
+        int sigma = (mx > 0.f && finite(mx)) ? 14 - e2 : 0;
+        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+        const float pw = ldexpf(1.f, sigma);
+        c1[j] = p.scale * kLog2e * ldexpf(1.f, -sigma);
+        float qs[8];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int h = grp + 4 * j;
-        if (h < G) {
-            u32x4 hi, lo;
-            split_hilo(qv[j], hi, lo);
-            afrag_s[1][2 * h][wgq][wkk] = hi;
-            afrag_s[1][2 * h + 1][wgq][wkk] = lo;
+        for (int c = 0; c < 8; ++c) qs[c] = qv[c] * pw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ca = LY::chE[2 * i], cb = LY::chE[2 * i + 1];
+            split2(qs[ca], qs[cb], quh[j][i], qul[j][i]);
+            split2(ldexpf(qs[ca], -LY::kE[2 * i]), ldexpf(qs[cb], -LY::kE[2 * i + 1]), qkh[j][i], qkl[j][i]);
+        }
+        if (valid) {
+            u32x4 dh, dl;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t hh, ll;
+                split2(qs[2 * i], qs[2 * i + 1], hh, ll);
+                dh[i] = hh;
+                dl[i] = ll;
+            }
+            const int r0 = 4 * (h & 3) + 2 * (h >> 2);
+            afrag_s[1][r0][wgq][wkk] = dh;
+            afrag_s[1][r0 + 1][wgq][wkk] = dl;
         }
     }
-    // identity fragments for the token<->channel transposition: B[k=8*grp+e][j=row] = 1
-    // iff grp == row/4 and e == 2*(row%4) + b  (b = 0, 1)
-    u32x4 ident[2];
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const bool on = (grp == (row >> 2)) && (k == (row & 3));
-            ident[bb][k] = on ? (bb ? 0x3c000000u : 0x00003c00u) : 0u;
-        }
-    }
-    // channel of PV output column `row` in N-tile n2 (kk = n2/2, half = n2%2)
-    int cch[8];
-#pragma unroll
-    for (int n2 = 0; n2 < 8; ++n2) cch[n2] = 32 * (row >> 2) + pi_channel<BITS>(n2 >> 1, 2 * (row & 3) + (n2 & 1));
 
-    // per-lane output heads (rows 4*grp .. 4*grp+3 = hA hi, hA lo, hB hi, hB lo)
-    const int hA = 2 * grp, hB = 2 * grp + 1;
-    const bool vA = hA < G, vB = hB < G;
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-    float acc[2][8];
+    // V lane constants: the lane's code bytes BITS*row .. of a token row, read
+    // as a dword pair starting at dword vdw, shifted right by vsh bits.
+    constexpr int VROW_DW = 4 * BITS;
+    const int vbyte = BITS * row;
+    const int vdw = (vbyte >> 2) < VROW_DW - 2 ? (vbyte >> 2) : VROW_DW - 2;
+    const uint32_t vsh = 8u * static_cast<uint32_t>(vbyte - 4 * vdw);
+
+    float m_run[NJ], l_run[NJ], acc[NJ][8];
 #pragma unroll
-    for (int n2 = 0; n2 < 8; ++n2) acc[0][n2] = acc[1][n2] = 0.f;
+    for (int j = 0; j < NJ; ++j) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[j][m] = 0.f;
+    }
     bool bad = false;
 
     const int64_t nbk = (!SCORES && p.k.blocks) ? p.k.blocks[b] : 0;
     const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
     const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
     lds_sync();
 
     KLoads<BITS> cur;
     if (!SCORES && t_begin < t_end && t_begin < nbk * kBlockTok)
-        issue_k_loads<BITS>(p, seqrow * p.k.block_cap + t_begin / kBlockTok, row, grp, wch, cur);
+        issue_k_loads<BITS>(p, seqrow * p.k.block_cap + t_begin / kBlockTok, row, grp, pch, cur);
 
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kBlockTok) {
         const int valid = static_cast<int>(t_end - t0 < kBlockTok ? t_end - t0 : kBlockTok);
@@ -352,244 +375,252 @@ __global__ __launch_bounds__(64) void attn_fast_kernel(FastParams p) {
         const int64_t ibv = seqrow * p.v.block_cap + t0 / kBlockTok;
         // ---- this block's V loads, then the next block's K loads, before any compute
         VLoads<BITS> vl;
-        if (vpacked) issue_v_loads<BITS>(p, ibv, row, grp, cch, vl);
+        if (vpacked) issue_v_loads<BITS>(p, ibv, row, grp, vdw, vl);
         KLoads<BITS> nxt;
         const int64_t t1 = t0 + kBlockTok;
-        if (!SCORES && t1 < t_end && t1 < nbk * kBlockTok) issue_k_loads<BITS>(p, ibk + 1, row, grp, wch, nxt);
-        float s[2][4];   // scores (log2 domain) for heads hA, hB at tokens 16*nt + row
+        if (!SCORES && t1 < t_end && t1 < nbk * kBlockTok) issue_k_loads<BITS>(p, ibk + 1, row, grp, pch, nxt);
+        float s[NJ][4];   // scores (log2 domain) of head grp + 4j at tokens 16*nt + row
 
         // ------------------------------------------------------------ scores
         if constexpr (SCORES) {
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const int tt = 16 * nt + row;
-                const bool ok = tt < valid;
-                const float *sa = p.scores + (static_cast<int64_t>(b) * p.heads_q + hq0) * p.scores_cap + t0 + tt;
-                s[0][nt] = (ok && vA) ? sa[hA * p.scores_cap] * kLog2e : -INFINITY;
-                s[1][nt] = (ok && vB) ? sa[hB * p.scores_cap] * kLog2e : -INFINITY;
+            for (int j = 0; j < NJ; ++j) {
+                const int h = grp + 4 * j;
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    const int tt = 16 * nt + row;
+                    s[j][nt] = (tt < valid && h < G)
+                                   ? p.scores[(static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.scores_cap + t0 + tt] * kLog2e
+                                   : -INFINITY;
+                }
             }
         } else {
             u32x4 af[4];
             f32x4 C[4];
             if (kpacked) {
-                // coefficient rows W = q (.) s_K (fp16 hi, lo) and q.m_K for head grp (+4)
-                float sv[8], mv[8];
-                {
-                    const uint32_t sw[4] = {cur.ks[0].x, cur.ks[0].y, cur.ks[1].x, cur.ks[1].y};
-                    const uint32_t mw[4] = {cur.km[0].x, cur.km[0].y, cur.km[1].x, cur.km[1].y};
-                    float sa_[4], sb_[4], ma_[4], mb_[4];
+                // coefficient rows W = q (.) s_K * 2^-kE (fp16 hi + lo) and q.m_K for head grp + 4j
+                const uint32_t S[4] = {cur.ks.x, cur.ks.y, cur.ks.z, cur.ks.w};
+                const uint32_t M[4] = {cur.km.x, cur.km.y, cur.km.z, cur.km.w};
+                uint32_t s2[4], m2[4];
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        sa_[2 * i] = lo_f32(sw[i]); sa_[2 * i + 1] = hi_f32(sw[i]);
-                        sb_[2 * i] = lo_f32(sw[2 + i]); sb_[2 * i + 1] = hi_f32(sw[2 + i]);
-                        ma_[2 * i] = lo_f32(mw[i]); ma_[2 * i + 1] = hi_f32(mw[i]);
-                        mb_[2 * i] = lo_f32(mw[2 + i]); mb_[2 * i + 1] = hi_f32(mw[2 + i]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool rev = pair_reversed<BITS>(4 * wkk + i);
-                        sv[2 * i] = rev ? sb_[i] : sa_[i];
-                        sv[2 * i + 1] = rev ? sa_[i] : sb_[i];
-                        mv[2 * i] = rev ? mb_[i] : ma_[i];
-                        mv[2 * i + 1] = rev ? ma_[i] : mb_[i];
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    s2[i] = half_pair(S, LY::chE[2 * i], LY::chE[2 * i + 1]);
+                    m2[i] = half_pair(M, LY::chE[2 * i], LY::chE[2 * i + 1]);
                 }
+                float qm[NJ];
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    const int h = grp + 4 * j;
-                    float w[8], qm = 0.f;
+                    u32x4 wh, wl;
+                    float d = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        w[e] = qv[j][e] * sv[e];
-                        qm = __builtin_fmaf(qv[j][e], mv[e], qm);
+                    for (int i = 0; i < 4; ++i) {
+                        const half2v sv = as_h2(s2[i]);
+                        const half2v hi = as_h2(qkh[j][i]) * sv;
+                        const half2v er = __builtin_elementwise_fma(as_h2(qkh[j][i]), sv, -hi);
+                        const half2v lo = __builtin_elementwise_fma(as_h2(qkl[j][i]), sv, er);
+                        wh[i] = as_u(hi);
+                        wl[i] = as_u(lo);
+                        d = __builtin_amdgcn_fdot2(as_h2(quh[j][i]), as_h2(m2[i]), d, false);
+                        d = __builtin_amdgcn_fdot2(as_h2(qul[j][i]), as_h2(m2[i]), d, false);
                     }
-                    qm = red16_sum(qm);
-                    if (h < G) {
-                        u32x4 hi, lo;
-                        split_hilo(w, hi, lo);
-                        afrag_s[0][2 * h][wgq][wkk] = hi;
-                        afrag_s[0][2 * h + 1][wgq][wkk] = lo;
-                        if (row == 0) qm_s[h] = qm;
-                    }
+                    qm[j] = red16_sum(d);
+                    const int h = grp + 4 * j;
+                    const int r0 = 4 * (h & 3) + 2 * (h >> 2);
+                    afrag_s[0][r0][wgq][wkk] = wh;
+                    afrag_s[0][r0 + 1][wgq][wkk] = wl;
                 }
                 lds_sync();
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = (row < 2 * G) ? afrag_s[0][row][grp][kk] : zero4;
+                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[0][row][grp][kk];
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
-                    uint32_t D[16];
-                    unpack_chunk<BITS>(cur.kc[nt], D);
+                    u32x4 Bz[4];
+                    kunpack(cur.kc[nt], Bz);
                     C[nt] = zf;
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) {
-                        const u32x4 bz = {D[4 * kk], D[4 * kk + 1], D[4 * kk + 2], D[4 * kk + 3]};
-                        C[nt] = mfma(af[kk], bz, C[nt]);
-                    }
+                    for (int kk = 0; kk < 4; ++kk) C[nt] = mfma(af[kk], Bz[kk], C[nt]);
                 }
-                const float qmA = vA ? qm_s[hA] : 0.f, qmB = vB ? qm_s[hB] : 0.f;
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const float f = cur.fk[nt] * sc2;
-                    s[0][nt] = vA ? (qmA + (C[nt][0] + C[nt][1]) * kTwo24) * f : -INFINITY;
-                    s[1][nt] = vB ? (qmB + (C[nt][2] + C[nt][3]) * kTwo24) * f : -INFINITY;
-                }
+                for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        s[j][nt] = (qm[j] + (C[nt][2 * j] + C[nt][2 * j + 1]) * 16777216.f) * (cur.fk[nt] * c1[j]);
             } else {
-                // dense fp16 keys: tokens t0 - 64*nbk + tt of the tail buffer
+                // dense fp16 keys: tokens t0 - 64*nbk + tt of the tail buffer, channels in natural order
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = (row < 2 * G) ? afrag_s[1][row][grp][kk] : zero4;
+                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[1][row][grp][kk];
                 const int64_t base = t0 - nbk * kBlockTok;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
                     const int tt = 16 * nt + row;
-                    uint32_t h[16], D[16];
-                    if (tt < valid) {
-                        load_dense_chunk(p.k.tail + (seqrow * p.k.tail_cap + base + tt) * kDim, grp, h);
-                    } else {
+                    uint4 v[4];
+                    const uint16_t *src = p.k.tail + (seqrow * p.k.tail_cap + base + tt) * kDim + 32 * grp;
 #pragma unroll
-                        for (int k = 0; k < 16; ++k) h[k] = 0u;
-                    }
-                    pair_dense<BITS>(h, D);
-                    C[nt] = zf;
+                    for (int kk = 0; kk < 4; ++kk) v[kk] = (tt < valid) ? ld16(src + 8 * kk) : uint4{0u, 0u, 0u, 0u};
+                    C[nt] = zf;   // the MFMAs run on the whole wave: out-of-range tokens feed zeros
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) {
-                        const u32x4 bz = {D[4 * kk], D[4 * kk + 1], D[4 * kk + 2], D[4 * kk + 3]};
-                        C[nt] = mfma(af[kk], bz, C[nt]);
-                    }
+                    for (int kk = 0; kk < 4; ++kk) C[nt] = mfma(af[kk], u32x4{v[kk].x, v[kk].y, v[kk].z, v[kk].w}, C[nt]);
                 }
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const bool ok = 16 * nt + row < valid;
-                    s[0][nt] = (vA && ok) ? (C[nt][0] + C[nt][1]) * sc2 : -INFINITY;
-                    s[1][nt] = (vB && ok) ? (C[nt][2] + C[nt][3]) * sc2 : -INFINITY;
-                }
+                for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        s[j][nt] = (16 * nt + row < valid) ? (C[nt][2 * j] + C[nt][2 * j + 1]) * c1[j] : -INFINITY;
             }
         }
 
         // ------------------------------------------------------------ softmax
-        float alpha[2], psum[2];
+        float bm[NJ];
+        bool grow = false;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            float bm = fmaxf(fmaxf(s[hh][0], s[hh][1]), fmaxf(s[hh][2], s[hh][3]));
-            bm = red16_max(bm);
-            const float mnew = fmaxf(m_run[hh], bm);
-            const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
-            alpha[hh] = (m_run[hh] == -INFINITY) ? 0.f : exp2f(m_run[hh] - msafe);
-            float ls = 0.f, ps = 0.f;
+        for (int j = 0; j < NJ; ++j) {
+            bm[j] = red16_max(fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+            grow |= bm[j] > m_run[j];
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const float mnew = fmaxf(m_run[j], bm[j]);
+                const float alpha = (m_run[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[j] - mnew);
+                l_run[j] *= alpha;
+#pragma unroll
+                for (int m = 0; m < 8; ++m) acc[j][m] *= alpha;
+                m_run[j] = mnew;
+            }
+        }
+        // p' = p f_V / F * 2^14 in [0, 2^14]: the scale keeps small weights out
+        // of the fp16 subnormal range (and the fp16 hi/lo split precise)
+        float F = 1.f, rF = kPScale;
+        if (vpacked) {
+            F = red16_max(fmaxf(fmaxf(vl.fv[0], vl.fv[1]), fmaxf(vl.fv[2], vl.fv[3])));
+            F = fmaxf(F, 1e-30f);
+            rF = __builtin_amdgcn_rcpf(F) * kPScale;
+        }
+        float spf[NJ];   // sum_t p f_V (packed V) -- the min term's weight
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const float msafe = (m_run[j] == -INFINITY) ? 0.f : m_run[j];
+            float ls = 0.f, ps = 0.f, pp[4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
-                const float pw = (s[hh][nt] == -INFINITY) ? 0.f : exp2f(s[hh][nt] - msafe);
+                const float pw = __builtin_amdgcn_exp2f(s[j][nt] - msafe);
                 ls += pw;
-                const float pp = vpacked ? pw * vl.fv[nt] : pw;
-                ps += pp;
-                s[hh][nt] = pp;
+                const float pf = vpacked ? pw * vl.fv[nt] : pw;
+                ps += pf;
+                pp[nt] = pf * rF;
             }
-            ls = red16_sum(ls);
-            psum[hh] = red16_sum(ps);
-            l_run[hh] = l_run[hh] * alpha[hh] + ls;
-            m_run[hh] = mnew;
-        }
-        if (vA) {
+            l_run[j] += red16_sum(ls);
+            spf[j] = red16_sum(ps);
+            const int h = grp + 4 * j;
+            // fp16 hi (toward zero) + lo rows: the weights keep ~22 bits
+            const int r0 = 4 * (h & 3) + 2 * (h >> 2);
+            uint16_t *phi = reinterpret_cast<uint16_t *>(&pbuf[r0][0]);
+            uint16_t *plo = reinterpret_cast<uint16_t *>(&pbuf[r0 + 1][0]);
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) pbuf[hA][16 * nt + row] = s[0][nt];
-        }
-        if (vB) {
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) pbuf[hB][16 * nt + row] = s[1][nt];
+            for (int k = 0; k < 2; ++k) {
+                uint32_t hi, lo;
+                split2(pp[2 * k], pp[2 * k + 1], hi, lo);
+                phi[32 * k + row] = static_cast<uint16_t>(hi);
+                phi[32 * k + 16 + row] = static_cast<uint16_t>(hi >> 16);
+                plo[32 * k + row] = static_cast<uint16_t>(lo);
+                plo[32 * k + 16 + row] = static_cast<uint16_t>(lo >> 16);
+            }
         }
         lds_sync();
 
         // ------------------------------------------------------------ P'.V
-        u32x4 pa[2];
-        {
-            const int h = row >> 1, part = row & 1;
-#pragma unroll
-            for (int kk2 = 0; kk2 < 2; ++kk2) {
-                if (h < G) {
-                    const float4 x0 = *reinterpret_cast<const float4 *>(&pbuf[h][32 * kk2 + 4 * grp]);
-                    const float4 x1 = *reinterpret_cast<const float4 *>(&pbuf[h][32 * kk2 + 16 + 4 * grp]);
-                    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                    u32x4 hi, lo;
-                    split_hilo(x, hi, lo);
-                    pa[kk2] = part ? lo : hi;
-                } else {
-                    pa[kk2] = zero4;
-                }
-            }
-        }
         f32x4 O[8];
 #pragma unroll
-        for (int n2 = 0; n2 < 8; ++n2) O[n2] = zf;
+        for (int m = 0; m < 8; ++m) O[m] = zf;
 #pragma unroll
         for (int kk2 = 0; kk2 < 2; ++kk2) {
-            uint32_t Da[16], Db[16];
+            const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
+            const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
+            uint32_t D[8][4];   // [tile m][token pair k]
             if (vpacked) {
-                unpack_chunk<BITS>(vl.vc[2 * kk2], Da);
-                unpack_chunk<BITS>(vl.vc[2 * kk2 + 1], Db);
-            } else {
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int tt = 16 * (2 * kk2 + half) + row;
-                    uint32_t h[16];
-                    if (tt < valid) {
-                        load_dense_chunk(p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok + tt) * kDim, grp, h);
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t wa0, wa1, wb0, wb1;
+                    {
+                        const uint64_t a64 = (static_cast<uint64_t>(vl.vc[kk2][2 * k].y) << 32 | vl.vc[kk2][2 * k].x) >> vsh;
+                        const uint64_t b64 = (static_cast<uint64_t>(vl.vc[kk2][2 * k + 1].y) << 32 | vl.vc[kk2][2 * k + 1].x) >> vsh;
+                        wa0 = static_cast<uint32_t>(a64); wa1 = static_cast<uint32_t>(a64 >> 32);
+                        wb0 = static_cast<uint32_t>(b64); wb1 = static_cast<uint32_t>(b64 >> 32);
+                    }
+                    if constexpr (BITS == 3) {
+                        uint32_t d8[8];
+                        vpair3(wa0, wb0, d8);
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) D[m][k] = d8[m];
                     } else {
 #pragma unroll
-                        for (int k = 0; k < 16; ++k) h[k] = 0u;
+                        for (int m = 0; m < 8; ++m) D[m][k] = vcode5(wa0, wa1, m) | (vcode5(wb0, wb1, m) << 16);
                     }
-                    if (half) pair_dense<BITS>(h, Db);
-                    else pair_dense<BITS>(h, Da);
+                }
+            } else {
+                // dense fp16 V: tokens 32*kk2 + 8*grp + e, channels 8*row .. 8*row+7
+                uint4 x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int tt = 32 * kk2 + 8 * grp + e;
+                    x[e] = (tt < valid)
+                               ? ld16(p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok + tt) * kDim + 8 * row)
+                               : uint4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t xa[4] = {x[2 * k].x, x[2 * k].y, x[2 * k].z, x[2 * k].w};
+                    const uint32_t xb[4] = {x[2 * k + 1].x, x[2 * k + 1].y, x[2 * k + 1].z, x[2 * k + 1].w};
+#pragma unroll
+                    for (int m = 0; m < 8; ++m)
+                        D[m][k] = perm(xb[m >> 1], xa[m >> 1], (m & 1) ? 0x07060302u : 0x05040100u);
                 }
             }
 #pragma unroll
-            for (int n2 = 0; n2 < 8; ++n2) {
-                const int kk = n2 >> 1, bb = n2 & 1;
-                const u32x4 aA = {Da[4 * kk], Da[4 * kk + 1], Da[4 * kk + 2], Da[4 * kk + 3]};
-                const u32x4 aB = {Db[4 * kk], Db[4 * kk + 1], Db[4 * kk + 2], Db[4 * kk + 3]};
-                const f32x4 Ta = mfma(aA, ident[bb], zf);
-                const f32x4 Tb = mfma(aB, ident[bb], zf);
-                const u32x4 bz = {pkrtz(Ta[0], Ta[1]), pkrtz(Ta[2], Ta[3]), pkrtz(Tb[0], Tb[1]), pkrtz(Tb[2], Tb[3])};
-                O[n2] = mfma(pa[kk2], bz, O[n2]);
-            }
+            for (int m = 0; m < 8; ++m) O[m] = mfma(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
         }
         // ------------------------------------------------------------ epilogue
         if (vpacked) {
+            const uint32_t VS[4] = {vl.vs.x, vl.vs.y, vl.vs.z, vl.vs.w};
+            const uint32_t VM[4] = {vl.vm.x, vl.vm.y, vl.vm.z, vl.vm.w};
 #pragma unroll
-            for (int n2 = 0; n2 < 8; ++n2) {
-                const float sc = f16_bits_to_f32(static_cast<uint16_t>(vl.vsm[n2] & 0xffffu)) * kTwo24;
-                const float mc = f16_bits_to_f32(static_cast<uint16_t>(vl.vsm[n2] >> 16));
-                acc[0][n2] = acc[0][n2] * alpha[0] + (sc * (O[n2][0] + O[n2][1]) + mc * psum[0]);
-                acc[1][n2] = acc[1][n2] * alpha[1] + (sc * (O[n2][2] + O[n2][3]) + mc * psum[1]);
+            for (int m = 0; m < 8; ++m) {
+                const float g = F * (static_cast<float>(1u << (24 - LY::kV[m])) / kPScale);
+                const float sc = (m & 1) ? f16hi(VS[m >> 1]) : f16lo(VS[m >> 1]);
+                const float mc = (m & 1) ? f16hi(VM[m >> 1]) : f16lo(VM[m >> 1]);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    float a = __builtin_fmaf(mc, spf[j], acc[j][m]);
+                    acc[j][m] = __builtin_fmaf(sc, (O[m][2 * j] + O[m][2 * j + 1]) * g, a);
+                }
             }
         } else {
 #pragma unroll
-            for (int n2 = 0; n2 < 8; ++n2) {
-                acc[0][n2] = acc[0][n2] * alpha[0] + (O[n2][0] + O[n2][1]);
-                acc[1][n2] = acc[1][n2] * alpha[1] + (O[n2][2] + O[n2][3]);
-            }
+            for (int m = 0; m < 8; ++m)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[j][m] += (O[m][2 * j] + O[m][2 * j + 1]) * (1.f / kPScale);
         }
         cur = nxt;
-        lds_sync();   // pbuf / afrag_s are rewritten by the next block
     }
 
     // ---------------------------------------------------------------- partials
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const int h = hh ? hB : hA;
-        const bool v = hh ? vB : vA;
-        if (!v) continue;
+    for (int j = 0; j < NJ; ++j) {
+        const int h = grp + 4 * j;
+        if (h >= G) continue;
         float *dst = p.partials + ((static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.n_splits + split) * kPartStride;
         if (row == 0) {
-            dst[0] = (m_run[hh] == -INFINITY) ? -INFINITY : m_run[hh] * kLn2;
-            dst[1] = l_run[hh];
+            dst[0] = (m_run[j] == -INFINITY) ? -INFINITY : m_run[j] * kLn2;
+            dst[1] = l_run[j];
             dst[2] = 0.f;
             dst[3] = 0.f;
-            bad |= !finite(l_run[hh]);
+            bad |= !finite(l_run[j]);
         }
+        float4 *o = reinterpret_cast<float4 *>(dst + 4 + 8 * row);
+        o[0] = float4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+        o[1] = float4{acc[j][4], acc[j][5], acc[j][6], acc[j][7]};
 #pragma unroll
-        for (int n2 = 0; n2 < 8; ++n2) {
-            dst[4 + cch[n2]] = acc[hh][n2];
-            bad |= !finite(acc[hh][n2]);
-        }
+        for (int m = 0; m < 8; ++m) bad |= !finite(acc[j][m]);
     }
     if (bad) raise_status(p.status, NSN_ST_NONFINITE_ATTN);
 }
@@ -601,16 +632,20 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     using namespace fast;
     const bool scores = a->k_mode == NSN_KV_SCORES;
     const int64_t G = a->heads_q / a->heads_kv;
-    if (G > kMaxGroup) return NSN_EINVAL;
+    if (G < 1 || G > kMaxGroup) return NSN_EINVAL;
     if (a->bits != 3 && a->bits != 5) return NSN_EINVAL;
     if (a->q_dtype != NSN_DTYPE_BF16 && a->q_dtype != NSN_DTYPE_F16) return NSN_EINVAL;
     auto side_ok = [](const nsn_kv_side &s) {
         if (s.blocks && (!s.codes || !s.mins || !s.scales || !s.factors)) return false;
         if (s.codes && (reinterpret_cast<uintptr_t>(s.codes) & 15u)) return false;
+        if (s.mins && (reinterpret_cast<uintptr_t>(s.mins) & 15u)) return false;
+        if (s.scales && (reinterpret_cast<uintptr_t>(s.scales) & 15u)) return false;
+        if (s.factors && (reinterpret_cast<uintptr_t>(s.factors) & 3u)) return false;
         if (s.tail && (s.tail_dtype != NSN_DTYPE_F16 || (reinterpret_cast<uintptr_t>(s.tail) & 15u))) return false;
         return true;
     };
     if (!side_ok(a->v) || (!scores && !side_ok(a->k))) return NSN_EINVAL;
+    if (a->q && (reinterpret_cast<uintptr_t>(a->q) & 1u)) return NSN_EINVAL;
     FastParams p{};
     p.q = a->q;
     p.heads_q = a->heads_q;
@@ -633,13 +668,10 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(a->n_splits), static_cast<unsigned>(a->heads_kv),
                     static_cast<unsigned>(a->batch));
     const bool bf = a->q_dtype == NSN_DTYPE_BF16;
-    if (G < 1 || G > 8) return NSN_EINVAL;
 #define NSN_FAST_LAUNCH1(B_, Q_, S_, G_) hipLaunchKernelGGL((attn_fast_kernel<B_, Q_, S_, G_>), grid, dim3(64), 0, st, p)
 #define NSN_FAST_LAUNCH(B_, Q_, S_)                                   \
     do {                                                              \
-        if (G == 1) NSN_FAST_LAUNCH1(B_, Q_, S_, 1);                  \
-        else if (G == 2) NSN_FAST_LAUNCH1(B_, Q_, S_, 2);             \
-        else if (G <= 4) NSN_FAST_LAUNCH1(B_, Q_, S_, 4);             \
+        if (G <= 4) NSN_FAST_LAUNCH1(B_, Q_, S_, 4);                  \
         else NSN_FAST_LAUNCH1(B_, Q_, S_, 8);                         \
     } while (0)
     if (a->bits == 3) {

@@ -112,8 +112,13 @@ def test_split_invariance(kernel):
         _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, split_tokens=split, kv_round_dtype=torch.float16,
                                           kernel=kernel)
         outs.append(ctx.cpu().numpy())
+    # The fast kernel's MFMA products carry ~12-19 significant bits relative to
+    # the largest term of each dot product (codes enter as fp16 subnormals),
+    # and the terms change with the split's running max, so two layouts agree
+    # to ~1e-4 there; a merge error would be orders of magnitude larger.
+    atol, rtol = (1e-5, 1e-5) if kernel == "reference" else (2e-4, 2e-3)
     for o in outs[1:]:
-        assert np.allclose(o, outs[0], atol=1e-5, rtol=1e-5)
+        assert np.allclose(o, outs[0], atol=atol, rtol=rtol)
 
 
 def test_gqa_equals_repeated_mha():
