@@ -332,7 +332,7 @@ def main():
     vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
     max_len = max(lengths)
     split, n_splits = kernels.default_split(B, HKV, max_len)
-    ws = torch.empty(B * HQ * n_splits * kernels.PART_STRIDE, dtype=torch.float32, device=dev)
+    ws = torch.empty(kernels.workspace_floats(B, HQ, n_splits), dtype=torch.float32, device=dev)
     out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
     ctx = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
     status = _dev.new_status(dev)

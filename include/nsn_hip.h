@@ -172,9 +172,12 @@ typedef struct {
     int64_t scores_cap;
     int kernel;             /* NSN_ATTN_REFERENCE | NSN_ATTN_FAST */
     int kv_round_dtype;     /* reference kernel: dtype restored K/V are rounded to */
-    int split_tokens;       /* tokens per split (multiple of 64) */
-    int n_splits;           /* ceil(max_seq_len / split_tokens) */
-    float *partials;        /* workspace [B, Hq, n_splits, 132] fp32 */
+    int split_tokens;       /* REFERENCE: tokens per split (multiple of 64) */
+    int n_splits;           /* REFERENCE: ceil(max_seq_len / split_tokens); FAST: partial slots per
+                               (b, hq), >= 2 (the FAST kernel splits the blocks of all sequences
+                               evenly over a fixed grid; max_seq_len bounds the slots it needs) */
+    float *partials;        /* workspace of nsn_attention_workspace_floats() floats: [B, Hq, n_splits, 132]
+                               fp32 partials, then one int32 partial count per (b, hq) */
     float *ctx;             /* [B, Hq, 128] fp32 (nullable) */
     void *out;              /* [B, Hq, 128] out_dtype */
     int out_dtype;
@@ -195,13 +198,15 @@ int nsn_decode_attention(const nsn_attn_args *args, nsn_stream_t stream);
 /*
  * Log-sum-exp merge of the per-split partials written by nsn_decode_attention
  * (with merge == 0): ctx = sum_s u_s e^(m_s - M) / sum_s z_s e^(m_s - M),
- * out = RNE cast of ctx.  Replaces the AF01 merge kernel
+ * out = RNE cast of ctx, over the partial count stored after the partials
+ * (see nsn_attn_args.partials).  Replaces the AF01 merge kernel
  * (experiments/ac08/source/loop_kv_af01_kernel.py:70-82).
  */
 int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, int n_splits, float *ctx,
                         void *out, int out_dtype, int32_t *status, nsn_stream_t stream);
 
-/* Workspace floats needed by nsn_decode_attention for the given shape. */
+/* Workspace floats needed by nsn_decode_attention for the given shape
+ * (partials plus the per-(b, hq) partial counts that nsn_attention_merge reads). */
 int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits);
 
 /*

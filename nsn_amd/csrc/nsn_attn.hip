@@ -38,6 +38,7 @@ struct AttnParams {
     int group;
     float scale;
     const int32_t *seq_len;
+    int64_t batch;
     int split_tokens, n_splits;
     SideParams k, v;
     const float *scores;
@@ -290,7 +291,12 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
         const int h = wave + 4 * k;
         if (h < G) {
             float *dst = p.partials + ((static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.n_splits + split) * kPartStride;
-            if (lane == 0) { dst[0] = run_m[h]; dst[1] = run_l[h]; dst[2] = 0.f; dst[3] = 0.f; }
+            if (lane == 0) {
+                dst[0] = run_m[h]; dst[1] = run_l[h]; dst[2] = 0.f; dst[3] = 0.f;
+                if (split == 0)   // every split writes a slot: the merge reads all n_splits
+                    reinterpret_cast<int32_t *>(p.partials + p.batch * p.heads_q * p.n_splits * kPartStride)
+                        [static_cast<int64_t>(b) * p.heads_q + hq0 + h] = p.n_splits;
+            }
             *reinterpret_cast<float2 *>(dst + 4 + 2 * lane) = make_float2(acc[k][0], acc[k][1]);
             bad_attn |= !finite(acc[k][0]) || !finite(acc[k][1]);
         }
@@ -305,13 +311,17 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
 // splits w, w+4, ... (all its loads in flight together), lane c owns channels
 // 2c, 2c+1; the four wave partials are combined in LDS.
 template <int ODT>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, int n_splits, float *ctx, void *out,
-                                                         int32_t *status) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, const int32_t *counts, int n_splits,
+                                                         float *ctx, void *out, int32_t *status) {
     __shared__ float red_z[4];
     __shared__ float2 red_u[4][64];
     const int64_t bh = blockIdx.x;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const float *base = partials + bh * n_splits * kPartStride;
+    // partial slots written for this (b, hq); clamped so that a stale count stays in bounds
+    int used = counts[bh];
+    used = used < 1 ? 1 : (used > n_splits ? n_splits : used);
+    n_splits = used;
     float L = -INFINITY;
     for (int s = lane; s < n_splits; s += 64) L = fmaxf(L, base[static_cast<int64_t>(s) * kPartStride]);
 #pragma unroll
@@ -398,7 +408,8 @@ int dispatch_q(int qdt, int rdt, int tdt, bool scores, dim3 grid, hipStream_t st
 extern "C" {
 
 int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits) {
-    return batch * heads_q * static_cast<int64_t>(n_splits) * kPartStride;
+    // partials, then one int32 partial count per (b, hq)
+    return batch * heads_q * (static_cast<int64_t>(n_splits) * kPartStride + 1);
 }
 
 int nsn_decode_attention(const nsn_attn_args *a, nsn_stream_t stream) {
@@ -426,6 +437,7 @@ int nsn_decode_attention(const nsn_attn_args *a, nsn_stream_t stream) {
     p.scale = a->scale;
     p.seq_len = a->seq_len;
     p.split_tokens = a->split_tokens;
+    p.batch = a->batch;
     p.n_splits = a->n_splits;
     p.k = to_side(a->k);
     p.v = to_side(a->v);
@@ -460,12 +472,13 @@ int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, i
     if (batch * heads_q > 0x7fffffff) return NSN_EINVAL;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 mgrid(static_cast<unsigned>(batch * heads_q));
+    const int32_t *counts = reinterpret_cast<const int32_t *>(partials + batch * heads_q * n_splits * kPartStride);
     if (out_dtype == NSN_DTYPE_BF16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_BF16>, mgrid, dim3(256), 0, st, partials, counts, n_splits, ctx, out, status);
     else if (out_dtype == NSN_DTYPE_F16)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F16>, mgrid, dim3(256), 0, st, partials, counts, n_splits, ctx, out, status);
     else if (out_dtype == NSN_DTYPE_F32)
-        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(256), 0, st, partials, n_splits, ctx, out, status);
+        hipLaunchKernelGGL(attn_merge_kernel<NSN_DTYPE_F32>, mgrid, dim3(256), 0, st, partials, counts, n_splits, ctx, out, status);
     else
         return NSN_EINVAL;
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;

@@ -171,11 +171,12 @@ struct FastSide {
 
 struct FastParams {
     const void *q;
-    int64_t heads_q, heads_kv;
+    int64_t batch, heads_q, heads_kv;
     int group;
     float scale;
     const int32_t *seq_len;
-    int split_tokens, n_splits;
+    int n_splits;              // partial slots per (sequence, q-head)
+    int64_t min_blocks;        // lower bound of the blocks per wave (keeps every stream within n_splits slots)
     FastSide k, v;
     const float *scores;
     int64_t scores_cap;
@@ -212,11 +213,6 @@ __device__ __forceinline__ float red16_sum(float x) {
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
-__device__ __forceinline__ uint2 ld8_a4(const uint32_t *p) {   // 8 bytes at a 4-byte aligned address
-    uint2 v;
-    __builtin_memcpy(&v, p, 8);
-    return v;
-}
 
 // K-side data of a packed block (needed first; issued one block ahead).
 template <int BITS>
@@ -225,10 +221,8 @@ struct KLoads {
     uint4 ks, km;           // scale / min at the coefficient-prep channels (8 fp16 each)
     float fk[4];            // decode factors at tokens 16*nt + row
 };
-// V-side data (issued when the block starts).
-template <int BITS>
+// V-side metadata (issued one block ahead; the codes go to LDS by DMA).
 struct VLoads {
-    uint2 vc[2][8];         // code dword pairs: token 32*kk2 + 8*grp + e, channels 8*row ..
     uint4 vs, vm;           // scale / min at channels 8*row .. 8*row+7
     float fv[4];            // decode factors at tokens 16*nt + row
 };
@@ -248,48 +242,56 @@ __device__ __forceinline__ void issue_k_loads(const FastParams &p, int64_t ibk, 
     for (int nt = 0; nt < 4; ++nt) f.fk[nt] = p.k.factors[ibk * kBlockTok + 16 * nt + row];
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// V block -> LDS stage: 16 bytes per lane per 1 KiB chunk (global_load_lds_dwordx4,
+// lane l's bytes land at stage + 16*l), plus the metadata into registers.
 template <int BITS>
-__device__ __forceinline__ void issue_v_loads(const FastParams &p, int64_t ibv, int row, int grp, int vdw,
-                                              VLoads<BITS> &f) {
+__device__ __forceinline__ void issue_v_loads(const FastParams &p, int64_t ibv, int row, int l, uint32_t *stage,
+                                              VLoads &f) {
     constexpr int NB = packed_block_bytes(BITS);
-    const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.v.codes + ibv * NB) + vdw;
+    const uint8_t *src = p.v.codes + ibv * NB + 16 * l;
 #pragma unroll
-    for (int kk2 = 0; kk2 < 2; ++kk2)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f.vc[kk2][e] = ld8_a4(cb + (32 * kk2 + 8 * grp + e) * (4 * BITS));
+    for (int c = 0; c < NB / 1024; ++c)
+        __builtin_amdgcn_global_load_lds((const glb_void_t *)(src + 1024 * c), (lds_void_t *)(stage + 256 * c), 16, 0, 0);
     f.vs = ld16(p.v.scales + ibv * kDim + 8 * row);
     f.vm = ld16(p.v.mins + ibv * kDim + 8 * row);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) f.fv[nt] = p.v.factors[ibv * kBlockTok + 16 * nt + row];
 }
 
+template <int BITS> struct Lds {
+    // A operands.  K side: row 4*(h%4) + 2*(h/4) + part holds head h's hi (part 0)
+    // or lo (part 1) coefficients; set 0 = packed-K coefficients (rebuilt per
+    // block), set 1 = the dense query (tails).  Rows are padded (17 x 16 B,
+    // 36 dwords) so that the 16 rows of a fragment read fall on distinct banks.
+    u32x4 afrag[2][16][17];   // [set][row][4*chunk + kstep]
+    // P' rows of the PV product (same row map as the K side: hi, lo), fp16 per token.
+    uint32_t pbuf[16][36];
+    // V code blocks, double-buffered: block i is read from stage i%2 while the
+    // DMA fills the other one with block i+1 (+4 dwords: a lane's last code
+    // window may read past the block's last row).
+    static constexpr int NBW = packed_block_bytes(BITS) / 4 + 4;
+    uint32_t vstage[2][NBW];
+};
+
+// One stream segment: tokens [t_begin, t_end) of (sequence b, kv-head kvh),
+// written as partial slot `slot` of each of the kv-head's G query heads.
 template <int BITS, int QDT, bool SCORES, int GRP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
+__device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int b, int kvh, int64_t t_begin,
+                                        int64_t t_end, int slot, int count) {
     using LY = Layout<BITS>;
     constexpr int NJ = GRP > 4 ? 2 : 1;   // query heads per 16-lane row (head grp + 4j)
     const int G = p.group;                // query heads per kv-head (<= GRP)
-    // A operands.  K side: row 4*(h%4) + 2*(h/4) + part holds head h's hi (part 0)
-    // or lo (part 1) coefficients; set 0 = packed-K coefficients (rebuilt per
-    // block), set 1 = the dense query (tails).  [row][chunk][kstep].
-    __shared__ u32x4 afrag_s[2][16][4][4];
-    // P' rows of the PV product (same row map as the K side: hi, lo), fp16 per token.
-    __shared__ uint32_t pbuf[16][32];
+    auto &afrag_s = sh.afrag;
+    auto &pbuf = sh.pbuf;
+    auto &vstage = sh.vstage;
 
     const int l = threadIdx.x;
     const int row = l & 15, grp = l >> 4;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
-    const int64_t T = p.seq_len[b];
-    const int64_t t_begin = static_cast<int64_t>(split) * p.split_tokens;
-    const int64_t t_end = t_begin + p.split_tokens < T ? t_begin + p.split_tokens : T;
     const int64_t hq0 = static_cast<int64_t>(kvh) * G;
-
-    // unused A rows stay zero
-#pragma unroll
-    for (int i = 0; i < 8; ++i) reinterpret_cast<u32x4 *>(&afrag_s[0][0][0][0])[l + 64 * i] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) reinterpret_cast<u32x4 *>(&pbuf[0][0])[l + 64 * i] = u32x4{0u, 0u, 0u, 0u};
-    lds_sync();
 
     // ---- query preparation.  Prep role of lane l: head grp + 4j, channels
     // pch .. pch+7 with pch = 32*wgq + 8*wkk (chunk wgq, K-step wkk).
@@ -336,17 +338,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
                 dl[i] = ll;
             }
             const int r0 = 4 * (h & 3) + 2 * (h >> 2);
-            afrag_s[1][r0][wgq][wkk] = dh;
-            afrag_s[1][r0 + 1][wgq][wkk] = dl;
+            afrag_s[1][r0][4 * wgq + wkk] = dh;
+            afrag_s[1][r0 + 1][4 * wgq + wkk] = dl;
         }
     }
 
-    // V lane constants: the lane's code bytes BITS*row .. of a token row, read
-    // as a dword pair starting at dword vdw, shifted right by vsh bits.
+    // V lane constants: the lane's code bytes BITS*row .. of a token row start
+    // in dword vdw at bit vsh (a funnel shift of that dword and the next).
     constexpr int VROW_DW = 4 * BITS;
     const int vbyte = BITS * row;
-    const int vdw = (vbyte >> 2) < VROW_DW - 2 ? (vbyte >> 2) : VROW_DW - 2;
-    const uint32_t vsh = 8u * static_cast<uint32_t>(vbyte - 4 * vdw);
+    const int vdw = vbyte >> 2;
+    const uint32_t vsh = 8u * static_cast<uint32_t>(vbyte & 3);
 
     float m_run[NJ], l_run[NJ], acc[NJ][8];
 #pragma unroll
@@ -363,22 +365,32 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
     lds_sync();
 
+    // ---- software pipeline: every load of block i is issued during block i-1
+    // (K codes and all metadata into registers, V codes into an LDS stage) and
+    // waited for with one vmcnt(0) at the top of block i.
     KLoads<BITS> cur;
-    if (!SCORES && t_begin < t_end && t_begin < nbk * kBlockTok)
-        issue_k_loads<BITS>(p, seqrow * p.k.block_cap + t_begin / kBlockTok, row, grp, pch, cur);
+    VLoads vl;
+    if (t_begin < t_end) {
+        if (!SCORES && t_begin < nbk * kBlockTok)
+            issue_k_loads<BITS>(p, seqrow * p.k.block_cap + t_begin / kBlockTok, row, grp, pch, cur);
+        if (t_begin < nbv * kBlockTok)
+            issue_v_loads<BITS>(p, seqrow * p.v.block_cap + t_begin / kBlockTok, row, l, &vstage[0][0], vl);
+    }
 
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBlockTok) {
+    int stage = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBlockTok, stage ^= 1) {
         const int valid = static_cast<int>(t_end - t0 < kBlockTok ? t_end - t0 : kBlockTok);
         const bool kpacked = !SCORES && (t0 < nbk * kBlockTok);
         const bool vpacked = t0 < nbv * kBlockTok;
         const int64_t ibk = seqrow * p.k.block_cap + t0 / kBlockTok;
         const int64_t ibv = seqrow * p.v.block_cap + t0 / kBlockTok;
-        // ---- this block's V loads, then the next block's K loads, before any compute
-        VLoads<BITS> vl;
-        if (vpacked) issue_v_loads<BITS>(p, ibv, row, grp, vdw, vl);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // block i's registers and LDS stage are in
+        // ---- block i+1's loads, before any compute on block i
         KLoads<BITS> nxt;
+        VLoads vnx;
         const int64_t t1 = t0 + kBlockTok;
         if (!SCORES && t1 < t_end && t1 < nbk * kBlockTok) issue_k_loads<BITS>(p, ibk + 1, row, grp, pch, nxt);
+        if (t1 < t_end && t1 < nbv * kBlockTok) issue_v_loads<BITS>(p, ibv + 1, row, l, &vstage[stage ^ 1][0], vnx);
         float s[NJ][4];   // scores (log2 domain) of head grp + 4j at tokens 16*nt + row
 
         // ------------------------------------------------------------ scores
@@ -426,12 +438,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
                     qm[j] = red16_sum(d);
                     const int h = grp + 4 * j;
                     const int r0 = 4 * (h & 3) + 2 * (h >> 2);
-                    afrag_s[0][r0][wgq][wkk] = wh;
-                    afrag_s[0][r0 + 1][wgq][wkk] = wl;
+                    afrag_s[0][r0][4 * wgq + wkk] = wh;
+                    afrag_s[0][r0 + 1][4 * wgq + wkk] = wl;
                 }
                 lds_sync();
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[0][row][grp][kk];
+                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[0][row][4 * grp + kk];
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
                     u32x4 Bz[4];
@@ -448,7 +460,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
             } else {
                 // dense fp16 keys: tokens t0 - 64*nbk + tt of the tail buffer, channels in natural order
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[1][row][grp][kk];
+                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[1][row][4 * grp + kk];
                 const int64_t base = t0 - nbk * kBlockTok;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
@@ -532,32 +544,44 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         f32x4 O[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) O[m] = zf;
+        if (vpacked) {
+            // the lane's 16 token words first (one LDS round trip), then unpack:
+            // w0 = code bits 0..31 of token 32*kk2 + 8*grp + e, w1 = bits 32..63
+            uint32_t w0[16], w1[16];
+            const uint32_t *vs0 = &vstage[stage][8 * grp * VROW_DW + vdw];
 #pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-            const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
-            const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
-            uint32_t D[8][4];   // [tile m][token pair k]
-            if (vpacked) {
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t *vp = vs0 + (32 * (i >> 3) + (i & 7)) * VROW_DW;
+                w0[i] = __builtin_amdgcn_alignbit(vp[1], vp[0], vsh);
+                w1[i] = (BITS == 3) ? 0u : __builtin_amdgcn_alignbit(vp[2], vp[1], vsh);
+            }
+#pragma unroll
+            for (int kk2 = 0; kk2 < 2; ++kk2) {
+                const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
+                const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
+                uint32_t D[8][4];   // [tile m][token pair k]
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    uint32_t wa0, wa1, wb0, wb1;
-                    {
-                        const uint64_t a64 = (static_cast<uint64_t>(vl.vc[kk2][2 * k].y) << 32 | vl.vc[kk2][2 * k].x) >> vsh;
-                        const uint64_t b64 = (static_cast<uint64_t>(vl.vc[kk2][2 * k + 1].y) << 32 | vl.vc[kk2][2 * k + 1].x) >> vsh;
-                        wa0 = static_cast<uint32_t>(a64); wa1 = static_cast<uint32_t>(a64 >> 32);
-                        wb0 = static_cast<uint32_t>(b64); wb1 = static_cast<uint32_t>(b64 >> 32);
-                    }
+                    const int ia = 8 * kk2 + 2 * k, ib = ia + 1;
                     if constexpr (BITS == 3) {
                         uint32_t d8[8];
-                        vpair3(wa0, wb0, d8);
+                        vpair3(w0[ia], w0[ib], d8);
 #pragma unroll
                         for (int m = 0; m < 8; ++m) D[m][k] = d8[m];
                     } else {
 #pragma unroll
-                        for (int m = 0; m < 8; ++m) D[m][k] = vcode5(wa0, wa1, m) | (vcode5(wb0, wb1, m) << 16);
+                        for (int m = 0; m < 8; ++m) D[m][k] = vcode5(w0[ia], w1[ia], m) | (vcode5(w0[ib], w1[ib], m) << 16);
                     }
                 }
-            } else {
+#pragma unroll
+                for (int m = 0; m < 8; ++m) O[m] = mfma(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
+            }
+        } else {
+#pragma unroll
+            for (int kk2 = 0; kk2 < 2; ++kk2) {
+                const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
+                const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
+                uint32_t D[8][4];
                 // dense fp16 V: tokens 32*kk2 + 8*grp + e, channels 8*row .. 8*row+7
                 uint4 x[8];
 #pragma unroll
@@ -575,9 +599,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
                     for (int m = 0; m < 8; ++m)
                         D[m][k] = perm(xb[m >> 1], xa[m >> 1], (m & 1) ? 0x07060302u : 0x05040100u);
                 }
-            }
 #pragma unroll
-            for (int m = 0; m < 8; ++m) O[m] = mfma(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
+                for (int m = 0; m < 8; ++m) O[m] = mfma(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
+            }
         }
         // ------------------------------------------------------------ epilogue
         if (vpacked) {
@@ -601,6 +625,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
                 for (int j = 0; j < NJ; ++j) acc[j][m] += (O[m][2 * j] + O[m][2 * j + 1]) * (1.f / kPScale);
         }
         cur = nxt;
+        vl = vnx;
     }
 
     // ---------------------------------------------------------------- partials
@@ -608,13 +633,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     for (int j = 0; j < NJ; ++j) {
         const int h = grp + 4 * j;
         if (h >= G) continue;
-        float *dst = p.partials + ((static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.n_splits + split) * kPartStride;
+        const int64_t bh = static_cast<int64_t>(b) * p.heads_q + hq0 + h;
+        float *dst = p.partials + (bh * p.n_splits + slot) * kPartStride;
         if (row == 0) {
             dst[0] = (m_run[j] == -INFINITY) ? -INFINITY : m_run[j] * kLn2;
             dst[1] = l_run[j];
             dst[2] = 0.f;
             dst[3] = 0.f;
             bad |= !finite(l_run[j]);
+            // partial count of this (sequence, q-head), read by the merge
+            reinterpret_cast<int32_t *>(p.partials + p.batch * p.heads_q * p.n_splits * kPartStride)[bh] = count;
         }
         float4 *o = reinterpret_cast<float4 *>(dst + 4 + 8 * row);
         o[0] = float4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
@@ -623,6 +651,59 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         for (int m = 0; m < 8; ++m) bad |= !finite(acc[j][m]);
     }
     if (bad) raise_status(p.status, NSN_ST_NONFINITE_ATTN);
+}
+
+// Balanced ("stream-K") partition: the 64-token blocks of all (sequence,
+// kv-head) streams, laid end to end, are split into equal contiguous ranges,
+// one per wave; a range that crosses a stream boundary yields one partial per
+// stream.  Every wave finishes at about the same time whatever the ragged
+// lengths.  Wave w's partial for stream s lands in slot w - first_wave(s).
+template <int BITS, int QDT, bool SCORES, int GRP>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
+    __shared__ Lds<BITS> sh;
+    const int l = threadIdx.x;
+    // unused A rows stay zero
+    for (int i = l; i < 2 * 16 * 17; i += 64) (&sh.afrag[0][0][0])[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = l; i < 16 * 36; i += 64) (&sh.pbuf[0][0])[i] = 0u;
+    lds_sync();
+
+    auto nblk = [&](int b) { return (static_cast<int64_t>(p.seq_len[b]) + kBlockTok - 1) / kBlockTok; };
+    int64_t N = 0;
+    for (int b = 0; b < p.batch; ++b) N += p.heads_kv * nblk(b);
+    const int64_t W = gridDim.x;
+    int64_t P = (N + W - 1) / W;
+    if (P < p.min_blocks) P = p.min_blocks;
+    int64_t g = static_cast<int64_t>(blockIdx.x) * P;
+    const int64_t g1 = (g + P < N) ? g + P : N;
+    if (g >= g1) return;
+    int b = 0;
+    int64_t start_b = 0, nb = nblk(0);
+    while (g >= start_b + p.heads_kv * nb) {
+        start_b += p.heads_kv * nb;
+        nb = nblk(++b);
+    }
+    int kvh = static_cast<int>((g - start_b) / nb);
+    int64_t i0 = g - start_b - kvh * nb;
+    while (g < g1) {
+        const int64_t start_s = start_b + kvh * nb;
+        const int64_t i1 = (i0 + (g1 - g) < nb) ? i0 + (g1 - g) : nb;
+        const int64_t T = p.seq_len[b];
+        const int slot = static_cast<int>(blockIdx.x - start_s / P);
+        const int count = static_cast<int>((start_s + nb - 1) / P - start_s / P + 1);
+        if (slot < p.n_splits && count <= p.n_splits) {
+            segment<BITS, QDT, SCORES, GRP>(p, sh, b, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
+                                            slot, count);
+        } else {
+            raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // workspace too small for this layout
+        }
+        g += i1 - i0;
+        i0 = 0;
+        if (++kvh == p.heads_kv && g < g1) {
+            kvh = 0;
+            start_b += p.heads_kv * nb;
+            nb = nblk(++b);
+        }
+    }
 }
 
 }  // namespace fast
@@ -646,15 +727,19 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     };
     if (!side_ok(a->v) || (!scores && !side_ok(a->k))) return NSN_EINVAL;
     if (a->q && (reinterpret_cast<uintptr_t>(a->q) & 1u)) return NSN_EINVAL;
+    if (a->n_splits < 2 || a->max_seq_len <= 0) return NSN_EINVAL;
     FastParams p{};
     p.q = a->q;
+    p.batch = a->batch;
     p.heads_q = a->heads_q;
     p.heads_kv = a->heads_kv;
     p.group = static_cast<int>(G);
     p.scale = a->scale;
     p.seq_len = a->seq_len;
-    p.split_tokens = a->split_tokens;
     p.n_splits = a->n_splits;
+    // a stream of n blocks touches at most ceil(n / P) + 1 waves
+    const int64_t nb_max = (static_cast<int64_t>(a->max_seq_len) + kBlockTok - 1) / kBlockTok;
+    p.min_blocks = (nb_max + a->n_splits - 2) / (a->n_splits - 1);
     auto side = [](const nsn_kv_side &s) {
         return FastSide{s.codes, s.mins, s.scales, s.factors, s.blocks, s.block_cap,
                         static_cast<const uint16_t *>(s.tail), s.tail_cap};
@@ -665,8 +750,13 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     p.scores_cap = a->scores_cap;
     p.partials = a->partials;
     p.status = a->status;
-    const dim3 grid(static_cast<unsigned>(a->n_splits), static_cast<unsigned>(a->heads_kv),
-                    static_cast<unsigned>(a->batch));
+    // two resident waves per SIMD: one wave per (CU, SIMD, slot)
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NSN_ELAUNCH;
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return NSN_ELAUNCH;
+    const dim3 grid(static_cast<unsigned>(8 * (cus[dev] > 0 ? cus[dev] : 256)));
     const bool bf = a->q_dtype == NSN_DTYPE_BF16;
 #define NSN_FAST_LAUNCH1(B_, Q_, S_, G_) hipLaunchKernelGGL((attn_fast_kernel<B_, Q_, S_, G_>), grid, dim3(64), 0, st, p)
 #define NSN_FAST_LAUNCH(B_, Q_, S_)                                   \

@@ -96,6 +96,12 @@ class PackedKV:
                     and self.tail.shape[3] == DIM, "Tail shape/type")
 
 
+def workspace_floats(batch, heads_q, n_splits):
+    """Workspace of nsn_decode_attention: [B, Hq, n_splits, 132] fp32 partials,
+    then one int32 partial count per (b, hq)."""
+    return batch * heads_q * (n_splits * PART_STRIDE + 1)
+
+
 def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
     """Split the context so that batch*heads_kv*splits covers the 256 CUs several times."""
     want = max(1, math.ceil(target_units / max(1, batch * heads_kv)))
@@ -143,11 +149,15 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
         split_tokens, n_splits = default_split(B, Hkv, max_seq_len)
     else:
         n_splits = max(1, math.ceil(max_seq_len / split_tokens))
+    if kernel == "fast":
+        # the fast kernel balances blocks over a fixed grid; n_splits is its
+        # partial-slot capacity per (b, hq) and must be at least 2
+        n_splits = max(2, n_splits)
     if kv_round_dtype is None:
         tdt = v.tail.dtype if v.tail is not None else torch.bfloat16
         kv_round_dtype = tdt
     dev = q.device
-    need = B * Hq * n_splits * PART_STRIDE
+    need = workspace_floats(B, Hq, n_splits)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.float32, device=dev)
     if out is None:

@@ -42,7 +42,7 @@ def test_library_rejects_bad_arguments_without_gpu_work():
     a = _lib.AttnArgs()
     a.batch, a.heads_q, a.heads_kv, a.bits = 1, 6, 4, 3          # 6 % 4 != 0
     assert lib.nsn_decode_attention(a, None) == _lib.NSN_EINVAL
-    assert lib.nsn_attention_workspace_floats(16, 32, 8) == 16 * 32 * 8 * 132
+    assert lib.nsn_attention_workspace_floats(16, 32, 8) == 16 * 32 * (8 * 132 + 1) == kernels.workspace_floats(16, 32, 8)
     # zero-size work is a no-op
     assert lib.nsn_pack_codes(None, 0, 3, None, None, None) == _lib.NSN_OK
 
