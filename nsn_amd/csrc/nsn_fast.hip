@@ -30,6 +30,8 @@
 // Reference routes replaced: experiments/ac08/source/loop_kv_vf01_kernel.py:56-139
 // (fused readout), experiments/nb06/source/loop_kv_nb06_kernel.py:54-154 (GQA),
 // experiments/ac08/source/loop_kv_af01_kernel.py:13-68 (score-input readout).
+#include <type_traits>
+
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -214,91 +216,129 @@ __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)"
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// K-side data of a packed block (needed first; issued one block ahead).
-template <int BITS>
-struct KLoads {
-    uint32_t kc[4][BITS];   // codes: token 16*nt + row, chunk grp
-    uint4 ks, km;           // scale / min at the coefficient-prep channels (8 fp16 each)
-    float fk[4];            // decode factors at tokens 16*nt + row
-};
-// V-side metadata (issued one block ahead; the codes go to LDS by DMA).
-struct VLoads {
-    uint4 vs, vm;           // scale / min at channels 8*row .. 8*row+7
-    float fv[4];            // decode factors at tokens 16*nt + row
-};
-
-template <int BITS>
-__device__ __forceinline__ void issue_k_loads(const FastParams &p, int64_t ibk, int row, int grp, int pch,
-                                              KLoads<BITS> &f) {
-    constexpr int NB = packed_block_bytes(BITS);
-    const uint32_t *cb = reinterpret_cast<const uint32_t *>(p.k.codes + ibk * NB);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int w = 0; w < BITS; ++w) f.kc[nt][w] = cb[(16 * nt + row) * (4 * BITS) + grp * BITS + w];
-    f.ks = ld16(p.k.scales + ibk * kDim + pch);
-    f.km = ld16(p.k.mins + ibk * kDim + pch);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) f.fk[nt] = p.k.factors[ibk * kBlockTok + 16 * nt + row];
-}
-
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
-// V block -> LDS stage: 16 bytes per lane per 1 KiB chunk (global_load_lds_dwordx4,
-// lane l's bytes land at stage + 16*l), plus the metadata into registers.
-template <int BITS>
-__device__ __forceinline__ void issue_v_loads(const FastParams &p, int64_t ibv, int row, int l, uint32_t *stage,
-                                              VLoads &f) {
-    constexpr int NB = packed_block_bytes(BITS);
-    const uint8_t *src = p.v.codes + ibv * NB + 16 * l;
-#pragma unroll
-    for (int c = 0; c < NB / 1024; ++c)
-        __builtin_amdgcn_global_load_lds((const glb_void_t *)(src + 1024 * c), (lds_void_t *)(stage + 256 * c), 16, 0, 0);
-    f.vs = ld16(p.v.scales + ibv * kDim + 8 * row);
-    f.vm = ld16(p.v.mins + ibv * kDim + 8 * row);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) f.fv[nt] = p.v.factors[ibv * kBlockTok + 16 * nt + row];
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
+// lane l's bytes land at dst + 16*l (dst uniform).  Issued as inline asm so the
+// compiler does not track it: otherwise it waits for every pending DMA before
+// any LDS read (it cannot tell the stages apart), which serialises the
+// prefetch.  The kernel waits for its DMAs itself (vmcnt(0) at the top of each
+// block); an untracked VMEM operation can only make the compiler's own vmcnt
+// waits stricter, never looser.  M0 carries the LDS address.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *src, uint32_t *dst) {
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Per-wave LDS.  Separate objects, so that the compiler can tell the DMA
+// targets of the next block from everything the current block reads (a DMA
+// into one stage then holds back no read of the other stage or of the operand
+// buffers).
+//   afrag  A operands of the K-side MFMA, one 16-byte entry per (row, chunk,
+//          kstep); the entry index is XOR-swizzled by the row so that the rows
+//          of one fragment read fall on different banks.
+//   pbuf   A operands of the PV MFMA: P' rows, fp16 per token, rows padded to
+//          36 dwords.
+//   Both store only the rows in use: the MFMA row of head h, part p (hi = 0,
+//   lo = 1) is 4*(h%4) + 2*(h/4) + p; at most 4 heads per kv-head leave rows
+//   with (row & 2) != 0 empty, read as zeros from a zero entry.
+//   k/v/m  block stages (double-buffered): K codes, V codes (+4 dwords: a
+//          lane's last code window may read past the block's last row) and
+//          metadata: [K scale | K min | K factor | V scale | V min | V factor],
+//          64 dwords each.
+template <int BITS, int GRP> struct LdsShape {
+    static constexpr int ROWS = GRP > 4 ? 16 : 8;
+    static constexpr int NBW = packed_block_bytes(BITS) / 4 + 4;
+    static constexpr int MW = 384;
+};
+template <int BITS, int GRP> struct Lds {
+    using S = LdsShape<BITS, GRP>;
+    u32x4 (&afrag)[S::ROWS * 16 + 1];
+    uint32_t (&pbuf)[S::ROWS * 36 + 4];
+    uint32_t (&k0)[S::NBW];
+    uint32_t (&k1)[S::NBW];
+    uint32_t (&v0)[S::NBW];
+    uint32_t (&v1)[S::NBW];
+    uint32_t (&m0)[S::MW];
+    uint32_t (&m1)[S::MW];
+};
+
+// Compact storage row of MFMA row r (or -1: an empty row, read as zero).
+template <int GRP>
+__device__ __forceinline__ int crow(int r) {
+    if (GRP > 4) return r;
+    return (r & 2) ? -1 : ((r >> 2) << 1) | (r & 1);
 }
 
-template <int BITS> struct Lds {
-    // A operands.  K side: row 4*(h%4) + 2*(h/4) + part holds head h's hi (part 0)
-    // or lo (part 1) coefficients; set 0 = packed-K coefficients (rebuilt per
-    // block), set 1 = the dense query (tails).  Rows are padded (17 x 16 B,
-    // 36 dwords) so that the 16 rows of a fragment read fall on distinct banks.
-    u32x4 afrag[2][16][17];   // [set][row][4*chunk + kstep]
-    // P' rows of the PV product (same row map as the K side: hi, lo), fp16 per token.
-    uint32_t pbuf[16][36];
-    // V code blocks, double-buffered: block i is read from stage i%2 while the
-    // DMA fills the other one with block i+1 (+4 dwords: a lane's last code
-    // window may read past the block's last row).
-    static constexpr int NBW = packed_block_bytes(BITS) / 4 + 4;
-    uint32_t vstage[2][NBW];
-};
+// Issue the DMA of one packed block into a stage: K codes (unless SCORES),
+// V codes, and the metadata of both sides.
+template <int BITS, bool SCORES>
+__device__ __forceinline__ void dma_block(const FastParams &p, int64_t ibk, int64_t ibv, int l, bool kside, bool vside,
+                                          uint32_t *kst, uint32_t *vst, uint32_t *mst) {
+    constexpr int NB = packed_block_bytes(BITS);
+    if (!SCORES && kside) {
+        const uint8_t *kc = p.k.codes + ibk * NB + 16 * l;
+#pragma unroll
+        for (int c = 0; c < NB / 1024; ++c) dma16(kc + 1024 * c, kst + 256 * c);
+    }
+    if (vside) {
+        const uint8_t *vc = p.v.codes + ibv * NB + 16 * l;
+#pragma unroll
+        for (int c = 0; c < NB / 1024; ++c) dma16(vc + 1024 * c, vst + 256 * c);
+    }
+    // metadata: lanes 0-15 K scale, 16-31 K min, 32-47 K factor, 48-63 V scale;
+    // then lanes 0-15 V min, 16-31 V factor
+    const int q = l & 15;
+    const uint16_t *vsc = vside ? p.v.scales + ibv * kDim : nullptr;
+    const void *src;
+    if (!SCORES && kside) {
+        src = (l < 16) ? static_cast<const void *>(p.k.scales + ibk * kDim + 8 * q)
+            : (l < 32) ? static_cast<const void *>(p.k.mins + ibk * kDim + 8 * q)
+            : (l < 48) ? static_cast<const void *>(p.k.factors + ibk * kBlockTok + 4 * q)
+            : vside    ? static_cast<const void *>(vsc + 8 * q)
+                       : static_cast<const void *>(p.k.scales + ibk * kDim + 8 * q);   // (slot not read)
+    } else {
+        src = static_cast<const void *>(vsc + 8 * q);   // (no K metadata: those slots are not read)
+    }
+    if (vside || (!SCORES && kside)) dma16(src, mst);
+    if (vside && l < 32)
+        dma16((l < 16) ? static_cast<const void *>(p.v.mins + ibv * kDim + 8 * q)
+                       : static_cast<const void *>(p.v.factors + ibv * kBlockTok + 4 * q),
+              mst + 256);
+}
 
 // One stream segment: tokens [t_begin, t_end) of (sequence b, kv-head kvh),
 // written as partial slot `slot` of each of the kv-head's G query heads.
 template <int BITS, int QDT, bool SCORES, int GRP>
-__device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int b, int kvh, int64_t t_begin,
-                                        int64_t t_end, int slot, int count) {
+__device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP> &sh, int b, int kvh,
+                                        int64_t t_begin, int64_t t_end, int slot, int count) {
     using LY = Layout<BITS>;
     constexpr int NJ = GRP > 4 ? 2 : 1;   // query heads per 16-lane row (head grp + 4j)
+    constexpr int NB = packed_block_bytes(BITS);
     const int G = p.group;                // query heads per kv-head (<= GRP)
-    auto &afrag_s = sh.afrag;
-    auto &pbuf = sh.pbuf;
-    auto &vstage = sh.vstage;
 
     const int l = threadIdx.x;
     const int row = l & 15, grp = l >> 4;
     const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
     const int64_t hq0 = static_cast<int64_t>(kvh) * G;
 
+    // ---- operand buffer addressing (loop invariant)
+    const int rdrow = crow<GRP>(row);                        // this lane's A row when reading
+    const u32x4 *af_rd = (rdrow < 0) ? &sh.afrag[GRP > 4 ? 16 * 16 : 8 * 16] : &sh.afrag[16 * rdrow];
+    const int af_x = (rdrow < 0) ? -1 : (rdrow & 15);        // swizzle (-1: the zero entry)
+    const uint32_t *pb_rd = (rdrow < 0) ? &sh.pbuf[(GRP > 4 ? 16 : 8) * 36] : &sh.pbuf[36 * rdrow];
+    const int pb_step = (rdrow < 0) ? 0 : 1;
+
     // ---- query preparation.  Prep role of lane l: head grp + 4j, channels
     // pch .. pch+7 with pch = 32*wgq + 8*wkk (chunk wgq, K-step wkk).
     const int wgq = (l >> 2) & 3, wkk = l & 3;
     const int pch = 32 * wgq + 8 * wkk;
-    float c1[NJ];                 // score scale: scale * log2(e) * 2^-sigma_h
-    uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): for q.m
+    float c1[NJ];                      // score scale: scale * log2(e) * 2^-sigma_h
+    uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): q.m and dense keys
     uint32_t qkh[NJ][4], qkl[NJ][4];   // the same * 2^-kE: the coefficient rows
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -328,20 +368,15 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
             split2(qs[ca], qs[cb], quh[j][i], qul[j][i]);
             split2(ldexpf(qs[ca], -LY::kE[2 * i]), ldexpf(qs[cb], -LY::kE[2 * i + 1]), qkh[j][i], qkl[j][i]);
         }
-        if (valid) {
-            u32x4 dh, dl;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t hh, ll;
-                split2(qs[2 * i], qs[2 * i + 1], hh, ll);
-                dh[i] = hh;
-                dl[i] = ll;
-            }
-            const int r0 = 4 * (h & 3) + 2 * (h >> 2);
-            afrag_s[1][r0][4 * wgq + wkk] = dh;
-            afrag_s[1][r0 + 1][4 * wgq + wkk] = dl;
-        }
     }
+    // write the A fragments (hi, lo rows) of head grp + 4j at the prep slot
+    auto put_frag = [&](int j, const u32x4 &hi, const u32x4 &lo) {
+        const int h = grp + 4 * j;
+        const int r0 = crow<GRP>(4 * (h & 3) + 2 * (h >> 2));
+        sh.afrag[16 * r0 + ((4 * wgq + wkk) ^ (r0 & 15))] = hi;
+        sh.afrag[16 * (r0 + 1) + ((4 * wgq + wkk) ^ ((r0 + 1) & 15))] = lo;
+    };
+    auto get_frag = [&](int kk) { return af_x < 0 ? af_rd[0] : af_rd[(4 * grp + kk) ^ af_x]; };
 
     // V lane constants: the lane's code bytes BITS*row .. of a token row start
     // in dword vdw at bit vsh (a funnel shift of that dword and the next).
@@ -363,34 +398,37 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
     const int64_t nbk = (!SCORES && p.k.blocks) ? p.k.blocks[b] : 0;
     const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
     const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
-    lds_sync();
 
-    // ---- software pipeline: every load of block i is issued during block i-1
-    // (K codes and all metadata into registers, V codes into an LDS stage) and
-    // waited for with one vmcnt(0) at the top of block i.
-    KLoads<BITS> cur;
-    VLoads vl;
-    if (t_begin < t_end) {
-        if (!SCORES && t_begin < nbk * kBlockTok)
-            issue_k_loads<BITS>(p, seqrow * p.k.block_cap + t_begin / kBlockTok, row, grp, pch, cur);
-        if (t_begin < nbv * kBlockTok)
-            issue_v_loads<BITS>(p, seqrow * p.v.block_cap + t_begin / kBlockTok, row, l, &vstage[0][0], vl);
-    }
+    // ---- software pipeline over the fully packed blocks [t_begin, t_fast):
+    // all data of block i+1 (codes and metadata of K and V) is moved into the
+    // other LDS stage by DMA while block i is computed, unconditionally --
+    // after the last block the last block is read again -- and waited for with
+    // one vmcnt(0) at the top of block i+1.  No prefetched data lives in
+    // registers, so the compiler never has to wait for it mid-block.  Blocks
+    // past t_fast (fp16 tail, dense K or V) fetch their own data first.
+    const int64_t kend = SCORES ? t_end : nbk * kBlockTok;
+    int64_t t_fast = (kend < nbv * kBlockTok) ? kend : nbv * kBlockTok;
+    t_fast = (t_fast < t_end) ? t_fast : t_end;
 
-    int stage = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBlockTok, stage ^= 1) {
+    auto block = [&](auto fast, auto stage_c, const int64_t t0) {
+        constexpr bool FAST = decltype(fast)::value;
+        constexpr int ST = decltype(stage_c)::value;
+        uint32_t *const kst = ST ? &sh.k1[0] : &sh.k0[0];
+        uint32_t *const vst = ST ? &sh.v1[0] : &sh.v0[0];
+        uint32_t *const mst = ST ? &sh.m1[0] : &sh.m0[0];
         const int valid = static_cast<int>(t_end - t0 < kBlockTok ? t_end - t0 : kBlockTok);
-        const bool kpacked = !SCORES && (t0 < nbk * kBlockTok);
-        const bool vpacked = t0 < nbv * kBlockTok;
-        const int64_t ibk = seqrow * p.k.block_cap + t0 / kBlockTok;
-        const int64_t ibv = seqrow * p.v.block_cap + t0 / kBlockTok;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // block i's registers and LDS stage are in
-        // ---- block i+1's loads, before any compute on block i
-        KLoads<BITS> nxt;
-        VLoads vnx;
-        const int64_t t1 = t0 + kBlockTok;
-        if (!SCORES && t1 < t_end && t1 < nbk * kBlockTok) issue_k_loads<BITS>(p, ibk + 1, row, grp, pch, nxt);
-        if (t1 < t_end && t1 < nbv * kBlockTok) issue_v_loads<BITS>(p, ibv + 1, row, l, &vstage[stage ^ 1][0], vnx);
+        const bool kpacked = FAST ? !SCORES : (!SCORES && (t0 < nbk * kBlockTok));
+        const bool vpacked = FAST ? true : (t0 < nbv * kBlockTok);
+        if (!FAST && (kpacked || vpacked))
+            dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t0 / kBlockTok, seqrow * p.v.block_cap + t0 / kBlockTok,
+                                    l, kpacked, vpacked, kst, vst, mst);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // block i's stage is in
+        if (FAST) {   // ---- block i+1's data, before any compute on block i
+            const int64_t t1 = (t0 + kBlockTok < t_fast) ? t0 + kBlockTok : t0;
+            dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t1 / kBlockTok, seqrow * p.v.block_cap + t1 / kBlockTok,
+                                    l, true, true, ST ? &sh.k0[0] : &sh.k1[0], ST ? &sh.v0[0] : &sh.v1[0],
+                                    ST ? &sh.m0[0] : &sh.m1[0]);
+        }
         float s[NJ][4];   // scores (log2 domain) of head grp + 4j at tokens 16*nt + row
 
         // ------------------------------------------------------------ scores
@@ -411,8 +449,10 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
             f32x4 C[4];
             if (kpacked) {
                 // coefficient rows W = q (.) s_K * 2^-kE (fp16 hi + lo) and q.m_K for head grp + 4j
-                const uint32_t S[4] = {cur.ks.x, cur.ks.y, cur.ks.z, cur.ks.w};
-                const uint32_t M[4] = {cur.km.x, cur.km.y, cur.km.z, cur.km.w};
+                const uint4 ks4 = *reinterpret_cast<const uint4 *>(mst + pch / 2);
+                const uint4 km4 = *reinterpret_cast<const uint4 *>(mst + 64 + pch / 2);
+                const uint32_t S[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+                const uint32_t M[4] = {km4.x, km4.y, km4.z, km4.w};
                 uint32_t s2[4], m2[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -436,18 +476,22 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
                         d = __builtin_amdgcn_fdot2(as_h2(qul[j][i]), as_h2(m2[i]), d, false);
                     }
                     qm[j] = red16_sum(d);
-                    const int h = grp + 4 * j;
-                    const int r0 = 4 * (h & 3) + 2 * (h >> 2);
-                    afrag_s[0][r0][4 * wgq + wkk] = wh;
-                    afrag_s[0][r0 + 1][4 * wgq + wkk] = wl;
+                    put_frag(j, wh, wl);
                 }
+                float fk[4];
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) fk[nt] = __builtin_bit_cast(float, mst[128 + 16 * nt + row]);
                 lds_sync();
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[0][row][4 * grp + kk];
+                for (int kk = 0; kk < 4; ++kk) af[kk] = get_frag(kk);
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
+                    uint32_t u[BITS];
+                    const uint32_t *src = kst + (16 * nt + row) * VROW_DW + BITS * grp;
+#pragma unroll
+                    for (int w = 0; w < BITS; ++w) u[w] = src[w];
                     u32x4 Bz[4];
-                    kunpack(cur.kc[nt], Bz);
+                    kunpack(u, Bz);
                     C[nt] = zf;
 #pragma unroll
                     for (int kk = 0; kk < 4; ++kk) C[nt] = mfma(af[kk], Bz[kk], C[nt]);
@@ -456,22 +500,34 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
                 for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
-                        s[j][nt] = (qm[j] + (C[nt][2 * j] + C[nt][2 * j + 1]) * 16777216.f) * (cur.fk[nt] * c1[j]);
+                        s[j][nt] = (qm[j] + (C[nt][2 * j] + C[nt][2 * j + 1]) * 16777216.f) * (fk[nt] * c1[j]);
             } else {
-                // dense fp16 keys: tokens t0 - 64*nbk + tt of the tail buffer, channels in natural order
+                // dense fp16 keys (tokens t0 - 64*nbk + tt of the tail buffer): the A rows are the
+                // query itself (q * 2^sigma, hi + lo), channels in the same element order
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) af[kk] = afrag_s[1][row][4 * grp + kk];
+                for (int j = 0; j < NJ; ++j)
+                    put_frag(j, u32x4{quh[j][0], quh[j][1], quh[j][2], quh[j][3]},
+                             u32x4{qul[j][0], qul[j][1], qul[j][2], qul[j][3]});
+                lds_sync();
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) af[kk] = get_frag(kk);
                 const int64_t base = t0 - nbk * kBlockTok;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
-                    const int tt = 16 * nt + row;
-                    uint4 v[4];
+                    // tokens past `valid` read the last valid token (in bounds); their
+                    // scores are set to -inf below, so the value never counts
+                    const int tt = (16 * nt + row < valid) ? 16 * nt + row : valid - 1;
                     const uint16_t *src = p.k.tail + (seqrow * p.k.tail_cap + base + tt) * kDim + 32 * grp;
+                    C[nt] = zf;
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) v[kk] = (tt < valid) ? ld16(src + 8 * kk) : uint4{0u, 0u, 0u, 0u};
-                    C[nt] = zf;   // the MFMAs run on the whole wave: out-of-range tokens feed zeros
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const uint4 v = ld16(src + 8 * kk);
+                        const uint32_t X[4] = {v.x, v.y, v.z, v.w};
+                        u32x4 Bd;
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) C[nt] = mfma(af[kk], u32x4{v[kk].x, v[kk].y, v[kk].z, v[kk].w}, C[nt]);
+                        for (int i = 0; i < 4; ++i) Bd[i] = half_pair(X, LY::chE[2 * i], LY::chE[2 * i + 1]);
+                        C[nt] = mfma(af[kk], Bd, C[nt]);
+                    }
                 }
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt)
@@ -486,13 +542,15 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
         bool grow = false;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            bm[j] = red16_max(fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+            bm[j] = fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3]));   // this lane's tokens
             grow |= bm[j] > m_run[j];
         }
+        // the row maximum is only reduced (and the state rescaled) when some
+        // lane's score exceeds the running maximum -- rare after the first blocks
         if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const float mnew = fmaxf(m_run[j], bm[j]);
+                const float mnew = fmaxf(m_run[j], red16_max(bm[j]));
                 const float alpha = (m_run[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[j] - mnew);
                 l_run[j] *= alpha;
 #pragma unroll
@@ -502,9 +560,12 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
         }
         // p' = p f_V / F * 2^14 in [0, 2^14]: the scale keeps small weights out
         // of the fp16 subnormal range (and the fp16 hi/lo split precise)
+        float fv[4];
         float F = 1.f, rF = kPScale;
         if (vpacked) {
-            F = red16_max(fmaxf(fmaxf(vl.fv[0], vl.fv[1]), fmaxf(vl.fv[2], vl.fv[3])));
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) fv[nt] = __builtin_bit_cast(float, mst[320 + 16 * nt + row]);
+            F = red16_max(fmaxf(fmaxf(fv[0], fv[1]), fmaxf(fv[2], fv[3])));
             F = fmaxf(F, 1e-30f);
             rF = __builtin_amdgcn_rcpf(F) * kPScale;
         }
@@ -517,17 +578,17 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
             for (int nt = 0; nt < 4; ++nt) {
                 const float pw = __builtin_amdgcn_exp2f(s[j][nt] - msafe);
                 ls += pw;
-                const float pf = vpacked ? pw * vl.fv[nt] : pw;
+                const float pf = vpacked ? pw * fv[nt] : pw;
                 ps += pf;
                 pp[nt] = pf * rF;
             }
-            l_run[j] += red16_sum(ls);
+            l_run[j] += ls;   // per lane; the row sum is taken once per segment
             spf[j] = red16_sum(ps);
             const int h = grp + 4 * j;
             // fp16 hi (toward zero) + lo rows: the weights keep ~22 bits
-            const int r0 = 4 * (h & 3) + 2 * (h >> 2);
-            uint16_t *phi = reinterpret_cast<uint16_t *>(&pbuf[r0][0]);
-            uint16_t *plo = reinterpret_cast<uint16_t *>(&pbuf[r0 + 1][0]);
+            const int r0 = crow<GRP>(4 * (h & 3) + 2 * (h >> 2));
+            uint16_t *phi = reinterpret_cast<uint16_t *>(&sh.pbuf[36 * r0]);
+            uint16_t *plo = reinterpret_cast<uint16_t *>(&sh.pbuf[36 * (r0 + 1)]);
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 uint32_t hi, lo;
@@ -548,7 +609,7 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
             // the lane's 16 token words first (one LDS round trip), then unpack:
             // w0 = code bits 0..31 of token 32*kk2 + 8*grp + e, w1 = bits 32..63
             uint32_t w0[16], w1[16];
-            const uint32_t *vs0 = &vstage[stage][8 * grp * VROW_DW + vdw];
+            const uint32_t *vs0 = vst + 8 * grp * VROW_DW + vdw;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const uint32_t *vp = vs0 + (32 * (i >> 3) + (i & 7)) * VROW_DW;
@@ -557,7 +618,7 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
             }
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; ++kk2) {
-                const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
+                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (16 * kk2 + 4 * grp));
                 const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
                 uint32_t D[8][4];   // [tile m][token pair k]
 #pragma unroll
@@ -579,22 +640,20 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
         } else {
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; ++kk2) {
-                const uint4 pv = *reinterpret_cast<const uint4 *>(&pbuf[row][16 * kk2 + 4 * grp]);
+                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (16 * kk2 + 4 * grp));
                 const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
                 uint32_t D[8][4];
-                // dense fp16 V: tokens 32*kk2 + 8*grp + e, channels 8*row .. 8*row+7
-                uint4 x[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int tt = 32 * kk2 + 8 * grp + e;
-                    x[e] = (tt < valid)
-                               ? ld16(p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok + tt) * kDim + 8 * row)
-                               : uint4{0u, 0u, 0u, 0u};
-                }
+                // dense fp16 V: tokens 32*kk2 + 8*grp + e, channels 8*row .. 8*row+7.
+                // Tokens past `valid` read the last valid token (in bounds); their
+                // weights are zero.
+                const uint16_t *vrow = p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok) * kDim + 8 * row;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const uint32_t xa[4] = {x[2 * k].x, x[2 * k].y, x[2 * k].z, x[2 * k].w};
-                    const uint32_t xb[4] = {x[2 * k + 1].x, x[2 * k + 1].y, x[2 * k + 1].z, x[2 * k + 1].w};
+                    const int ta = 32 * kk2 + 8 * grp + 2 * k, tb = ta + 1;
+                    const uint4 xa4 = ld16(vrow + (ta < valid ? ta : valid - 1) * kDim);
+                    const uint4 xb4 = ld16(vrow + (tb < valid ? tb : valid - 1) * kDim);
+                    const uint32_t xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
+                    const uint32_t xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
 #pragma unroll
                     for (int m = 0; m < 8; ++m)
                         D[m][k] = perm(xb[m >> 1], xa[m >> 1], (m & 1) ? 0x07060302u : 0x05040100u);
@@ -605,8 +664,10 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
         }
         // ------------------------------------------------------------ epilogue
         if (vpacked) {
-            const uint32_t VS[4] = {vl.vs.x, vl.vs.y, vl.vs.z, vl.vs.w};
-            const uint32_t VM[4] = {vl.vm.x, vl.vm.y, vl.vm.z, vl.vm.w};
+            const uint4 vs4 = *reinterpret_cast<const uint4 *>(mst + 192 + 4 * row);
+            const uint4 vm4 = *reinterpret_cast<const uint4 *>(mst + 256 + 4 * row);
+            const uint32_t VS[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+            const uint32_t VM[4] = {vm4.x, vm4.y, vm4.z, vm4.w};
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
                 const float g = F * (static_cast<float>(1u << (24 - LY::kV[m])) / kPScale);
@@ -624,11 +685,36 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) acc[j][m] += (O[m][2 * j] + O[m][2 * j + 1]) * (1.f / kPScale);
         }
-        cur = nxt;
-        vl = vnx;
+    };
+
+    using F_ = std::false_type;
+    using T_ = std::true_type;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    int64_t t0 = t_begin;
+    int free_stage = 0;   // a stage no DMA writes to once the pipelined loop has ended
+    if (t0 < t_fast) {
+        dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t0 / kBlockTok, seqrow * p.v.block_cap + t0 / kBlockTok, l,
+                                true, true, &sh.k0[0], &sh.v0[0], &sh.m0[0]);
+        for (;;) {
+            block(T_{}, S0{}, t0);
+            t0 += kBlockTok;
+            free_stage = 0;
+            if (t0 >= t_fast) break;
+            block(T_{}, S1{}, t0);
+            t0 += kBlockTok;
+            free_stage = 1;
+            if (t0 >= t_fast) break;
+        }
+    }
+    for (; t0 < t_end; t0 += kBlockTok) {
+        if (free_stage) block(F_{}, S1{}, t0);
+        else block(F_{}, S0{}, t0);
     }
 
     // ---------------------------------------------------------------- partials
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) l_run[j] = red16_sum(l_run[j]);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int h = grp + 4 * j;
@@ -660,11 +746,16 @@ __device__ __forceinline__ void segment(const FastParams &p, Lds<BITS> &sh, int 
 // lengths.  Wave w's partial for stream s lands in slot w - first_wave(s).
 template <int BITS, int QDT, bool SCORES, int GRP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
-    __shared__ Lds<BITS> sh;
+    using S = LdsShape<BITS, GRP>;
+    __shared__ u32x4 s_afrag[S::ROWS * 16 + 1];
+    __shared__ uint32_t s_pbuf[S::ROWS * 36 + 4];
+    __shared__ uint32_t s_k0[S::NBW], s_k1[S::NBW], s_v0[S::NBW], s_v1[S::NBW];
+    __shared__ uint32_t s_m0[S::MW], s_m1[S::MW];
+    const Lds<BITS, GRP> sh{s_afrag, s_pbuf, s_k0, s_k1, s_v0, s_v1, s_m0, s_m1};
     const int l = threadIdx.x;
-    // unused A rows stay zero
-    for (int i = l; i < 2 * 16 * 17; i += 64) (&sh.afrag[0][0][0])[i] = u32x4{0u, 0u, 0u, 0u};
-    for (int i = l; i < 16 * 36; i += 64) (&sh.pbuf[0][0])[i] = 0u;
+    // empty A rows and the zero entries stay zero
+    for (int i = l; i < S::ROWS * 16 + 1; i += 64) s_afrag[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = l; i < S::ROWS * 36 + 4; i += 64) s_pbuf[i] = 0u;
     lds_sync();
 
     auto nblk = [&](int b) { return (static_cast<int64_t>(p.seq_len[b]) + kBlockTok - 1) / kBlockTok; };
@@ -721,7 +812,7 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
         if (s.codes && (reinterpret_cast<uintptr_t>(s.codes) & 15u)) return false;
         if (s.mins && (reinterpret_cast<uintptr_t>(s.mins) & 15u)) return false;
         if (s.scales && (reinterpret_cast<uintptr_t>(s.scales) & 15u)) return false;
-        if (s.factors && (reinterpret_cast<uintptr_t>(s.factors) & 3u)) return false;
+        if (s.factors && (reinterpret_cast<uintptr_t>(s.factors) & 15u)) return false;
         if (s.tail && (s.tail_dtype != NSN_DTYPE_F16 || (reinterpret_cast<uintptr_t>(s.tail) & 15u))) return false;
         return true;
     };
