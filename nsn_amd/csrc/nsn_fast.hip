@@ -208,6 +208,22 @@ __device__ __forceinline__ float red16_sum(float x) {
     return x;
 }
 
+// Wave-wide (64-lane) inclusive prefix sum, and a uniform read of one lane.
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
+    const int l = threadIdx.x;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t y = __shfl_up(static_cast<long long>(x), d);
+        if (l >= d) x += y;
+    }
+    return x;
+}
+__device__ __forceinline__ int64_t lane_get(int64_t x, int lane) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), lane));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x >> 32), lane));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // LDS hand-off inside the single wave of a workgroup: the wave's LDS accesses
 // complete in order, so waiting for them (and stopping the compiler from
 // moving memory accesses across) is enough -- no s_barrier, and prefetched
@@ -313,9 +329,11 @@ __device__ __forceinline__ void dma_block(const FastParams &p, int64_t ibk, int6
 
 // One stream segment: tokens [t_begin, t_end) of (sequence b, kv-head kvh),
 // written as partial slot `slot` of each of the kv-head's G query heads.
+// nbk_b / nbv_b: the sequence's packed K / V block counts (0 without blocks).
 template <int BITS, int QDT, bool SCORES, int GRP>
 __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP> &sh, int b, int kvh,
-                                        int64_t t_begin, int64_t t_end, int slot, int count) {
+                                        int64_t t_begin, int64_t t_end, int64_t nbk_b, int64_t nbv_b, int slot,
+                                        int count) {
     using LY = Layout<BITS>;
     constexpr int NJ = GRP > 4 ? 2 : 1;   // query heads per 16-lane row (head grp + 4j)
     constexpr int NB = packed_block_bytes(BITS);
@@ -325,6 +343,19 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     const int row = l & 15, grp = l >> 4;
     const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
     const int64_t hq0 = static_cast<int64_t>(kvh) * G;
+
+    // ---- the first packed block's DMA goes out before anything else, so its
+    // latency overlaps the query loads and preparation below.  Blocks
+    // [t_begin, t_fast) are fully packed on every side that has blocks.
+    const int64_t nbk = SCORES ? 0 : nbk_b;
+    const int64_t nbv = nbv_b;
+    const int64_t kend = SCORES ? t_end : nbk * kBlockTok;
+    int64_t t_fast = (kend < nbv * kBlockTok) ? kend : nbv * kBlockTok;
+    t_fast = (t_fast < t_end) ? t_fast : t_end;
+    if (t_begin < t_fast)
+        dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t_begin / kBlockTok,
+                                seqrow * p.v.block_cap + t_begin / kBlockTok, l, true, true, &sh.k0[0], &sh.v0[0],
+                                &sh.m0[0]);
 
     // ---- operand buffer addressing (loop invariant)
     const int rdrow = crow<GRP>(row);                        // this lane's A row when reading
@@ -395,20 +426,15 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     }
     bool bad = false;
 
-    const int64_t nbk = (!SCORES && p.k.blocks) ? p.k.blocks[b] : 0;
-    const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
     const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
 
     // ---- software pipeline over the fully packed blocks [t_begin, t_fast):
     // all data of block i+1 (codes and metadata of K and V) is moved into the
-    // other LDS stage by DMA while block i is computed, unconditionally --
-    // after the last block the last block is read again -- and waited for with
+    // other LDS stage by DMA while block i is computed, and waited for with
     // one vmcnt(0) at the top of block i+1.  No prefetched data lives in
-    // registers, so the compiler never has to wait for it mid-block.  Blocks
-    // past t_fast (fp16 tail, dense K or V) fetch their own data first.
-    const int64_t kend = SCORES ? t_end : nbk * kBlockTok;
-    int64_t t_fast = (kend < nbv * kBlockTok) ? kend : nbv * kBlockTok;
-    t_fast = (t_fast < t_end) ? t_fast : t_end;
+    // registers, so the compiler never has to wait for it mid-block, and no
+    // DMA is left in flight when the pipelined loop ends.  Blocks past t_fast
+    // (fp16 tail, dense K or V) fetch their own data first.
 
     auto block = [&](auto fast, auto stage_c, const int64_t t0) {
         constexpr bool FAST = decltype(fast)::value;
@@ -423,8 +449,8 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
             dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t0 / kBlockTok, seqrow * p.v.block_cap + t0 / kBlockTok,
                                     l, kpacked, vpacked, kst, vst, mst);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // block i's stage is in
-        if (FAST) {   // ---- block i+1's data, before any compute on block i
-            const int64_t t1 = (t0 + kBlockTok < t_fast) ? t0 + kBlockTok : t0;
+        if (FAST && t0 + kBlockTok < t_fast) {   // ---- block i+1's data, before any compute on block i
+            const int64_t t1 = t0 + kBlockTok;
             dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t1 / kBlockTok, seqrow * p.v.block_cap + t1 / kBlockTok,
                                     l, true, true, ST ? &sh.k0[0] : &sh.k1[0], ST ? &sh.v0[0] : &sh.v1[0],
                                     ST ? &sh.m0[0] : &sh.m1[0]);
@@ -692,25 +718,17 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     int64_t t0 = t_begin;
-    int free_stage = 0;   // a stage no DMA writes to once the pipelined loop has ended
-    if (t0 < t_fast) {
-        dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t0 / kBlockTok, seqrow * p.v.block_cap + t0 / kBlockTok, l,
-                                true, true, &sh.k0[0], &sh.v0[0], &sh.m0[0]);
+    if (t0 < t_fast) {   // (block t_begin is already in flight to stage 0)
         for (;;) {
             block(T_{}, S0{}, t0);
             t0 += kBlockTok;
-            free_stage = 0;
             if (t0 >= t_fast) break;
             block(T_{}, S1{}, t0);
             t0 += kBlockTok;
-            free_stage = 1;
             if (t0 >= t_fast) break;
         }
     }
-    for (; t0 < t_end; t0 += kBlockTok) {
-        if (free_stage) block(F_{}, S1{}, t0);
-        else block(F_{}, S0{}, t0);
-    }
+    for (; t0 < t_end; t0 += kBlockTok) block(F_{}, S0{}, t0);   // (no DMA in flight here)
 
     // ---------------------------------------------------------------- partials
 #pragma unroll
@@ -758,41 +776,82 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     for (int i = l; i < S::ROWS * 36 + 4; i += 64) s_pbuf[i] = 0u;
     lds_sync();
 
-    auto nblk = [&](int b) { return (static_cast<int64_t>(p.seq_len[b]) + kBlockTok - 1) / kBlockTok; };
-    int64_t N = 0;
-    for (int b = 0; b < p.batch; ++b) N += p.heads_kv * nblk(b);
+    // Lane l of a chunk holds sequence c0 + l: its length, packed K / V block
+    // counts and 64-token block count -- one vector load per field for 64
+    // sequences rather than one dependent scalar load per sequence.
+    const int64_t H = p.heads_kv;
+    int64_t c0 = 0;
+    int32_t t_l = 0, nk_l = 0, nv_l = 0, nb_l = 0;
+    int64_t incl = 0;   // blocks of sequences c0 .. c0 + l, all kv-heads
+    auto load_chunk = [&]() {
+        const int64_t bb = c0 + l;
+        const bool in = bb < p.batch;
+        const int32_t t = in ? p.seq_len[bb] : 0;
+        t_l = t > 0 ? t : 0;
+        nk_l = (in && !SCORES && p.k.blocks) ? p.k.blocks[bb] : 0;
+        nv_l = (in && p.v.blocks) ? p.v.blocks[bb] : 0;
+        nb_l = static_cast<int32_t>((static_cast<int64_t>(t_l) + kBlockTok - 1) / kBlockTok);
+        incl = H * wave_incl_scan(nb_l);
+    };
+    load_chunk();
+    int64_t N = lane_get(incl, 63);
+    for (int64_t c = 64; c < p.batch; c += 64) {   // sequences past the first 64
+        const int32_t t = (c + l < p.batch) ? p.seq_len[c + l] : 0;
+        N += lane_get(H * wave_incl_scan((static_cast<int64_t>(t > 0 ? t : 0) + kBlockTok - 1) / kBlockTok), 63);
+    }
     const int64_t W = gridDim.x;
     int64_t P = (N + W - 1) / W;
     if (P < p.min_blocks) P = p.min_blocks;
     int64_t g = static_cast<int64_t>(blockIdx.x) * P;
     const int64_t g1 = (g + P < N) ? g + P : N;
     if (g >= g1) return;
-    int b = 0;
-    int64_t start_b = 0, nb = nblk(0);
-    while (g >= start_b + p.heads_kv * nb) {
-        start_b += p.heads_kv * nb;
-        nb = nblk(++b);
+
+    // the stream holding block g: first sequence whose blocks end past g
+    int64_t base = 0;   // first block of chunk c0
+    int lane = 0;
+    for (;;) {
+        const uint64_t hit = __ballot(c0 + l < p.batch && base + incl > g);
+        if (hit) {
+            lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+            break;
+        }
+        base += lane_get(incl, 63);
+        c0 += 64;
+        if (c0 >= p.batch) return;   // (not reached: g < N)
+        load_chunk();
     }
+    auto at = [&](int32_t x) { return static_cast<int64_t>(__builtin_amdgcn_readlane(x, lane)); };
+    int64_t nb = at(nb_l);
+    int64_t start_b = base + lane_get(incl, lane) - H * nb;   // first block of sequence c0 + lane
     int kvh = static_cast<int>((g - start_b) / nb);
     int64_t i0 = g - start_b - kvh * nb;
     while (g < g1) {
         const int64_t start_s = start_b + kvh * nb;
         const int64_t i1 = (i0 + (g1 - g) < nb) ? i0 + (g1 - g) : nb;
-        const int64_t T = p.seq_len[b];
+        const int64_t T = at(t_l);
         const int slot = static_cast<int>(blockIdx.x - start_s / P);
         const int count = static_cast<int>((start_s + nb - 1) / P - start_s / P + 1);
         if (slot < p.n_splits && count <= p.n_splits) {
-            segment<BITS, QDT, SCORES, GRP>(p, sh, b, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
-                                            slot, count);
+            segment<BITS, QDT, SCORES, GRP>(p, sh, static_cast<int>(c0 + lane), kvh, i0 * kBlockTok,
+                                            (i1 * kBlockTok < T) ? i1 * kBlockTok : T, at(nk_l), at(nv_l), slot,
+                                            count);
         } else {
             raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // workspace too small for this layout
         }
         g += i1 - i0;
         i0 = 0;
-        if (++kvh == p.heads_kv && g < g1) {
+        if (++kvh == p.heads_kv && g < g1) {   // next sequence (one with blocks: g < g1 <= N)
             kvh = 0;
-            start_b += p.heads_kv * nb;
-            nb = nblk(++b);
+            start_b += H * nb;
+            do {
+                if (++lane == 64) {
+                    c0 += 64;
+                    if (c0 >= p.batch) return;   // (not reached)
+                    load_chunk();
+                    lane = 0;
+                }
+                nb = at(nb_l);
+            } while (nb == 0);
         }
     }
 }
