@@ -218,6 +218,16 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
     }
     return x;
 }
+__device__ __forceinline__ int32_t wave_sum(int32_t x) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) x += __shfl_xor(x, d);
+    return x;
+}
+__device__ __forceinline__ int32_t wave_max(int32_t x) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) x = max(x, __shfl_xor(x, d));
+    return x;
+}
 __device__ __forceinline__ int64_t lane_get(int64_t x, int lane) {
     const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), lane));
     const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x >> 32), lane));
@@ -757,11 +767,13 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     if (bad) raise_status(p.status, NSN_ST_NONFINITE_ATTN);
 }
 
-// Balanced ("stream-K") partition: the 64-token blocks of all (sequence,
-// kv-head) streams, laid end to end, are split into equal contiguous ranges,
-// one per wave; a range that crosses a stream boundary yields one partial per
-// stream.  Every wave finishes at about the same time whatever the ragged
-// lengths.  Wave w's partial for stream s lands in slot w - first_wave(s).
+// Work partition over a fixed grid of waves, balanced whatever the ragged
+// lengths.  Normally each (sequence, kv-head) stream is cut into near-equal
+// contiguous ranges on waves of its own, one segment per wave (partial slot =
+// range index).  With more streams than waves (or more than 64 sequences) the
+// 64-token blocks of all streams are laid end to end and cut into equal
+// ranges ("stream-K"); a range that crosses a stream boundary yields one
+// partial per stream, wave w's for stream s in slot w - first_wave(s).
 template <int BITS, int QDT, bool SCORES, int GRP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
     using S = LdsShape<BITS, GRP>;
@@ -799,7 +811,48 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int32_t t = (c + l < p.batch) ? p.seq_len[c + l] : 0;
         N += lane_get(H * wave_incl_scan((static_cast<int64_t>(t > 0 ? t : 0) + kBlockTok - 1) / kBlockTok), 63);
     }
+    if (N == 0) return;
     const int64_t W = gridDim.x;
+    int lane = 0;   // (uniform) the lane holding the current sequence
+    auto at = [&](int32_t x) { return static_cast<int64_t>(__builtin_amdgcn_readlane(x, lane)); };
+
+    if (p.batch <= 64 && H * wave_sum(nb_l > 0) <= W) {
+        // Per-stream partition (every stream fits on its own waves): stream s
+        // gets n_s = ceil(nb_s / P) waves with near-equal contiguous block
+        // ranges, P the smallest block count per wave with sum_s n_s <= W.
+        // Each wave runs exactly one segment; the longest range is P blocks.
+        int64_t lo = (N + W - 1) / W, hi = wave_max(nb_l);
+        lo = (lo > p.min_blocks) ? lo : p.min_blocks;
+        lo = (lo < hi) ? lo : hi;
+        while (lo < hi) {
+            const int32_t mid = static_cast<int32_t>((lo + hi) / 2);
+            if (H * wave_sum((nb_l + mid - 1) / mid) <= W) hi = mid;
+            else lo = mid + 1;
+        }
+        const int32_t P = static_cast<int32_t>(lo);
+        const int32_t n_l = (nb_l + P - 1) / P;
+        const int64_t wincl = H * wave_incl_scan(n_l);   // waves of sequences 0 .. l
+        const int64_t w = blockIdx.x;
+        const uint64_t hit = __ballot(l < p.batch && wincl > w);
+        if (!hit) return;   // a spare wave
+        lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+        const int64_t n = at(n_l), nb = at(nb_l);
+        const int64_t r = w - (lane_get(wincl, lane) - H * n);
+        const int kvh = static_cast<int>(r / n);
+        const int64_t k = r - kvh * n;
+        const int64_t i0 = k * nb / n, i1 = (k + 1) * nb / n;
+        const int64_t T = at(t_l);
+        if (n <= p.n_splits) {
+            segment<BITS, QDT, SCORES, GRP>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
+                                            at(nk_l), at(nv_l), static_cast<int>(k), static_cast<int>(n));
+        } else {
+            raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // workspace too small for this layout
+        }
+        return;
+    }
+
+    // Stream-K partition (more streams than waves, or more than 64
+    // sequences): the blocks of all streams laid end to end, P per wave.
     int64_t P = (N + W - 1) / W;
     if (P < p.min_blocks) P = p.min_blocks;
     int64_t g = static_cast<int64_t>(blockIdx.x) * P;
@@ -808,7 +861,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
 
     // the stream holding block g: first sequence whose blocks end past g
     int64_t base = 0;   // first block of chunk c0
-    int lane = 0;
     for (;;) {
         const uint64_t hit = __ballot(c0 + l < p.batch && base + incl > g);
         if (hit) {
@@ -820,7 +872,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         if (c0 >= p.batch) return;   // (not reached: g < N)
         load_chunk();
     }
-    auto at = [&](int32_t x) { return static_cast<int64_t>(__builtin_amdgcn_readlane(x, lane)); };
     int64_t nb = at(nb_l);
     int64_t start_b = base + lane_get(incl, lane) - H * nb;   // first block of sequence c0 + lane
     int kvh = static_cast<int>((g - start_b) / nb);
