@@ -103,6 +103,22 @@ def test_5bit_decode_vs_oracle(kernel):
     assert ok, err
 
 
+@pytest.mark.parametrize("split", [None, 512])
+def test_fast_stream_k_partition_many_sequences(split):
+    """More than 64 sequences: the fast kernel cuts the blocks of all streams,
+    laid end to end, into equal ranges.  split=512 (>= every length) leaves two
+    partial slots per stream, so each range is as long as the longest stream
+    and most ranges cross stream boundaries."""
+    rng = np.random.default_rng(11)
+    lengths = [int(x) for x in rng.integers(1, 400, size=70)]
+    lengths[:4] = [64, 128, 1, 399]
+    k, v, qb, kk, vv, seq = make_case(11, 70, 8, 2, lengths)
+    _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel="fast", split_tokens=split,
+                                      kv_round_dtype=torch.float16)
+    ok, err = within(ctx.cpu().numpy(), oracle_ctx(k, v, qb, lengths, 3, "float32"))
+    assert ok, err
+
+
 @pytest.mark.parametrize("kernel", ["reference", "fast"])
 def test_split_invariance(kernel):
     lengths = [1500, 900]
