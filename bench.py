@@ -60,6 +60,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
+    p.add_argument("--workload", default="c2", choices=["c2", "c3"],
+                   help="c2: the headline line (default); c3: the 5-bit configuration, one line of its own")
     return p.parse_args()
 
 
@@ -285,6 +287,99 @@ def profile_run(args):
     log(f"[bench] profile run done: {args.steps} steps")
 
 
+C3 = dict(B=64, HQ=16, HKV=4, L=8192, bits=5)
+
+
+def main_c3(args):
+    """C3: 5-bit codes, B=64, 16q/4kv heads, every
+    sequence 8192 tokens (128 packed blocks, no tail), K and V heavy-tailed
+    (per-channel Student-t df=3 x lognormal token norms; GPU generator seed 3).
+    Measures the encode of every block of K and V (one launch over both) and
+    one fused decode step; prints one JSON line of its own."""
+    import torch
+    from nsn_amd import _dev, _lib, cache, kernels, synthetic
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    b_, hq, hkv, L, bits = C3["B"], C3["HQ"], C3["HKV"], C3["L"], C3["bits"]
+    gen = torch.Generator(device=dev).manual_seed(3)
+    log(f"[bench] generating C3 K/V on the GPU: B={b_} Hkv={hkv} L={L}, {bits}-bit")
+    kv = synthetic.heavy_tailed_torch(gen, (2, b_, hkv, L, D), dev)     # [K | V]
+    q = torch.randn((b_, hq, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+    # ---- encode: all 64-token blocks of K and V, one launch
+    rows, nblk = 2 * b_ * hkv, L // 64
+    nb_bytes = 64 * D * bits // 8
+    codes = torch.empty((rows, nblk, nb_bytes), dtype=torch.uint8, device=dev)
+    nrm = torch.empty((rows, nblk, 64), dtype=torch.float16, device=dev)
+    mn = torch.empty((rows, nblk, 128), dtype=torch.float16, device=dev)
+    sc = torch.empty((rows, nblk, 128), dtype=torch.float16, device=dev)
+    st = _dev.new_status(dev)
+    lib = _lib.lib()
+
+    def encode_all():
+        rc = lib.nsn_encode_blocks(kv.data_ptr(), _lib.DTYPE_F16, rows, nblk, L * D, 0, bits, _lib.NORM_LANES8, 1,
+                                   codes.data_ptr(), nrm.data_ptr(), mn.data_ptr(), sc.data_ptr(), None, None, nblk, 0, 0,
+                                   None, st.data_ptr(), stream.cuda_stream)
+        assert rc == 0
+    enc_ms = timed(encode_all, 10, 2, stream)
+    assert _dev.read_status(st) == 0
+    per_tok = 256 + bits * 16 + 10
+    enc_tokens = rows * L
+    enc_gbs = enc_tokens * per_tok / (enc_ms * 1e-3) / 1e9
+    log(f"[bench] C3 encode: {enc_ms * 1e3:.1f} us per launch ({enc_tokens} token-heads), "
+        f"{enc_tokens / (enc_ms * 1e-3) / 1e9:.2f} G tok/s, {enc_gbs:.0f} GB/s algorithmic ({per_tok} B/token)")
+    del codes, nrm, mn, sc
+
+    # ---- one decode step over the packed cache
+    lengths = [L] * b_
+    kk, seq = cache.pack_sequences(kv[0], lengths, bits=bits, tail_dtype=torch.float16)
+    vv, _ = cache.pack_sequences(kv[1], lengths, bits=bits, tail_dtype=torch.float16)
+    del kv
+    split, n_splits = kernels.default_split(b_, hkv, L)
+    n_splits = max(2, n_splits)
+    ws = torch.empty(kernels.workspace_floats(b_, hq, n_splits), dtype=torch.float32, device=dev)
+    out = torch.empty((b_, hq, D), dtype=torch.bfloat16, device=dev)
+    ctx = torch.empty((b_, hq, D), dtype=torch.float32, device=dev)
+    status = _dev.new_status(dev)
+    kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
+                             workspace=ws, out=out, ctx=ctx)
+
+    def step(merge=True):
+        kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
+                                 workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=merge)
+    ms_step = timed(step, args.steps, args.warmup, stream)
+    ms_split = timed(lambda: step(merge=False), args.steps, 2, stream)
+    assert _dev.read_status(status) == 0
+    nbytes = b_ * hkv * 2 * L * (bits * 16 + 10) + 2 * b_ * hq * D * 2
+    achieved = nbytes / (ms_split * 1e-3) / 1e9
+    log(f"[bench] C3 decode step {ms_step * 1e3:.1f} us, split kernel {ms_split * 1e3:.1f} us, "
+        f"{nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    _, ref_ctx = kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel="reference",
+                                          kv_round_dtype=torch.float32)
+    err = (ctx - ref_ctx).abs()
+    ok = bool((err <= 2e-3 + 1e-2 * ref_ctx.abs()).all())
+    log(f"[bench] C3 parity vs exact-order kernel: max abs {float(err.max()):.2e}, within tol: {ok}")
+    result = {
+        "metric": "C3 5-bit fused decode-attn µs/step (B=64, 16q/4kv, ctx 8192) + encode of all K/V blocks",
+        "value": round(ms_step * 1e3, 2), "unit": "µs/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (GPU torch.Generator seed 3)",
+        "config": {"workload": "C3: 5-bit packed K+V, B=64, 16q/4kv heads, d=128, ctx 8192 (128 blocks, no tail)",
+                   "batch": b_, "heads_q": hq, "heads_kv": hkv, "head_dim": D, "ctx": L, "bits": bits,
+                   "kernel": args.kernel, "split_tokens": split, "n_splits": n_splits},
+        "encode_us": round(enc_ms * 1e3, 1), "encode_gbs": round(enc_gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
+                     "kernel_us": round(ms_split * 1e3, 2)},
+        "encode_roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(enc_gbs / HBM_PEAK_GBS, 4)},
+        "parity_ok": ok,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -296,6 +391,9 @@ def main():
         return
     if args.profile:
         profile_run(args)
+        return
+    if args.workload == "c3":
+        main_c3(args)
         return
     import numpy as np
     import torch

@@ -36,7 +36,7 @@ struct EncodeParams {
     int zero_flat_scale;
 };
 
-constexpr int kXPad = kDim + 4;  // LDS row pitch (floats)
+constexpr int kXPadT = kDim + 8;  // LDS row pitch of the encode input block (elements; 16-byte rows)
 
 template <int DT>
 __device__ __forceinline__ void load_row8(const typename Elem<DT>::T *src, float (&v)[8]) {
@@ -131,13 +131,21 @@ template <int DT, int BITS, int ORDER>
 __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     using T = typename Elem<DT>::T;
     constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
-    __shared__ float xs[kBlockTok * kXPad];
+    // The input block (in its own type) is only read by the norm pass; the
+    // min/max partials and then the unpacked codes reuse its bytes.  Keeping
+    // the block at 2 bytes per element (fp16/bf16 inputs) holds the LDS to
+    // ~22 KB, so that six blocks share a CU.
+    constexpr int kXBytes = kBlockTok * kXPadT * static_cast<int>(sizeof(T));
+    static_assert(kXBytes >= 8192 + 2 * 4 * kDim * 4, "LDS aliasing");
+    __shared__ __align__(16) uint8_t xraw[kXBytes];
+    T *const xs = reinterpret_cast<T *>(xraw);
+    uint32_t *const codes_s = reinterpret_cast<uint32_t *>(xraw);                  // bytes [0, 8K): after the norms
+    float (*const redmin)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 8192);   // [8K, 10K)
+    float (*const redmax)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 10240);  // [10K, 12K)
     __shared__ float nrm_s[kBlockTok];
     __shared__ double rden_s[kBlockTok];
-    __shared__ float redmin[4][kDim], redmax[4][kDim];
-    __shared__ float m_s[kDim], s_s[kDim];
+    __shared__ float m_s[kDim];
     __shared__ double rs_s[kDim];
-    __shared__ uint32_t codes_s[kBlockTok * kDim / 4];
     __shared__ float mh_s[kDim], sh_s[kDim], nh_s[kBlockTok];
     __shared__ int bad_s;
 
@@ -155,12 +163,24 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = r0 + 16 * j;
-        load_row8<DT>(x + r * kDim + 8 * cg, v[j]);
+        const T *src = x + r * kDim + 8 * cg;
+        T *dst = xs + r * kXPadT + 8 * cg;
+        if constexpr (DT == NSN_DTYPE_F32) {
+            load_row8<DT>(src, v[j]);
+            *reinterpret_cast<float4 *>(dst) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            *reinterpret_cast<float4 *>(dst + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
+        } else {
+            const uint4 a = *reinterpret_cast<const uint4 *>(src);
+            *reinterpret_cast<uint4 *>(dst) = a;
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[j][2 * k] = Elem<DT>::load(static_cast<uint16_t>(w[k] & 0xffffu));
+                v[j][2 * k + 1] = Elem<DT>::load(static_cast<uint16_t>(w[k] >> 16));
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) bad |= !finite(v[j][e]);
-        float *dst = xs + r * kXPad + 8 * cg;
-        *reinterpret_cast<float4 *>(dst) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
-        *reinterpret_cast<float4 *>(dst + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
     }
     __syncthreads();
     if (bad) bad_s = 1;
@@ -171,9 +191,18 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float2 q = *reinterpret_cast<const float2 *>(xs + r * kXPad + 8 * k + jp);
-            a0 = __builtin_fmaf(q.x, q.x, a0);
-            a1 = __builtin_fmaf(q.y, q.y, a1);
+            float q0, q1;
+            if constexpr (DT == NSN_DTYPE_F32) {
+                const float2 q = *reinterpret_cast<const float2 *>(xs + r * kXPadT + 8 * k + jp);
+                q0 = q.x;
+                q1 = q.y;
+            } else {
+                const uint32_t q = *reinterpret_cast<const uint32_t *>(xs + r * kXPadT + 8 * k + jp);
+                q0 = Elem<DT>::load(static_cast<uint16_t>(q & 0xffffu));
+                q1 = Elem<DT>::load(static_cast<uint16_t>(q >> 16));
+            }
+            a0 = __builtin_fmaf(q0, q0, a0);
+            a1 = __builtin_fmaf(q1, q1, a1);
         }
         const float b0 = __shfl_down(a0, 1), b1 = __shfl_down(a1, 1);
         const float c0 = __shfl_down(a0, 2), c1 = __shfl_down(a1, 2);
@@ -188,7 +217,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         if (tid < kBlockTok) {
             float s = 0.f;
             for (int c = 0; c < kDim; ++c) {
-                const float q = xs[tid * kXPad + c];
+                const float q = Elem<DT>::load(xs[tid * kXPadT + c]);
                 s = __builtin_fmaf(q, q, s);
             }
             const float n = sqrt_rn(s);
@@ -236,8 +265,9 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         }
         const float s = div_by_recip(hi - lo, recip_rn(kLevels));
         m_s[tid] = lo;
-        s_s[tid] = s;
-        rs_s[tid] = (s == 0.f) ? 1.0 : recip_rn(s);
+        // 1/s; for s == 0 the reference divides by 1 (every d - m is 0 then),
+        // or zeroes the codes when zero_flat_scale is set: a factor of 0
+        rs_s[tid] = (s == 0.f) ? (p.zero_flat_scale ? 0.0 : 1.0) : recip_rn(s);
         const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
         p.mins[ob * kDim + tid] = hm;
         p.scales[ob * kDim + tid] = hs;
@@ -264,11 +294,9 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
         for (int e = 0; e < 8; ++e) {
             const int c = 8 * cg + e;
             const float t = v[j][e] - m_s[c];
-            float qf = __builtin_rintf(div_by_recip(t, rs_s[c]));
-            qf = qf < 0.f ? 0.f : (qf > kLevels ? kLevels : qf);
-            uint32_t q = static_cast<uint32_t>(qf);
-            if (p.zero_flat_scale && s_s[c] == 0.f) q = 0u;
-            packed[e >> 2] |= q << (8 * (e & 3));
+            // clamp(round_half_even(t / s), 0, 2^b - 1); t is finite for valid input
+            const float qf = __builtin_amdgcn_fmed3f(__builtin_rintf(div_by_recip(t, rs_s[c])), 0.f, kLevels);
+            packed[e >> 2] |= static_cast<uint32_t>(qf) << (8 * (e & 3));
         }
         const int r = r0 + 16 * j;
         codes_s[r * 32 + 2 * cg] = packed[0];
