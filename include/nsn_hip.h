@@ -210,6 +210,37 @@ int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, i
 int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits);
 
 /*
+ * Chunked-prefill attention: n_q chunk queries per (sequence, q-head) attend
+ * the sequence's context -- k.blocks[b] packed blocks, then ctx_len[b] -
+ * 64*blocks[b] tail tokens -- and the chunk's own K/V causally (chunk query i
+ * sees chunk tokens 0..i).  Packed blocks are dequantised tile by tile into
+ * LDS (direction m + s*z times the decode factor, fp16) and never reach HBM
+ * densely; QK^T and PV run on fp16 MFMA with fp32 accumulation and an online
+ * log2-domain softmax.  Replaces the reference's prefill route: materialise
+ * every packed block and the tail (PackedCache.materialize / update,
+ * experiments/ac08/source/loop_kv_pk01_cache.py:87-106, restore_group :40-42)
+ * followed by dense attention over the materialised K/V.
+ * Needs k.blocks and v.blocks equal per sequence (or both NULL), decode
+ * factors, 16-byte aligned arrays, and one dtype (fp16 or bf16) for q, the
+ * chunk K/V, the tails and out.
+ */
+typedef struct {
+    const void *q;          /* [B, Hq, n_q, 128] dtype */
+    int dtype;              /* NSN_DTYPE_F16 | NSN_DTYPE_BF16 */
+    int64_t batch, heads_q, heads_kv, n_q;   /* heads_q = G * heads_kv */
+    float scale;            /* 1/sqrt(128) */
+    const int32_t *ctx_len; /* [B] context tokens before the chunk (device) */
+    int bits;               /* 3 or 5 */
+    nsn_kv_side k, v;       /* packed context + tail (tail_dtype == dtype) */
+    const void *k_chunk;    /* [B, Hkv, n_q, 128] dtype: the chunk's own K */
+    const void *v_chunk;    /* [B, Hkv, n_q, 128] dtype */
+    void *out;              /* [B, Hq, n_q, 128] dtype */
+    int32_t *status;        /* NSN_ST_NONFINITE_OUTPUT; NSN_ST_NONFINITE_ATTN on an inconsistent cache */
+} nsn_prefill_args;
+
+int nsn_prefill_attention(const nsn_prefill_args *args, nsn_stream_t stream);
+
+/*
  * NaN/Inf scan over up to 16 arrays; array i sets bit i of flags[0] (int32)
  * and NSN_ST_NONFINITE_SCAN in status.  Replaces the grouped finite checks
  * (experiments/ac08/source/loop_kv_vf01_checks.py:20-63,

@@ -47,6 +47,12 @@ class AttnArgs(ctypes.Structure):
                 ("merge", I32)]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [("q", P), ("dtype", I32), ("batch", I64), ("heads_q", I64), ("heads_kv", I64), ("n_q", I64),
+                ("scale", ctypes.c_float), ("ctx_len", P), ("bits", I32), ("k", KVSide), ("v", KVSide),
+                ("k_chunk", P), ("v_chunk", P), ("out", P), ("status", P)]
+
+
 # symbol -> (restype, argtypes); must cover every function include/nsn_hip.h declares
 SIGNATURES = {
     "nsn_version": (ctypes.c_char_p, []),
@@ -59,6 +65,7 @@ SIGNATURES = {
     "nsn_attention_merge": (I32, [P, I64, I64, I32, P, P, I32, P, P]),
     "nsn_attention_workspace_floats": (I64, [I64, I64, I32]),
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
+    "nsn_prefill_attention": (I32, [ctypes.POINTER(PrefillArgs), P]),
 }
 
 _lib = None

@@ -1,0 +1,529 @@
+// Chunked-prefill attention over a packed K/V context (gfx950).
+//
+// One chunk of n_q queries per (sequence, q-head) attends the sequence's
+// context -- packed 64-token blocks, then an fp16/bf16 tail -- and the chunk's
+// own dense K/V, causally (chunk query i sees chunk tokens 0..i).  The
+// reference path materialises the whole K/V (restore of every packed block
+// plus the tail, loop_kv_pk01_cache.py:87-106) and runs dense attention on it;
+// here the packed blocks are dequantised tile by tile into LDS and never reach
+// HBM in dense form.
+//
+// Workgroup = 4 waves = 128 consecutive chunk queries of one (b, q-head);
+// each wave owns 32 queries (two 16-query MFMA column tiles).  Per 64-token
+// block:
+//   1. the raw block (K/V codes, K/V min and scale, K/V decode factors) is
+//      staged into LDS by DMA one block ahead;
+//   2. the 256 threads dequantise it once for the workgroup into
+//      K' [64 tok][128 ch] and V'^T [128 ch][64 tok] (fp16; the directions
+//      m + s*z, without the per-token factor);
+//   3. each wave computes S^T = K' Q^T and O^T += V'^T P^T on
+//      v_mfma_f32_16x16x32_f16, the per-token factors applied to the scores
+//      (K) and to the softmax weights (V) -- the transposed products keep P
+//      in registers: the C layout of S^T is already the B layout of P^T for
+//      a token order in which lane group g of a 32-token step holds tokens
+//      4g..4g+3 of both 16-token tiles.
+// Softmax runs in the log2 domain (Q pre-scaled by scale*log2(e)).
+#include "nsn_common.hpp"
+
+namespace nsn {
+namespace prefill {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQTile = 128;   // chunk queries per workgroup
+constexpr int kKP = 136;      // K' row pitch (halves): 272 B rows
+constexpr int kVP = 72;       // V'^T row pitch (halves): 144 B rows
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// fp32 pair -> packed fp16 (round to nearest even)
+__device__ __forceinline__ uint32_t pk16(float a, float b) {
+    const half2v h = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ float h16(uint32_t w, int hi) {
+    return static_cast<float>(__builtin_bit_cast(half2v, w)[hi]);
+}
+
+// Channel order inside each group of 8 (the K' columns and the Q
+// fragments share it): element p holds channel chE[p], whose 3-bit code the
+// unpack leaves at bit kE[p] of an fp16 half (a subnormal z * 2^(kE-24)).
+template <int BITS> struct Order;
+template <> struct Order<3> {
+    static constexpr int chE[8] = {0, 3, 1, 4, 2, 5, 6, 7};
+    static constexpr int kE[8] = {0, 1, 3, 4, 6, 7, 2, 5};
+};
+template <> struct Order<5> {
+    static constexpr int chE[8] = {0, 1, 2, 3, 4, 5, 6, 7};
+    static constexpr int kE[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+};
+
+// The 8 codes of one token's 8-channel group, from the staged code bytes:
+// 4 dwords, element p (dword p/2, half p%2) = code of channel chE[p] at bit kE[p].
+template <int BITS>
+__device__ __forceinline__ void codes8(const uint8_t *row, int cg, uint32_t (&B)[4]) {
+    const int byte = BITS * cg;   // the group's first byte within the token row
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(row + (byte & ~3));
+    const uint32_t sh = 8u * static_cast<uint32_t>(byte & 3);
+    const uint32_t x = __builtin_amdgcn_alignbit(w[1], w[0], sh);
+    if constexpr (BITS == 3) {
+        const uint32_t P = perm(x, x, 0x02010100u), Q = perm(x, x, 0x0C020C02u);
+        B[0] = P & 0x000E0007u;
+        B[1] = P & 0x00700038u;
+        B[2] = P & 0x038001C0u;
+        B[3] = Q & 0x00E0001Cu;
+    } else {
+        const uint32_t y = __builtin_amdgcn_alignbit(w[2], w[1], sh);   // code bits 32..63
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t z[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int e = 2 * i + h;
+                z[h] = (e < 6) ? __builtin_amdgcn_ubfe(x, 5 * e, 5)
+                     : (e == 6) ? (__builtin_amdgcn_alignbit(y, x, 30) & 31u)
+                                : ((y >> 3) & 31u);
+            }
+            B[i] = z[0] | (z[1] << 16);
+        }
+    }
+}
+
+struct Side {
+    const uint8_t *codes;
+    const uint16_t *mins, *scales;
+    const float *factors;
+    const int32_t *blocks;
+    int64_t block_cap;
+    const uint16_t *tail;   // DT
+    int64_t tail_cap;
+};
+
+struct PrefillParams {
+    const uint16_t *q;     // [B, Hq, n_q, 128] DT
+    int64_t batch, heads_q, heads_kv, n_q;
+    int group;
+    float qscale;          // scale * log2(e)
+    const int32_t *ctx_len;
+    Side k, v;
+    const uint16_t *kc, *vc;   // chunk K/V [B, Hkv, n_q, 128] DT
+    uint16_t *out;             // [B, Hq, n_q, 128] DT
+    int32_t *status;
+};
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from global memory straight into LDS at M0 + 16*lane.
+__device__ __forceinline__ void dma16(const void *src, void *dst) {
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Staged block layout (bytes): [K codes NB | V codes NB | K min 256 | K scale 256 |
+// V min 256 | V scale 256 | K factor 256 | V factor 256].
+template <int BITS> struct Stage {
+    static constexpr int NB = packed_block_bytes(BITS);
+    static constexpr int META = 2 * NB;
+    static constexpr int BYTES = 2 * NB + 1536;
+    static constexpr int NI = 2 * NB / 1024 + 2;   // 1 KiB DMA instructions per block
+};
+
+// DMA of packed block ib of (b, kvh) into one stage; instruction i of the
+// block is issued by wave i % 4.
+template <int BITS>
+__device__ __forceinline__ void stage_block(const PrefillParams &p, int64_t rk, int64_t rv, int wave, int l,
+                                            uint8_t *st) {
+    using S = Stage<BITS>;
+    const int q = l & 15;
+    for (int i = wave; i < S::NI; i += 4) {
+        if (i < S::NB / 1024) {
+            dma16(p.k.codes + rk * S::NB + 1024 * i + 16 * l, st + 1024 * i);
+        } else if (i < 2 * S::NB / 1024) {
+            const int c = i - S::NB / 1024;
+            dma16(p.v.codes + rv * S::NB + 1024 * c + 16 * l, st + S::NB + 1024 * c);
+        } else if (i == 2 * S::NB / 1024) {
+            const uint16_t *src = (l < 16) ? p.k.mins + rk * kDim : (l < 32) ? p.k.scales + rk * kDim
+                                : (l < 48) ? p.v.mins + rv * kDim : p.v.scales + rv * kDim;
+            dma16(src + 8 * q, st + S::META);
+        } else if (l < 32) {
+            const float *src = (l < 16) ? p.k.factors + rk * kBlockTok : p.v.factors + rv * kBlockTok;
+            dma16(src + 4 * q, st + S::META + 1024);
+        }
+    }
+}
+
+// Fill K' and V'^T from a dense token source x (row pitch 128, `valid` rows;
+// rows past it are zero).  Thread: tokens 4*rg .. 4*rg+3, channels 8*cg ..
+template <int BITS, int DT>
+__device__ __forceinline__ void fill_dense(const uint16_t *xk, const uint16_t *xv, int valid, int rg, int cg,
+                                          uint16_t *kt, uint16_t *vt) {
+    using O = Order<BITS>;
+    uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * rg + i;
+        float kf[8], vf[8];
+        if (t < valid) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(xk + static_cast<int64_t>(t) * kDim + 8 * cg);
+            const uint4 c = *reinterpret_cast<const uint4 *>(xv + static_cast<int64_t>(t) * kDim + 8 * cg);
+            const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t ka = static_cast<uint16_t>(wa[e >> 1] >> (16 * (e & 1)));
+                const uint16_t va = static_cast<uint16_t>(wc[e >> 1] >> (16 * (e & 1)));
+                kf[e] = Elem<DT>::load(ka);
+                vf[e] = Elem<DT>::load(va);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[e] = vf[e] = 0.f;
+        }
+        uint4 kw;
+        kw.x = pk16(kf[O::chE[0]], kf[O::chE[1]]);
+        kw.y = pk16(kf[O::chE[2]], kf[O::chE[3]]);
+        kw.z = pk16(kf[O::chE[4]], kf[O::chE[5]]);
+        kw.w = pk16(kf[O::chE[6]], kf[O::chE[7]]);
+        *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) = kw;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vf[e]));
+            if (i & 1) vcol[e][i >> 1] |= h << 16;
+            else vcol[e][i >> 1] = h;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<u32x2 *>(vt + (8 * cg + e) * kVP + 4 * rg) = u32x2{vcol[e][0], vcol[e][1]};
+}
+
+// Fill K' and V'^T from a staged packed block: direction m + s*z per element
+// (one fma with the code as an exact fp16 subnormal, scaled back by 2^(24-k)).
+template <int BITS>
+__device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, uint16_t *kt, uint16_t *vt) {
+    using S = Stage<BITS>;
+    using O = Order<BITS>;
+    constexpr int ROWB = BITS * 16;   // code bytes per token row
+    const uint4 km4 = *reinterpret_cast<const uint4 *>(st + S::META + 16 * cg);
+    const uint4 ks4 = *reinterpret_cast<const uint4 *>(st + S::META + 256 + 16 * cg);
+    const uint4 vm4 = *reinterpret_cast<const uint4 *>(st + S::META + 512 + 16 * cg);
+    const uint4 vs4 = *reinterpret_cast<const uint4 *>(st + S::META + 768 + 16 * cg);
+    const uint32_t KM[4] = {km4.x, km4.y, km4.z, km4.w}, KS[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+    const uint32_t VM[4] = {vm4.x, vm4.y, vm4.z, vm4.w}, VS[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+    float kmE[8], ksE[8], vmE[8], vsE[8];   // per element p (channel chE[p])
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int c = O::chE[p];
+        const float sc = static_cast<float>(1u << (24 - O::kE[p]));
+        kmE[p] = h16(KM[c >> 1], c & 1);
+        ksE[p] = h16(KS[c >> 1], c & 1) * sc;
+        vmE[p] = h16(VM[c >> 1], c & 1);
+        vsE[p] = h16(VS[c >> 1], c & 1) * sc;
+    }
+    uint32_t vcol[8][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * rg + i;
+        uint32_t bk[4], bv[4];
+        codes8<BITS>(st + t * ROWB, cg, bk);
+        codes8<BITS>(st + S::NB + t * ROWB, cg, bv);
+        float kd[8], vd[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            kd[p] = __builtin_fmaf(h16(bk[p >> 1], p & 1), ksE[p], kmE[p]);
+            vd[p] = __builtin_fmaf(h16(bv[p >> 1], p & 1), vsE[p], vmE[p]);
+        }
+        uint4 kw;
+        kw.x = pk16(kd[0], kd[1]);
+        kw.y = pk16(kd[2], kd[3]);
+        kw.z = pk16(kd[4], kd[5]);
+        kw.w = pk16(kd[6], kd[7]);
+        *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) = kw;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vd[p]));
+            if (i & 1) vcol[p][i >> 1] |= h << 16;
+            else vcol[p][i >> 1] = h;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+        *reinterpret_cast<u32x2 *>(vt + (8 * cg + O::chE[p]) * kVP + 4 * rg) = u32x2{vcol[p][0], vcol[p][1]};
+}
+
+template <int BITS, int DT>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
+    using S = Stage<BITS>;
+    using O = Order<BITS>;
+    __shared__ __align__(16) uint16_t kt[kBlockTok * kKP];
+    __shared__ __align__(16) uint16_t vt[kDim * kVP];
+    __shared__ __align__(16) uint8_t stg[2][S::BYTES];
+
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: the DMA targets are scalar)
+    const int row = l & 15, g = l >> 4;
+    const int rg = tid >> 4, cg = tid & 15;   // fill role
+    const int b = blockIdx.z, hq = blockIdx.y;
+    const int kvh = hq / p.group;
+    const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQTile;
+    const int64_t qw = q0 + 32 * wave;                     // this wave's first query
+    const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
+
+    const int64_t T = p.ctx_len[b];
+    const int64_t nbk = p.k.blocks ? p.k.blocks[b] : 0;
+    const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
+    const int64_t nb = nbk;                                // (== nbv, checked below)
+    const int64_t ntail = T - nb * kBlockTok;
+    const int64_t qend = (q0 + kQTile < p.n_q) ? q0 + kQTile : p.n_q;   // chunk tokens this workgroup sees
+    const int64_t nt_blk = (ntail + kBlockTok - 1) / kBlockTok;
+    const int64_t nblk = nb + nt_blk + (qend + kBlockTok - 1) / kBlockTok;
+    if (nbk != nbv || ntail < 0 || ntail > p.k.tail_cap || ntail > p.v.tail_cap) {
+        if (tid == 0) raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // inconsistent cache (host checks first)
+        return;
+    }
+
+    // ---- Q fragments (B operand of S^T = K' Q^T): query qw + 16*qt + row,
+    // channels 32*ks + 8*g + chE[e], times scale*log2(e), fp16
+    u32x4 qf[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int64_t qi = qw + 16 * qt + row;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
+            if (qi < p.n_q) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(
+                    p.q + ((static_cast<int64_t>(b) * p.heads_q + hq) * p.n_q + qi) * kDim + 32 * ks + 8 * g);
+                const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    x[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)))) * p.qscale;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.f;
+            }
+            qf[qt][ks] = u32x4{pk16(x[O::chE[0]], x[O::chE[1]]), pk16(x[O::chE[2]], x[O::chE[3]]),
+                               pk16(x[O::chE[4]], x[O::chE[5]]), pk16(x[O::chE[6]], x[O::chE[7]])};
+        }
+    }
+
+    f32x4 acc[8][2];   // O^T tiles [channel tile ct][query tile qt]
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    bool bad = false;
+
+    if (nb > 0) stage_block<BITS>(p, seqrow * p.k.block_cap, seqrow * p.v.block_cap, wave, l, stg[0]);
+
+    for (int64_t j = 0; j < nblk; ++j) {
+        // staged block j (all waves' DMA) is in; K'/V'^T are free
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const bool packed = j < nb;
+        if (j + 1 < nb)
+            stage_block<BITS>(p, seqrow * p.k.block_cap + j + 1, seqrow * p.v.block_cap + j + 1, wave, l,
+                              stg[(j + 1) & 1]);
+        // token range of block j: positions relative to its source
+        int valid;            // rows of the block in use
+        int64_t cpos = -1;    // chunk position of the block's first token (chunk blocks), else -1
+        if (packed) {
+            valid = kBlockTok;
+            fill_packed<BITS>(stg[j & 1], rg, cg, kt, vt);
+        } else if (j < nb + nt_blk) {
+            const int64_t t0 = (j - nb) * kBlockTok;
+            valid = static_cast<int>((ntail - t0 < kBlockTok) ? ntail - t0 : kBlockTok);
+            fill_dense<BITS, DT>(p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim,
+                                 p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim, valid, rg, cg, kt, vt);
+        } else {
+            cpos = (j - nb - nt_blk) * kBlockTok;
+            valid = static_cast<int>((qend - cpos < kBlockTok) ? qend - cpos : kBlockTok);
+            fill_dense<BITS, DT>(p.kc + (seqrow * p.n_q + cpos) * kDim, p.vc + (seqrow * p.n_q + cpos) * kDim,
+                                 valid, rg, cg, kt, vt);
+        }
+        __syncthreads();
+        if (qw >= p.n_q) continue;   // (a wave past the chunk end only helps fill)
+
+        // ---- S^T[token][query] = K' Q^T
+        f32x4 s[4][2];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) s[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(kt + (16 * tt + row) * kKP + 32 * ks + 8 * g);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) s[tt][qt] = mfma(a, qf[qt][ks], s[tt][qt]);
+            }
+        }
+        // per-token factors of this lane's tokens 16*tt + 4*g + i
+        float fk[4][4], fv[4][4];
+        if (packed) {
+            const float *fks = reinterpret_cast<const float *>(stg[j & 1] + S::META + 1024);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const float4 a = *reinterpret_cast<const float4 *>(fks + 16 * tt + 4 * g);
+                const float4 c = *reinterpret_cast<const float4 *>(fks + 64 + 16 * tt + 4 * g);
+                fk[tt][0] = a.x; fk[tt][1] = a.y; fk[tt][2] = a.z; fk[tt][3] = a.w;
+                fv[tt][0] = c.x; fv[tt][1] = c.y; fv[tt][2] = c.z; fv[tt][3] = c.w;
+            }
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) fk[tt][i] = fv[tt][i] = 1.f;
+        }
+        // ---- online softmax per query (lane's query qw + 16*qt + row)
+        u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int64_t qi = qw + 16 * qt + row;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tok = 16 * tt + 4 * g + i;
+                    const bool ok = tok < valid && (cpos < 0 || cpos + tok <= qi);
+                    const float v = ok ? s[tt][qt][i] * fk[tt][i] : -INFINITY;
+                    s[tt][qt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(m_run[qt], mx);
+            const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - msafe);   // 0 while nothing was seen
+            m_run[qt] = mnew;
+            float ls = 0.f;
+            float pw[4][4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = __builtin_amdgcn_exp2f(s[tt][qt][i] - msafe);
+                    ls += e;
+                    pw[tt][i] = e * fv[tt][i];
+                }
+            l_run[qt] = l_run[qt] * alpha + ls;
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct) acc[ct][qt] *= alpha;
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2)
+                pb[ks2][qt] = u32x4{pk16(pw[2 * ks2][0], pw[2 * ks2][1]), pk16(pw[2 * ks2][2], pw[2 * ks2][3]),
+                                    pk16(pw[2 * ks2 + 1][0], pw[2 * ks2 + 1][1]),
+                                    pk16(pw[2 * ks2 + 1][2], pw[2 * ks2 + 1][3])};
+        }
+        // ---- O^T[channel][query] += V'^T P''^T (k order: tokens 4g..4g+3 of both 16-token tiles)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                const uint16_t *vr = vt + (16 * ct + row) * kVP + 32 * ks2 + 4 * g;
+                const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr);
+                const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16);
+                const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma(a, pb[ks2][qt], acc[ct][qt]);
+            }
+        }
+    }
+
+    // ---- output: O[q][c] = O^T / l, channels 16*ct + 4*g + i of query qw + 16*qt + row
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        float lt = l_run[qt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const int64_t qi = qw + 16 * qt + row;
+        if (qi >= p.n_q) continue;
+        const float r = 1.f / lt;
+        uint16_t *dst = p.out + ((static_cast<int64_t>(b) * p.heads_q + hq) * p.n_q + qi) * kDim;
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[i] = acc[ct][qt][i] * r;
+                bad |= !finite(o[i]);
+            }
+            const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(o[0])) | (static_cast<uint32_t>(Elem<DT>::store(o[1])) << 16);
+            const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(o[2])) | (static_cast<uint32_t>(Elem<DT>::store(o[3])) << 16);
+            *reinterpret_cast<u32x2 *>(dst + 16 * ct + 4 * g) = u32x2{w0, w1};
+        }
+    }
+    if (bad) raise_status(p.status, NSN_ST_NONFINITE_OUTPUT);
+}
+
+}  // namespace prefill
+}  // namespace nsn
+
+using namespace nsn;
+
+extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t stream) {
+    using namespace nsn::prefill;
+    if (!a || !a->q || !a->ctx_len || !a->k_chunk || !a->v_chunk || !a->out) return NSN_EINVAL;
+    if (a->batch <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv || a->n_q < 0) return NSN_EINVAL;
+    if (a->n_q == 0) return NSN_OK;
+    if (a->bits != 3 && a->bits != 5) return NSN_EINVAL;
+    if (a->dtype != NSN_DTYPE_F16 && a->dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
+    auto side_ok = [](const nsn_kv_side &s) {
+        if (s.blocks && (!s.codes || !s.mins || !s.scales || !s.factors || s.block_cap <= 0)) return false;
+        if (s.codes && (reinterpret_cast<uintptr_t>(s.codes) & 15u)) return false;
+        if (s.mins && (reinterpret_cast<uintptr_t>(s.mins) & 15u)) return false;
+        if (s.scales && (reinterpret_cast<uintptr_t>(s.scales) & 15u)) return false;
+        if (s.factors && (reinterpret_cast<uintptr_t>(s.factors) & 15u)) return false;
+        if (s.tail && (reinterpret_cast<uintptr_t>(s.tail) & 15u)) return false;
+        if (s.tail_cap > 0 && !s.tail) return false;
+        return true;
+    };
+    if (!side_ok(a->k) || !side_ok(a->v)) return NSN_EINVAL;
+    if (!a->k.blocks != !a->v.blocks) return NSN_EINVAL;
+    if (a->k.tail && a->k.tail_dtype != a->dtype) return NSN_EINVAL;
+    if (a->v.tail && a->v.tail_dtype != a->dtype) return NSN_EINVAL;
+    for (const void *ptr : {static_cast<const void *>(a->q), a->k_chunk, a->v_chunk, static_cast<const void *>(a->out)})
+        if (reinterpret_cast<uintptr_t>(ptr) & 15u) return NSN_EINVAL;
+    const int64_t qt = (a->n_q + kQTile - 1) / kQTile;
+    if (qt > 0x7fffffff || a->heads_q > 65535 || a->batch > 65535) return NSN_EINVAL;
+    PrefillParams p{};
+    p.q = static_cast<const uint16_t *>(a->q);
+    p.batch = a->batch;
+    p.heads_q = a->heads_q;
+    p.heads_kv = a->heads_kv;
+    p.n_q = a->n_q;
+    p.group = static_cast<int>(a->heads_q / a->heads_kv);
+    p.qscale = a->scale * kLog2e;
+    p.ctx_len = a->ctx_len;
+    auto side = [](const nsn_kv_side &s) {
+        return Side{s.codes, s.mins, s.scales, s.factors, s.blocks, s.block_cap,
+                    static_cast<const uint16_t *>(s.tail), s.tail_cap};
+    };
+    p.k = side(a->k);
+    p.v = side(a->v);
+    p.kc = static_cast<const uint16_t *>(a->k_chunk);
+    p.vc = static_cast<const uint16_t *>(a->v_chunk);
+    p.out = static_cast<uint16_t *>(a->out);
+    p.status = a->status;
+    const dim3 grid(static_cast<unsigned>(qt), static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool bf = a->dtype == NSN_DTYPE_BF16;
+    if (a->bits == 3) {
+        if (bf) hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_BF16>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_F16>), grid, dim3(256), 0, st, p);
+    } else {
+        if (bf) hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_BF16>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_F16>), grid, dim3(256), 0, st, p);
+    }
+    return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
+}

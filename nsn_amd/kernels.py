@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _dev, _lib, codec
-from .errors import IntegrityError, NumericalFailure, require
+from .errors import ContractError, IntegrityError, NumericalFailure, require
 
 SCALE = 0.08838834764831845   # 1/sqrt(128), loop_kv_vf01_kernel.py:90
 BLOCK, DIM = 64, 128
@@ -197,6 +197,77 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):
             raise NumericalFailure("Nonfinite fused attention intermediate/output")
     return out, ctx
+
+
+def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, k_chunk, v_chunk, *, scale=SCALE,
+                      status=None, check=True, out=None):
+    """Chunked-prefill attention over a packed context (C4's prefill step).
+
+    q [B, Hq, n, 128]; k_chunk, v_chunk [B, Hkv, n, 128] (the chunk's own K/V;
+    one dtype, fp16 or bf16, for q, chunk, tails and output).  Chunk query i
+    attends the context -- ``blocks[b]`` packed blocks then ``ctx_len[b] -
+    64*blocks[b]`` tail tokens of k/v (None: no context) -- and chunk tokens
+    0..i.  Returns out [B, Hq, n, 128].  The reference materialises the
+    packed blocks and runs dense attention instead
+    (loop_kv_pk01_cache.py:87-106).
+    """
+    _dev.require_gpu(q, k_chunk, v_chunk, ctx_len)
+    require(q.ndim == 4 and q.shape[3] == DIM and q.is_contiguous(), "Query shape/type")
+    B, Hq, n, _ = q.shape
+    require(q.dtype in (torch.float16, torch.bfloat16), "Prefill dtype (fp16 or bf16)")
+    require(k_chunk.dtype == q.dtype and v_chunk.dtype == q.dtype and k_chunk.shape == v_chunk.shape
+            and k_chunk.ndim == 4 and k_chunk.shape[0] == B and k_chunk.shape[2] == n and k_chunk.shape[3] == DIM
+            and k_chunk.is_contiguous() and v_chunk.is_contiguous(), "Chunk K/V shape/type")
+    Hkv = k_chunk.shape[1]
+    require(Hq % Hkv == 0, "GQA group")
+    require(ctx_len.dtype == torch.int32 and ctx_len.numel() == B and ctx_len.is_cuda, "Context lengths")
+    a = _lib.PrefillArgs()
+    bits = 3
+    if (k is None) != (v is None):
+        raise ContractError("K and V context must both be given or both be None")
+    if k is not None:
+        for side in (k, v):
+            side.validate(B, Hkv)
+            require(side.codes is None or side.factor is not None, "Prefill needs decode factors")
+            require(side.tail is None or side.tail.dtype == q.dtype, "Tail dtype must equal the query dtype")
+        require(k.bits == v.bits and k.bits in (3, 5), "Prefill supports 3- and 5-bit codes")
+        require((k.codes is None) == (v.codes is None), "K/V packed layout differs")
+        bits = k.bits
+        if check:
+            L = ctx_len.cpu().numpy().astype(np.int64)
+            nk = k.blocks.cpu().numpy().astype(np.int64) if k.codes is not None else np.zeros_like(L)
+            nv = v.blocks.cpu().numpy().astype(np.int64) if v.codes is not None else np.zeros_like(L)
+            require(np.array_equal(nk, nv), "K/V packed block counts differ")
+            tk = k.tail.shape[2] if k.tail is not None else 0
+            tv = v.tail.shape[2] if v.tail is not None else 0
+            rest = L - BLOCK * nk
+            require(np.all(rest >= 0) and np.all(rest <= min(tk, tv)), "Context tail exceeds capacity")
+            if k.codes is not None:
+                require(np.all(nk <= k.codes.shape[2]), "Packed block count exceeds capacity")
+        a.k = k.side()
+        a.v = v.side()
+    elif check:
+        require(bool((ctx_len == 0).all()), "Context lengths without a context")
+    if out is None:
+        out = torch.empty_like(q)
+    st = status if status is not None else _dev.new_status(q.device)
+    a.q = q.data_ptr()
+    a.dtype = _dev.dtype_code(q.dtype)
+    a.batch, a.heads_q, a.heads_kv, a.n_q = B, Hq, Hkv, n
+    a.scale = scale
+    a.ctx_len = ctx_len.data_ptr()
+    a.bits = bits
+    a.k_chunk = k_chunk.data_ptr()
+    a.v_chunk = v_chunk.data_ptr()
+    a.out = out.data_ptr()
+    a.status = st.data_ptr()
+    rc = _lib.lib().nsn_prefill_attention(a, _dev.stream())
+    _lib.check(rc, "nsn_prefill_attention")
+    if check and status is None:
+        s = _dev.read_status(st)
+        if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_OUTPUT):
+            raise NumericalFailure("Nonfinite prefill output or inconsistent cache")
+    return out
 
 
 def _validate_lengths(seq_len, k, v, scores, max_seq_len):

@@ -1,0 +1,100 @@
+"""GPU parity of the chunked-prefill attention (nsn_prefill_attention) through the C-ABI.
+
+Expected values: the context K/V restored by the oracle (C restatement of
+nsn_encode + nsn_decode, fp32 reconstructions), the tail and the chunk K/V as
+stored, then float64 causal softmax attention per (sequence, q-head).
+Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise, on
+top of the output's own rounding (bf16/fp16).
+"""
+import numpy as np
+import pytest
+import torch
+
+from nsn_amd import cache, kernels, synthetic
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+ATOL, RTOL = 2e-3, 1e-2
+SCALE = 0.08838834764831845
+
+
+def restore_ctx(x16, length, bits, dtype):
+    """[H, T, 128] fp16 source -> fp32 [H, length, 128]: packed blocks restored
+    (fp32), tail tokens as stored in `dtype`."""
+    H = x16.shape[0]
+    C = (length // 64) * 64
+    parts = []
+    if C:
+        blocks = x16[:, :C].astype(np.float32).reshape(H, C // 64, 64, 128)
+        q, n, m, s, err = O.nsn_encode(blocks, bits)
+        assert err == 0
+        parts.append(O.nsn_decode_f32(q, n, m, s).reshape(H, C, 128))
+    if length > C:
+        parts.append(torch.from_numpy(x16[:, C:length]).to(dtype).float().numpy())
+    return np.concatenate(parts, axis=1) if parts else np.zeros((H, 0, 128), np.float32)
+
+
+def oracle_prefill(q, kctx, vctx, kch, vch):
+    """q [Hq, n, 128]; kctx/vctx [Hkv, L, 128]; kch/vch [Hkv, n, 128] -> [Hq, n, 128] float64."""
+    Hq, n, _ = q.shape
+    G = Hq // kch.shape[0]
+    out = np.zeros((Hq, n, 128))
+    for h in range(Hq):
+        kv = h // G
+        k = np.concatenate([kctx[kv], kch[kv]]).astype(np.float64)
+        v = np.concatenate([vctx[kv], vch[kv]]).astype(np.float64)
+        L = kctx.shape[1]
+        s = (q[h].astype(np.float64) @ k.T) * SCALE          # [n, L + n]
+        causal = np.arange(n)[:, None] < np.arange(n)[None, :]
+        s[:, L:][causal] = -np.inf
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[h] = (p @ v) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
+    rng = np.random.default_rng(seed)
+    T = max(max(ctx_lengths), 1)
+    kx = synthetic.kv_tokens(rng, (B, Hkv), T)
+    vx = synthetic.kv_tokens(rng, (B, Hkv), T)
+    kch = torch.from_numpy(synthetic.kv_tokens(rng, (B, Hkv), n)).to(dtype)
+    vch = torch.from_numpy(synthetic.kv_tokens(rng, (B, Hkv), n)).to(dtype)
+    q = torch.from_numpy(rng.standard_normal((B, Hq, n, 128)).astype(np.float32)).to(dtype)
+    if max(ctx_lengths) > 0:
+        kk, seq = cache.pack_sequences(torch.from_numpy(kx).to(DEV), ctx_lengths, bits=bits, tail_dtype=dtype)
+        vv, _ = cache.pack_sequences(torch.from_numpy(vx).to(DEV), ctx_lengths, bits=bits, tail_dtype=dtype)
+    else:
+        kk = vv = None
+        seq = torch.zeros(B, dtype=torch.int32, device=DEV)
+    out = kernels.prefill_attention(q.to(DEV), kk, vv, seq, kch.to(DEV), vch.to(DEV))
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        L = ctx_lengths[b]
+        kc = restore_ctx(kx[b], L, bits, dtype)
+        vc = restore_ctx(vx[b], L, bits, dtype)
+        ref = oracle_prefill(q[b].float().numpy(), kc, vc, kch[b].float().numpy(), vch[b].float().numpy())
+        ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11      # output rounding
+        err = np.abs(got[b] - ref)
+        bound = ATOL + (RTOL + ulp) * np.abs(ref)
+        assert np.all(err <= bound), (b, float(err.max()), float((err / bound).max()))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_packed_context_tail_and_chunk(dtype):
+    # sequence 0: 4 blocks + 44 tail tokens; sequence 1: 1 block + 13 tail; chunk of 150 (two query tiles)
+    run_case(21, 2, 4, 2, [300, 77], 150, 3, dtype)
+
+
+def test_prefill_no_context_is_causal_attention():
+    run_case(22, 1, 2, 2, [0], 200, 3, torch.bfloat16)
+
+
+def test_prefill_block_aligned_context_gqa8():
+    # context of whole blocks only (no tail); 8 q-heads per kv-head
+    run_case(23, 1, 8, 1, [256], 64, 3, torch.bfloat16)
+
+
+def test_prefill_5bit():
+    run_case(24, 2, 2, 2, [192, 100], 70, 5, torch.float16)
