@@ -118,3 +118,17 @@ def test_product_path_never_imports_the_oracle():
                 assert not any(a.name.startswith("oracle") for a in node.names), path
             if isinstance(node, ast.ImportFrom):
                 assert not (node.module or "").startswith("oracle"), path
+
+
+def test_stream_cache_policy_matches_reference_formulas():
+    """post_prefill / post_decode targets (loop_kv_pk01_cache.py:122-127), and
+    the tail-length invariant they keep over a long token-by-token run."""
+    from nsn_amd.stream_cache import decode_target, prefill_target
+    for L in range(0, 1000):
+        assert prefill_target(L) == max(0, ((L - 64) // 64) * 64)
+    L, C = 8192, prefill_target(8192)
+    assert L - C == 64
+    for _ in range(5000):
+        L += 1
+        C = decode_target(L, C)
+        assert C % 64 == 0 and 64 <= L - C < 128
