@@ -60,8 +60,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
-    p.add_argument("--workload", default="c2", choices=["c2", "c3"],
-                   help="c2: the headline line (default); c3: the 5-bit configuration, one line of its own")
+    p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4"],
+                   help="c2: the headline line (default); c3 / c4: the 5-bit and streaming-cache "
+                        "configurations, one line each")
+    p.add_argument("--slots", type=int, default=2, help="c4: attention slots measured (each the same work)")
+    p.add_argument("--decode-steps", type=int, default=64, help="c4: decode steps timed (of the 256)")
     return p.parse_args()
 
 
@@ -380,6 +383,127 @@ def main_c3(args):
     print(json.dumps(result), flush=True)
 
 
+C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
+
+
+def main_c4(args):
+    """C4: a streaming packed cache of Ouro-like
+    slots (MHA, 16 kv heads, d=128, batch 32, N(0,1) fp16 activations, GPU
+    generator seed 4).  Per slot: an 8192-token chunked prefill (16 chunks of
+    512: prefill attention over packed context + tail + the chunk, append,
+    compress), then decode steps that append one token, attend over packed +
+    tail with the fast kernel and compress a block every 64 tokens.  The 96
+    slots of the configuration do identical work; `--slots` of them are run
+    and the figures are per slot."""
+    import torch
+    from nsn_amd import _dev, kernels
+    from nsn_amd.stream_cache import StreamingKVCache
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    b_, h, T, ch = C4["B"], C4["H"], C4["T"], C4["chunk"]
+    S = max(1, args.slots)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    nchunks = T // ch
+    log(f"[bench] C4: {S} slots x B={b_} x {h} kv-heads, {T}-token chunked prefill (chunk {ch}), decode")
+    # activations: one set of chunk K/V/Q shared by the slots (identical work per slot)
+    acts = [tuple(torch.randn((b_, h, ch, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+                  for _ in range(3)) for _ in range(nchunks)]
+    cache = StreamingKVCache(S, b_, h, T + C4["steps"] + 64, bits=3, dtype=torch.float16, max_append=ch, device=dev)
+
+    def prefill_slot(s):
+        for c in range(nchunks):
+            qc, kc, vc = acts[c]
+            cache.prefill(s, qc, kc, vc, check=False)
+            cache.append(s, kc, vc)
+            cache.compress_to(s, max(cache.compressed[s], ((cache.length[s] - 64) // 64) * 64))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for s in range(S):
+        prefill_slot(s)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pre_ms = e0.elapsed_time(e1) / S
+    cache.post_prefill()
+    cache.check_status()
+    flops = 2.0 * b_ * h * T * T * D          # causal QK^T + PV (2 * B * H * T^2 * d)
+    mfma = flops / (pre_ms * 1e-3) / 1e12
+    log(f"[bench] C4 prefill: {pre_ms:.2f} ms per slot (16 chunks incl. append + in-place encode), "
+        f"{mfma:.0f} TFLOP/s = {mfma / 2500:.1%} of 2.5 PFLOP/s dense fp16")
+    # the prefill kernel alone, on the last chunk of one slot (context 7680 tokens)
+    qc, kc, vc = acts[-1]
+    saved = (cache.length[0], cache.compressed[0])
+    cache.length[0], cache.compressed[0] = T - ch, ((T - ch - 64) // 64) * 64   # state before the last chunk
+    for name in ("K", "V"):
+        cache.side(0, name).blocks.fill_(cache.compressed[0] // 64)
+    pk_ms = timed(lambda: cache.prefill(0, qc, kc, vc, check=False), 5, 2, stream)
+    last_flops = 2.0 * 2 * b_ * h * ch * D * ((T - ch) + (ch + 1) / 2)
+    log(f"[bench] C4 prefill kernel, last chunk (context {T - ch}): {pk_ms * 1e3:.0f} us, "
+        f"{last_flops / (pk_ms * 1e-3) / 1e12:.0f} TFLOP/s")
+    cache.length[0], cache.compressed[0] = saved
+    for name in ("K", "V"):
+        cache.side(0, name).blocks.fill_(cache.compressed[0] // 64)
+
+    # ---- decode steps: append, attend (fast kernel), compress every 64 tokens
+    qd = torch.randn((b_, h, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    tok = [torch.randn((b_, h, 1, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+           for _ in range(2)]
+    ws = torch.empty(kernels.workspace_floats(b_, h, 64), dtype=torch.float32, device=dev)
+    out = torch.empty((b_, h, D), dtype=torch.bfloat16, device=dev)
+    ctx = torch.empty((b_, h, D), dtype=torch.float32, device=dev)
+    status = _dev.new_status(dev)
+
+    def decode_step():
+        for s in range(S):
+            cache.append(s, tok[0], tok[1])
+            L = cache.length[s]
+            kernels.decode_attention(qd, cache.side(s, "K"), cache.side(s, "V"), cache.lengths(s), max_seq_len=L,
+                                     kernel="fast", split_tokens=256, workspace=ws, out=out, ctx=ctx,
+                                     status=status, check=False)
+        cache.post_decode()
+    n_dec = max(1, min(args.decode_steps, C4["steps"] - 2))
+    for L in range(cache.length[0], cache.length[0] + n_dec + 3):
+        cache.length_tensor(L)          # the per-length int32 tensors exist before timing
+    for _ in range(2):
+        decode_step()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(n_dec):
+        decode_step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dec_us = e0.elapsed_time(e1) * 1e3 / n_dec / S
+    assert _dev.read_status(status) == 0
+    cache.check_status()
+    L = cache.length[0]
+    C = cache.compressed[0]
+    dec_bytes = b_ * h * 2 * (C * 58 + (L - C) * 256) + 2 * b_ * h * D * 2
+    dec_gbs = dec_bytes / (dec_us * 1e-6) / 1e9
+    log(f"[bench] C4 decode: {dec_us:.1f} us per slot per step (append + fast decode + policy; context {L}), "
+        f"{dec_bytes / 1e6:.0f} MB -> {dec_gbs:.0f} GB/s ({dec_gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    result = {
+        "metric": "C4 streaming cache: chunked-prefill ms/slot (MFMA %) + decode µs/slot/step",
+        "value": round(dec_us, 2), "unit": "µs/slot/step", "n_gpus": 1, "steps": n_dec, "warmup": 2,
+        "ms_per_step": round(dec_us * S / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic N(0,1) (GPU torch.Generator seed 4)",
+        "config": {"workload": "C4: Ouro-like streaming cache, MHA 16 kv heads, d=128, batch 32, 8192-token "
+                               "chunked prefill (chunk 512) + decode over packed INT3 + fp16 tail",
+                   "slots_run": S, "batch": b_, "heads": h, "head_dim": D, "prefill_tokens": T, "chunk": ch,
+                   "bits": 3},
+        "prefill_ms_per_slot": round(pre_ms, 3),
+        "prefill_roofline": {"bound": "mfma", "achieved": round(mfma, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                             "frac": round(mfma / 2500, 4), "flops_per_slot": flops},
+        "prefill_kernel_last_chunk_us": round(pk_ms * 1e3, 1),
+        "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode step (append + fast decode + merge + policy)", "algorithmic_bytes": dec_bytes},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -394,6 +518,9 @@ def main():
         return
     if args.workload == "c3":
         main_c3(args)
+        return
+    if args.workload == "c4":
+        main_c4(args)
         return
     import numpy as np
     import torch

@@ -261,7 +261,7 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, u
 }
 
 template <int BITS, int DT>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
     __shared__ __align__(16) uint16_t kt[kBlockTok * kKP];
@@ -367,9 +367,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
                 for (int qt = 0; qt < 2; ++qt) s[tt][qt] = mfma(a, qf[qt][ks], s[tt][qt]);
             }
         }
-        // per-token factors of this lane's tokens 16*tt + 4*g + i
+        // per-token factors of this lane's tokens 16*tt + 4*g + i (packed blocks)
         float fk[4][4], fv[4][4];
-        if (packed) {
+        {
             const float *fks = reinterpret_cast<const float *>(stg[j & 1] + S::META + 1024);
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -378,34 +378,45 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
                 fk[tt][0] = a.x; fk[tt][1] = a.y; fk[tt][2] = a.z; fk[tt][3] = a.w;
                 fv[tt][0] = c.x; fv[tt][1] = c.y; fv[tt][2] = c.z; fv[tt][3] = c.w;
             }
-        } else {
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) fk[tt][i] = fv[tt][i] = 1.f;
         }
-        // ---- online softmax per query (lane's query qw + 16*qt + row)
+        // ---- online softmax per query (lane's query qw + 16*qt + row).  The
+        // running maximum (and the state's rescale) only moves when some
+        // lane's block maximum exceeds it.
+        const bool masked = valid < kBlockTok || cpos >= 0;   // (uniform) partial or causal block
         u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            const int64_t qi = qw + 16 * qt + row;
+            if (packed) {
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[tt][qt][i] *= fk[tt][i];
+            }
+            if (masked) {
+                // allowed tokens of this block: tok < valid and (chunk blocks) tok <= query - cpos
+                const int64_t rel = (cpos >= 0) ? qw + 16 * qt + row - cpos : kBlockTok;
+                const int lim = static_cast<int>((rel < valid - 1) ? rel : valid - 1);
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * tt + 4 * g + i > lim) s[tt][qt][i] = -INFINITY;
+            }
             float mx = -INFINITY;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tok = 16 * tt + 4 * g + i;
-                    const bool ok = tok < valid && (cpos < 0 || cpos + tok <= qi);
-                    const float v = ok ? s[tt][qt][i] * fk[tt][i] : -INFINITY;
-                    s[tt][qt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
+                mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qt][0], s[tt][qt][1]), fmaxf(s[tt][qt][2], s[tt][qt][3])));
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(m_run[qt], mx);
-            const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
-            const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - msafe);   // 0 while nothing was seen
-            m_run[qt] = mnew;
+            if (__builtin_amdgcn_ballot_w64(mx > m_run[qt])) {
+                const float mnew = fmaxf(m_run[qt], mx);
+                const float alpha = (m_run[qt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qt] - mnew);
+                l_run[qt] *= alpha;
+#pragma unroll
+                for (int ct = 0; ct < 8; ++ct) acc[ct][qt] *= alpha;
+                m_run[qt] = mnew;
+            }
+            const float msafe = (m_run[qt] == -INFINITY) ? 0.f : m_run[qt];
             float ls = 0.f;
             float pw[4][4];
 #pragma unroll
@@ -414,11 +425,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
                 for (int i = 0; i < 4; ++i) {
                     const float e = __builtin_amdgcn_exp2f(s[tt][qt][i] - msafe);
                     ls += e;
-                    pw[tt][i] = e * fv[tt][i];
+                    pw[tt][i] = packed ? e * fv[tt][i] : e;
                 }
-            l_run[qt] = l_run[qt] * alpha + ls;
-#pragma unroll
-            for (int ct = 0; ct < 8; ++ct) acc[ct][qt] *= alpha;
+            l_run[qt] += ls;
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2)
                 pb[ks2][qt] = u32x4{pk16(pw[2 * ks2][0], pw[2 * ks2][1]), pk16(pw[2 * ks2][2], pw[2 * ks2][3]),

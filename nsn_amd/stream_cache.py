@@ -102,7 +102,10 @@ class StreamingKVCache:
 
     def lengths(self, slot) -> torch.Tensor:
         """int32 [B] device tensor of the slot's length (every sequence equal)."""
-        L = self.length[slot]
+        return self.length_tensor(self.length[slot])
+
+    def length_tensor(self, L) -> torch.Tensor:
+        """int32 [B] device tensor filled with L (made once per L and kept)."""
         t = self._len_dev.get(L)
         if t is None:
             t = torch.full((self.batch,), L, dtype=torch.int32, device=self.device)
