@@ -169,6 +169,7 @@ __device__ __forceinline__ void fill_dense(const uint16_t *xk, const uint16_t *x
                                           uint16_t *kt, uint16_t *vt) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
+    float vprev[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = 4 * rg + i;
@@ -196,9 +197,8 @@ __device__ __forceinline__ void fill_dense(const uint16_t *xk, const uint16_t *x
         *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) = kw;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vf[e]));
-            if (i & 1) vcol[e][i >> 1] |= h << 16;
-            else vcol[e][i >> 1] = h;
+            if (i & 1) vcol[e][i >> 1] = pk16(vprev[e], vf[e]);
+            else vprev[e] = vf[e];
         }
     }
 #pragma unroll
@@ -229,31 +229,27 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, u
         vmE[p] = h16(VM[c >> 1], c & 1);
         vsE[p] = h16(VS[c >> 1], c & 1) * sc;
     }
-    uint32_t vcol[8][2];
+    uint32_t vcol[8][2];   // V'^T: per channel, tokens (4rg, 4rg+1), (4rg+2, 4rg+3) as fp16 pairs
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = 4 * rg + i;
-        uint32_t bk[4], bv[4];
-        codes8<BITS>(st + t * ROWB, cg, bk);
-        codes8<BITS>(st + S::NB + t * ROWB, cg, bv);
-        float kd[8], vd[8];
+    for (int k = 0; k < 2; ++k) {
+        float vd[2][8];
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            kd[p] = __builtin_fmaf(h16(bk[p >> 1], p & 1), ksE[p], kmE[p]);
-            vd[p] = __builtin_fmaf(h16(bv[p >> 1], p & 1), vsE[p], vmE[p]);
+        for (int h = 0; h < 2; ++h) {
+            const int t = 4 * rg + 2 * k + h;
+            uint32_t bk[4], bv[4];
+            codes8<BITS>(st + t * ROWB, cg, bk);
+            codes8<BITS>(st + S::NB + t * ROWB, cg, bv);
+            float kd[8];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                kd[p] = __builtin_fmaf(h16(bk[p >> 1], p & 1), ksE[p], kmE[p]);
+                vd[h][p] = __builtin_fmaf(h16(bv[p >> 1], p & 1), vsE[p], vmE[p]);
+            }
+            *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) =
+                uint4{pk16(kd[0], kd[1]), pk16(kd[2], kd[3]), pk16(kd[4], kd[5]), pk16(kd[6], kd[7])};
         }
-        uint4 kw;
-        kw.x = pk16(kd[0], kd[1]);
-        kw.y = pk16(kd[2], kd[3]);
-        kw.z = pk16(kd[4], kd[5]);
-        kw.w = pk16(kd[6], kd[7]);
-        *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) = kw;
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vd[p]));
-            if (i & 1) vcol[p][i >> 1] |= h << 16;
-            else vcol[p][i >> 1] = h;
-        }
+        for (int p = 0; p < 8; ++p) vcol[p][k] = pk16(vd[0][p], vd[1][p]);
     }
 #pragma unroll
     for (int p = 0; p < 8; ++p)
@@ -271,7 +267,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: the DMA targets are scalar)
     const int row = l & 15, g = l >> 4;
-    const int rg = tid >> 4, cg = tid & 15;   // fill role
+    // fill role: each 16-lane LDS pass covers all 16 token groups of one channel
+    // group, so its transposed V'^T writes are one contiguous 128-byte row
+    const int rg = tid & 15, cg = tid >> 4;
     const int b = blockIdx.z, hq = blockIdx.y;
     const int kvh = hq / p.group;
     const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQTile;
