@@ -99,9 +99,9 @@ template <> struct Layout<3> {
     static constexpr int kV[8] = {0, 3, 6, 1, 4, 7, 2, 5};
 };
 template <> struct Layout<5> {
-    static constexpr int chE[8] = {0, 1, 2, 3, 4, 5, 6, 7};
-    static constexpr int kE[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    static constexpr int kV[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    static constexpr int chE[8] = {0, 1, 2, 4, 5, 7, 3, 6};
+    static constexpr int kE[8] = {0, 5, 2, 4, 1, 3, 1, 0};
+    static constexpr int kV[8] = {0, 5, 2, 1, 4, 1, 0, 3};
 };
 
 // 3-bit K chunk (u0, u1, u2 = 12 bytes, 32 codes) -> 4 K-step B operands.
@@ -120,21 +120,30 @@ __device__ __forceinline__ void kunpack(const uint32_t (&u)[3], u32x4 (&B)[4]) {
     kgroup3(perm(u[2], u[1], 0x04030302u), perm(u[2], u[1], 0x0C040C04u), B[2]);
     kgroup3(perm(u[2], u[2], 0x03020201u), perm(u[2], u[2], 0x0C030C03u), B[3]);
 }
-// Generic width: code j of the chunk at bits [j*BITS, +BITS) of u[].
-template <int BITS>
-__device__ __forceinline__ uint32_t code_at(const uint32_t (&u)[BITS], int i) {
-    const int pos = i * BITS, w = pos >> 5, sh = pos & 31;
-    uint32_t v;
-    if (sh + BITS <= 32) v = u[w] >> sh;
-    else v = __builtin_amdgcn_alignbit(u[w + 1], u[w], sh);
-    return v & ((1u << BITS) - 1u);
+// 5-bit K chunk (u0..u4 = 20 bytes, 32 codes) -> 4 K-step B operands.  Group
+// g = bytes b0..b4 = 5g..5g+4 (8 codes at bits 5k).  Byte windows hold codes
+// 0/1 (b0 b1: bits 0, 5), 2 (b1 b2: bit 2), 4 (b2 b3: bit 4), 5 (b3 b4: bit
+// 1), 7 (b4: bit 3); codes 3 and 6 straddle bytes at bits 15 and 30 and come
+// from the group shifted by 14 bits (bit 1 of the low half, bit 0 of the high
+// half).  One AND per pair of codes, 3 perms and 1 funnel shift per group.
+__device__ __forceinline__ constexpr uint32_t sel4(int a, int b, int c, int d) {
+    return static_cast<uint32_t>(a | (b << 8) | (c << 16) | (d << 24));
 }
 __device__ __forceinline__ void kunpack(const uint32_t (&u)[5], u32x4 (&B)[4]) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            B[kk][i] = code_at<5>(u, 8 * kk + 2 * i) | (code_at<5>(u, 8 * kk + 2 * i + 1) << 16);
+    for (int g = 0; g < 4; ++g) {
+        const int w = (5 * g) / 4, o = 5 * g - 4 * w;           // group bytes at o .. o+4 of (u[w+1]:u[w])
+        const uint32_t lo = u[w], hi = u[w + 1 < 5 ? w + 1 : 4];
+        const uint32_t P0 = perm(hi, lo, sel4(o, o + 1, o, o + 1));
+        const uint32_t P1 = perm(hi, lo, sel4(o + 1, o + 2, o + 2, o + 3));
+        const uint32_t P2 = perm(hi, lo, sel4(o + 3, o + 4, o + 4, o + 4));
+        const int bit = 40 * g + 14, aw = bit / 32;
+        const uint32_t A = __builtin_amdgcn_alignbit(u[aw + 1 < 5 ? aw + 1 : 4], u[aw], bit % 32);
+        B[g][0] = P0 & 0x03E0001Fu;   // ch0 @0 | ch1 @5
+        B[g][1] = P1 & 0x01F0007Cu;   // ch2 @2 | ch4 @4
+        B[g][2] = P2 & 0x00F8003Eu;   // ch5 @1 | ch7 @3
+        B[g][3] = A & 0x001F003Eu;    // ch3 @1 | ch6 @0
+    }
 }
 
 // V: 16 token words w[t] (the lane's BITS*8 code bits of token t, aligned to
@@ -150,10 +159,27 @@ __device__ __forceinline__ void vpair3(uint32_t wa, uint32_t wb, uint32_t (&D)[8
     D[6] = Z & 0x001C001Cu;
     D[7] = Z & 0x00E000E0u;
 }
-__device__ __forceinline__ uint32_t vcode5(uint32_t w0, uint32_t w1, int m) {
-    if (m < 6) return __builtin_amdgcn_ubfe(w0, 5 * m, 5);
-    if (m == 6) return __builtin_amdgcn_alignbit(w1, w0, 30) & 31u;
-    return (w1 >> 3) & 31u;
+// 5-bit V: token words (w0 = code bits 0..31, w1 = 32..39) of tokens a, b ->
+// per channel m: code m of a (low half) | of b (high half), at bit kV[m]
+// (the byte windows of the K side; codes 3 and 6 from the words shifted by 14).
+__device__ __forceinline__ void vpair5(uint32_t w0a, uint32_t w1a, uint32_t w0b, uint32_t w1b, uint32_t (&D)[8]) {
+    const uint32_t X0 = perm(w0b, w0a, 0x05040100u);   // a b0 b1 | b b0 b1
+    const uint32_t X1 = perm(w0b, w0a, 0x06050201u);   // b1 b2
+    const uint32_t X2 = perm(w0b, w0a, 0x07060302u);   // b2 b3
+    const uint32_t ta = __builtin_amdgcn_alignbit(w1a, w0a, 24), tb = __builtin_amdgcn_alignbit(w1b, w0b, 24);
+    const uint32_t X3 = perm(tb, ta, 0x05040100u);     // b3 b4
+    const uint32_t X4 = perm(tb, ta, 0x05050101u);     // b4
+    const uint32_t sa = __builtin_amdgcn_alignbit(w1a, w0a, 14), sb = __builtin_amdgcn_alignbit(w1b, w0b, 14);
+    const uint32_t X5 = perm(sb, sa, 0x05040100u);     // bits 14..29
+    const uint32_t X6 = perm(sb, sa, 0x07060302u);     // bits 30..45
+    D[0] = X0 & 0x001F001Fu;
+    D[1] = X0 & 0x03E003E0u;
+    D[2] = X1 & 0x007C007Cu;
+    D[3] = X5 & 0x003E003Eu;
+    D[4] = X2 & 0x01F001F0u;
+    D[5] = X3 & 0x003E003Eu;
+    D[6] = X6 & 0x001F001Fu;
+    D[7] = X4 & 0x00F800F8u;
 }
 
 template <int QDT>
@@ -666,8 +692,10 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 #pragma unroll
                         for (int m = 0; m < 8; ++m) D[m][k] = d8[m];
                     } else {
+                        uint32_t d8[8];
+                        vpair5(w0[ia], w1[ia], w0[ib], w1[ib], d8);
 #pragma unroll
-                        for (int m = 0; m < 8; ++m) D[m][k] = vcode5(w0[ia], w1[ia], m) | (vcode5(w0[ib], w1[ib], m) << 16);
+                        for (int m = 0; m < 8; ++m) D[m][k] = d8[m];
                     }
                 }
 #pragma unroll
