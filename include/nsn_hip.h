@@ -46,6 +46,8 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 #define NSN_ST_NONFINITE_ATTN 0x20    /* attention: nonfinite score/weights  */
 #define NSN_ST_NONFINITE_OUTPUT 0x40  /* attention merge: nonfinite context  */
 #define NSN_ST_NONFINITE_SCAN 0x80    /* finite scan: nonfinite raw input    */
+#define NSN_ST_NONFINITE_ATTN_INPUT 0x100 /* attention: nonfinite raw input read by the kernel
+                                             (q, tail tokens; block metadata in the REFERENCE kernel) */
 
 /* Return codes. */
 #define NSN_OK 0

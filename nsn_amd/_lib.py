@@ -25,6 +25,7 @@ ST_NONFINITE_RESTORE = 0x10
 ST_NONFINITE_ATTN = 0x20
 ST_NONFINITE_OUTPUT = 0x40
 ST_NONFINITE_SCAN = 0x80
+ST_NONFINITE_ATTN_INPUT = 0x100
 
 NSN_OK, NSN_EINVAL, NSN_ELAUNCH = 0, -1, -2
 

@@ -52,19 +52,26 @@ __device__ __forceinline__ float load_elem(const void *base, int64_t idx) {
     return Elem<DT>::load(static_cast<const typename Elem<DT>::T *>(base)[idx]);
 }
 
+// Flags returned by the tile loaders.
+constexpr int kBadRestore = 1;   // a reconstructed value is nonfinite
+constexpr int kBadInput = 2;     // a raw input (block metadata, tail token) is nonfinite
+
 // Reconstruct packed block `blk` of row `row` (= b*Hkv + kvh) into tile[64][kXP]
-// as fp32 values already rounded to RDT.  Returns true if any value is nonfinite.
+// as fp32 values already rounded to RDT.  Returns kBad* flags.
 template <int BITS, int RDT>
-__device__ bool restore_tile(const SideParams &sd, int64_t row, int64_t blk, float *tile, uint32_t *codes_s,
+__device__ int restore_tile(const SideParams &sd, int64_t row, int64_t blk, float *tile, uint32_t *codes_s,
                              float *m_s, float *s_s, float *n_s, double *rden_s) {
     constexpr int kXP = kDim + 4;
     const int tid = threadIdx.x;
     const int64_t ib = row * sd.block_cap + blk;
+    bool bad_in = false;   // the grouped finite check of the metadata, fused here
     if (tid < kDim) {
         m_s[tid] = f16_bits_to_f32(sd.mins[ib * kDim + tid]);
         s_s[tid] = f16_bits_to_f32(sd.scales[ib * kDim + tid]);
+        bad_in = !finite(m_s[tid]) || !finite(s_s[tid]);
     } else if (tid < kDim + kBlockTok) {
         n_s[tid - kDim] = f16_bits_to_f32(sd.norms[ib * kBlockTok + tid - kDim]);
+        bad_in = !finite(n_s[tid - kDim]);
     }
     {
         const uint32_t *src = reinterpret_cast<const uint32_t *>(sd.codes + ib * packed_block_bytes(BITS)) + tid * BITS;
@@ -129,12 +136,13 @@ __device__ bool restore_tile(const SideParams &sd, int64_t row, int64_t blk, flo
             dst[e] = y;
         }
     }
-    return bad;
+    return (bad ? kBadRestore : 0) | (bad_in ? kBadInput : 0);
 }
 
 // Dense tile: tokens [t0, t0 + valid) of the tail buffer row, zero beyond.
+// A nonfinite tail token is a raw-input failure.
 template <int TDT>
-__device__ bool dense_tile(const SideParams &sd, int64_t row, int64_t t0, int valid, float *tile) {
+__device__ int dense_tile(const SideParams &sd, int64_t row, int64_t t0, int valid, float *tile) {
     constexpr int kXP = kDim + 4;
     const int tid = threadIdx.x;
     const int cg = tid & 15, r0 = tid >> 4;
@@ -155,11 +163,11 @@ __device__ bool dense_tile(const SideParams &sd, int64_t row, int64_t t0, int va
             for (int e = 0; e < 8; ++e) dst[e] = 0.f;
         }
     }
-    return bad;
+    return bad ? kBadInput : 0;
 }
 
 template <int BITS, int RDT, int TDT>
-__device__ bool load_tile(const SideParams &sd, int64_t row, int b, int64_t t0, int valid, float *tile,
+__device__ int load_tile(const SideParams &sd, int64_t row, int b, int64_t t0, int valid, float *tile,
                           uint32_t *codes_s, float *m_s, float *s_s, float *n_s, double *rden_s) {
     const int64_t nb = sd.blocks ? sd.blocks[b] : 0;
     if (t0 < nb * kBlockTok)
@@ -192,9 +200,11 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < kMaxGroup / 4; ++k) acc[k][0] = acc[k][1] = 0.f;
 
+    bool bad_in = false;   // raw inputs: q, block metadata, tail tokens (the fused finite check)
     for (int i = tid; i < G * kDim; i += 256) {
         const int h = i / kDim, c = i - h * kDim;
         q_s[i] = load_elem<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + c);
+        bad_in |= !finite(q_s[i]);
     }
     if (tid < G) { run_m[tid] = -INFINITY; run_l[tid] = 0.f; }
     bool bad_attn = false, bad_restore = false;
@@ -214,7 +224,9 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
                 sc_s[i] = s;
             }
         } else {
-            bad_restore |= load_tile<BITS, RDT, TDT>(p.k, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+            const int fl = load_tile<BITS, RDT, TDT>(p.k, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+            bad_restore |= (fl & kBadRestore) != 0;
+            bad_in |= (fl & kBadInput) != 0;
             __syncthreads();
             const int r = tid >> 2, qq = tid & 3;
             for (int h = 0; h < G; ++h) {
@@ -262,7 +274,11 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
         }
         __syncthreads();
         // ---- V tile and P.V ----
-        bad_restore |= load_tile<BITS, RDT, TDT>(p.v, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+        {
+            const int fl = load_tile<BITS, RDT, TDT>(p.v, row, b, t0, valid, tile, codes_s, m_s, s_s, n_s, rden_s);
+            bad_restore |= (fl & kBadRestore) != 0;
+            bad_in |= (fl & kBadInput) != 0;
+        }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < kMaxGroup / 4; ++k) {
@@ -301,7 +317,8 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
             bad_attn |= !finite(acc[k][0]) || !finite(acc[k][1]);
         }
     }
-    int st = (bad_attn ? NSN_ST_NONFINITE_ATTN : 0) | (bad_restore ? NSN_ST_NONFINITE_RESTORE : 0);
+    int st = (bad_attn ? NSN_ST_NONFINITE_ATTN : 0) | (bad_restore ? NSN_ST_NONFINITE_RESTORE : 0) |
+             (bad_in ? NSN_ST_NONFINITE_ATTN_INPUT : 0);
     if (__any(st != 0)) {
         if (st) raise_status(p.status, st);
     }

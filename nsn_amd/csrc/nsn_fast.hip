@@ -260,6 +260,13 @@ __device__ __forceinline__ int64_t lane_get(int64_t x, int lane) {
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Nonzero iff one of the 8 fp16 values in w has an all-ones exponent (Inf/NaN):
+// the masked exponent plus one exponent step carries into the half's sign bit.
+__device__ __forceinline__ uint32_t f16x8_nonfinite(const uint4 &w) {
+    const uint32_t m = 0x7C007C00u, one = 0x04000400u, top = 0x80008000u;
+    return (((w.x & m) + one) | ((w.y & m) + one) | ((w.z & m) + one) | ((w.w & m) + one)) & top;
+}
+
 // LDS hand-off inside the single wave of a workgroup: the wave's LDS accesses
 // complete in order, so waiting for them (and stopping the compiler from
 // moving memory accesses across) is enough -- no s_barrier, and prefetched
@@ -404,6 +411,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     // pch .. pch+7 with pch = 32*wgq + 8*wkk (chunk wgq, K-step wkk).
     const int wgq = (l >> 2) & 3, wkk = l & 3;
     const int pch = 32 * wgq + 8 * wkk;
+    bool bad_in = false;   // raw inputs read here (q, tail tokens): the fused finite check
     float c1[NJ];                      // score scale: scale * log2(e) * 2^-sigma_h
     uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): q.m and dense keys
     uint32_t qkh[NJ][4], qkl[NJ][4];   // the same * 2^-kE: the coefficient rows
@@ -417,6 +425,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         for (int c = 0; c < 8; ++c) {
             qv[c] = valid ? load_q<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + pch + c) : 0.f;
             mx = fmaxf(mx, fabsf(qv[c]));
+            bad_in |= !finite(qv[c]);
         }
         mx = red16_max(mx);
         // sigma: max|q| * 2^sigma in [2^13, 2^14), so every coefficient |q s| < 2^14 * 2/7 stays fp16
@@ -584,6 +593,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 #pragma unroll
                     for (int kk = 0; kk < 4; ++kk) {
                         const uint4 v = ld16(src + 8 * kk);
+                        bad_in |= f16x8_nonfinite(v) != 0;
                         const uint32_t X[4] = {v.x, v.y, v.z, v.w};
                         u32x4 Bd;
 #pragma unroll
@@ -716,6 +726,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                     const int ta = 32 * kk2 + 8 * grp + 2 * k, tb = ta + 1;
                     const uint4 xa4 = ld16(vrow + (ta < valid ? ta : valid - 1) * kDim);
                     const uint4 xb4 = ld16(vrow + (tb < valid ? tb : valid - 1) * kDim);
+                    bad_in |= (f16x8_nonfinite(xa4) | f16x8_nonfinite(xb4)) != 0;
                     const uint32_t xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
                     const uint32_t xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
 #pragma unroll
@@ -793,6 +804,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         for (int m = 0; m < 8; ++m) bad |= !finite(acc[j][m]);
     }
     if (bad) raise_status(p.status, NSN_ST_NONFINITE_ATTN);
+    if (bad_in) raise_status(p.status, NSN_ST_NONFINITE_ATTN_INPUT);
 }
 
 // Work partition over a fixed grid of waves, balanced whatever the ragged

@@ -194,6 +194,8 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     _lib.check(rc, "nsn_decode_attention")
     if check and status is None:
         s = _dev.read_status(st)
+        if s & _lib.ST_NONFINITE_ATTN_INPUT:
+            raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):
             raise NumericalFailure("Nonfinite fused attention intermediate/output")
     return out, ctx
@@ -396,12 +398,13 @@ def restore_v(g, tail):
     return out.reshape(1, h, -1, DIM)
 
 
-def launch(g, kt, q, vg, vt, trace=False, kernel="reference"):
+def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
     """Fused packed-K/V readout (loop_kv_vf01_kernel.py:128-139; GQA: loop_kv_nb06_kernel.py:142-154).
 
     Returns (out [1,1,Hq,128] bf16, context [1,Hq,1,128] fp32, score, v): score
     and v are only produced with ``trace`` (computed from the exactly restored
-    K/V; the fused kernel itself keeps neither).
+    K/V; the fused kernel itself keeps neither).  With ``status`` (an int32
+    device word) nothing is raised: the caller reads the NSN_ST_* bits.
     """
     Hq = q.shape[1]
     T = _length(g, kt)
@@ -409,7 +412,7 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference"):
     ks, vs = _group_side(g, kt, factors=fast), _group_side(vg, vt, factors=fast)
     seq = torch.full((1,), T, dtype=torch.int32, device=q.device)
     out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
-                                kv_round_dtype=kt.dtype)
+                                kv_round_dtype=kt.dtype, status=status)
     score = vtr = None
     if trace:
         kk = restore_v(g, kt).float()
@@ -441,6 +444,11 @@ def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
     return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM)
 
 
+# The fused arms check their raw inputs inside the attention kernel instead of
+# a separate grouped scan (loop_kv_vf01_checks.py:55-63) before it.
+FUSED_VALIDATION = True
+
+
 def pipeline(arm, data, trace=False):
     """Checked route selection (loop_kv_vf01_kernel.py:141-158, loop_kv_nb06_kernel.py:175-191).
 
@@ -452,6 +460,24 @@ def pipeline(arm, data, trace=False):
     g, kt, q, vg, vt = data
     LAST_STAGE = "structural"
     structural(g, kt, q, vg, vt)
+    if arm in ("V_FUSED", "GQA_FUSED") and FUSED_VALIDATION:
+        # the grouped finite check (q, tails, block metadata) runs inside the
+        # attention kernel: one launch, one status read; a nonfinite raw input
+        # still fails at the 'input_finite' stage
+        LAST_STAGE = "attention"
+        st = _dev.new_status(q.device)
+        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace, status=st)
+        s = _dev.read_status(st)
+        if s & _lib.ST_NONFINITE_ATTN_INPUT:
+            LAST_STAGE = "input_finite"
+            raise NumericalFailure("VF01 nonfinite raw input")
+        if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):
+            raise NumericalFailure("Nonfinite fused attention intermediate/output")
+        LAST_STAGE = "output"
+        if not bool(torch.isfinite(out).all()):
+            raise NumericalFailure("Nonfinite VF01 output")
+        LAST_STAGE = "returned"
+        return (out, ctx, score, v) if trace else out
     LAST_STAGE = "input_finite"
     finite(g, kt, q, vg, vt)
     if arm in ("V_FUSED", "GQA_FUSED"):

@@ -282,9 +282,16 @@ def test_fast_matches_reference_launch_surface():
     assert ok, err
 
 
-def test_negative_fixtures_rejected_at_reference_stage():
+@pytest.mark.parametrize("fused", [True, False])
+def test_negative_fixtures_rejected_at_reference_stage(fused, monkeypatch):
     """NaN/Inf inputs stop at 'input_finite'; overflowing scores at 'attention'
-    (loop_kv_vf01_contract.py:98-120)."""
+    (loop_kv_vf01_contract.py:98-120) -- with the finite check fused into the
+    attention kernel (no separate scan is launched) and with the grouped scan."""
+    monkeypatch.setattr(kernels, "FUSED_VALIDATION", fused)
+    if fused:
+        def no_scan(*a, **k):
+            raise AssertionError("separate finite scan launched")
+        monkeypatch.setattr(kernels, "finite", no_scan)
     f = {"compressed": 64, "length": 65, "pattern": "mixed_codes"}
     a, (g, kt, q, vg, vt) = _fixture_data(f)
     q2 = q.clone()
@@ -305,3 +312,17 @@ def test_negative_fixtures_rejected_at_reference_stage():
     with pytest.raises(NumericalFailure):
         kernels.pipeline("V_FUSED", (None, tail, big, None, tail.clone()))
     assert kernels.LAST_STAGE == "attention"
+
+
+def test_fast_kernel_flags_nonfinite_raw_input():
+    """The fast kernel's fused finite check: a NaN query or tail token raises
+    as a raw-input failure, not as an attention intermediate."""
+    lengths = [200, 70]
+    k, v, qb, kk, vv, seq = make_case(7, 2, 8, 2, lengths)
+    q2 = qb.clone()
+    q2[1, 3, 5] = float("nan")
+    with pytest.raises(NumericalFailure, match="raw attention input"):
+        kernels.decode_attention(q2.to(DEV), kk, vv, seq, kernel="fast")
+    vv.tail[0, 1, 3, 7] = float("inf")          # token 64*3 + 3 of sequence 0 (tail)
+    with pytest.raises(NumericalFailure, match="raw attention input"):
+        kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel="fast")
