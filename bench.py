@@ -64,6 +64,9 @@ def parse():
                    help="c2: the headline line (default); c3 / c4: the 5-bit and streaming-cache "
                         "configurations, one line each")
     p.add_argument("--slots", type=int, default=2, help="c4: attention slots measured (each the same work)")
+    p.add_argument("--stats-summary", metavar="DIR",
+                   help="c3 / c4: turn a rocprofv3 --kernel-trace --stats run of that workload under DIR "
+                        "into profiles/<workload>.md")
     p.add_argument("--decode-steps", type=int, default=64, help="c4: decode steps timed (of the 256)")
     return p.parse_args()
 
@@ -504,6 +507,33 @@ def main_c4(args):
     print(json.dumps(result), flush=True)
 
 
+STATS_DOC = {
+    "c3": ("attn_fast_c3", "C3: 5-bit packed K/V, B=64, 16q/4kv, ctx 8192 -- encode of all blocks + decode steps",
+           "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c3 --no-cpu"),
+    "c4": ("prefill_c4", "C4: streaming cache, MHA 16 kv-heads, batch 32 -- 8192-token chunked prefill + decode steps",
+           "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c4 "
+           "--slots 1 --decode-steps 16"),
+}
+
+
+def stats_summary(d, workload):
+    """profiles/<name>.md from the kernel statistics of one rocprofv3 run."""
+    name, title, cmd = STATS_DOC[workload]
+    stats = _rows((Path(d) / "kt", "**/*kernel_stats.csv"))
+    top = sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:12]
+    L = [f"# {title}", "", "Command (from the repository root on one MI355X, `OUT` = an output folder), then "
+         f"`python3 bench.py --workload {workload} --stats-summary OUT`:", "", "```", cmd, "```", "",
+         "Kernels by total time (the largest are the synthetic-data generators of the set-up):", "",
+         "| kernel | calls | avg us | min us | max us | total ms |", "|---|---|---|---|---|---|"]
+    for r in top:
+        L.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                 f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                 f"{float(r['TotalDurationNs']) / 1e6:.2f} |")
+    L.append("")
+    (ROOT / "profiles" / f"{name}.md").write_text("\n".join(L))
+    print("\n".join(L))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -512,6 +542,9 @@ def main():
         sys.exit(2)
     if args.summarize:
         summarize(args.summarize)
+        return
+    if args.stats_summary:
+        stats_summary(args.stats_summary, args.workload)
         return
     if args.profile:
         profile_run(args)
