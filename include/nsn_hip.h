@@ -243,6 +243,16 @@ typedef struct {
 int nsn_prefill_attention(const nsn_prefill_args *args, nsn_stream_t stream);
 
 /*
+ * Append n new K and V tokens of `rows` = B*Hkv rows to preallocated tails
+ * in place: row r, token i of k_new (at (r*new_row_stride + i)*128 elements)
+ * goes to token offset + i of row r of k_tail ([rows, tail_cap, 128]); the
+ * same for v.  One launch for both sides.  Replaces the tail concatenation
+ * of PackedCache.update (experiments/ac08/source/loop_kv_pk01_cache.py:101-102).
+ */
+int nsn_tail_append(const void *k_new, const void *v_new, int64_t rows, int64_t n, int64_t new_row_stride,
+                    void *k_tail, void *v_tail, int64_t tail_cap, int64_t offset, int dtype, nsn_stream_t stream);
+
+/*
  * NaN/Inf scan over up to 16 arrays; array i sets bit i of flags[0] (int32)
  * and NSN_ST_NONFINITE_SCAN in status.  Replaces the grouped finite checks
  * (experiments/ac08/source/loop_kv_vf01_checks.py:20-63,

@@ -67,6 +67,7 @@ SIGNATURES = {
     "nsn_attention_workspace_floats": (I64, [I64, I64, I32]),
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
     "nsn_prefill_attention": (I32, [ctypes.POINTER(PrefillArgs), P]),
+    "nsn_tail_append": (I32, [P, P, I64, I64, I64, P, P, I64, I64, I32, P]),
 }
 
 _lib = None

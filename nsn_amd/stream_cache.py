@@ -126,8 +126,12 @@ class StreamingKVCache:
             raise IntegrityError("Tail overflow: compress before appending more tokens")
         if self.length[slot] + n > self.block_cap * BLOCK + self.tail_cap:
             raise IntegrityError("Cache capacity exceeded")
-        for name, x in (("K", k), ("V", v)):
-            self._sides[(slot, name)].kv.tail[:, :, t0:t0 + n] = x
+        require(k.dtype == self.dtype and v.dtype == self.dtype and k.is_contiguous() and v.is_contiguous(),
+                "Append dtype/layout")
+        kt, vt = self._sides[(slot, "K")].kv.tail, self._sides[(slot, "V")].kv.tail
+        rc = _lib.lib().nsn_tail_append(k.data_ptr(), v.data_ptr(), self.batch * self.heads, n, n, kt.data_ptr(),
+                                        vt.data_ptr(), self.tail_cap, t0, _dev.dtype_code(self.dtype), _dev.stream())
+        _lib.check(rc, "nsn_tail_append")
         self.length[slot] += n
 
     def compress_to(self, slot, target):
