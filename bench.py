@@ -91,6 +91,13 @@ def timed(fn, steps, warmup, stream):
     return e0.elapsed_time(e1) / steps
 
 
+def timed_median(fn, steps, stream, reps=5):
+    """Median over `reps` repetitions of timed(fn, steps, ...): the split
+    kernel's launch duration for the roofline, steadier than one short run."""
+    vals = sorted(timed(fn, steps, 5 if i == 0 else 2, stream) for i in range(reps))
+    return vals[len(vals) // 2]
+
+
 def algorithmic_bytes(lengths, bits):
     """Bytes the split kernel must move per step: packed K and V (codes + fp16
     norm/min/scale = bits*16 + 10 B per token per kv-head), fp16 tails
@@ -355,7 +362,7 @@ def main_c3(args):
         kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
                                  workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=merge)
     ms_step = timed(step, args.steps, args.warmup, stream)
-    ms_split = timed(lambda: step(merge=False), args.steps, 2, stream)
+    ms_split = timed_median(lambda: step(merge=False), args.steps, stream)
     assert _dev.read_status(status) == 0
     nbytes = b_ * hkv * 2 * L * (bits * 16 + 10) + 2 * b_ * hq * D * 2
     achieved = nbytes / (ms_split * 1e-3) / 1e9
@@ -605,7 +612,7 @@ def main():
     log(f"[bench] decode: kernel={args.kernel} split={split} tokens x {n_splits} splits, "
         f"{B * HKV * n_splits} work units; warmup {args.warmup}, steps {args.steps}")
     ms_step = timed(step, args.steps, args.warmup, stream)
-    ms_split = timed(lambda: step(merge=False), args.steps, 2, stream)
+    ms_split = timed_median(lambda: step(merge=False), args.steps, stream)
     st_val = _dev.read_status(status)
     assert st_val == 0, f"status word {st_val:#x}"
     nbytes = algorithmic_bytes(lengths, 3)

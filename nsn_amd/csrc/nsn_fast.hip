@@ -244,15 +244,40 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
     }
     return x;
 }
-__device__ __forceinline__ int32_t wave_sum(int32_t x) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) x += __shfl_xor(x, d);
-    return x;
+// 32-bit wave reductions and scan on DPP row operations plus scalar reads of
+// the four row results: a few cycles per step instead of an LDS permute each.
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i(int32_t x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);   // (lanes without a source read 0)
 }
-__device__ __forceinline__ int32_t wave_max(int32_t x) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) x = max(x, __shfl_xor(x, d));
-    return x;
+__device__ __forceinline__ int32_t rows4_sum(int32_t x) {
+    return __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16) + __builtin_amdgcn_readlane(x, 32) +
+           __builtin_amdgcn_readlane(x, 48);
+}
+__device__ __forceinline__ int32_t wave_sum(int32_t x) {   // (uniform result)
+    x += dpp_i<0xb1>(x);
+    x += dpp_i<0x4e>(x);
+    x += dpp_i<0x141>(x);
+    x += dpp_i<0x140>(x);
+    return rows4_sum(x);
+}
+__device__ __forceinline__ int32_t wave_max(int32_t x) {   // (uniform result)
+    x = max(x, dpp_i<0xb1>(x));
+    x = max(x, dpp_i<0x4e>(x));
+    x = max(x, dpp_i<0x141>(x));
+    x = max(x, dpp_i<0x140>(x));
+    return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+__device__ __forceinline__ int32_t wave_incl_scan32(int32_t x) {
+    x += dpp_i<0x111>(x);   // row_shr:1, 2, 4, 8: inclusive scan inside each 16-lane row
+    x += dpp_i<0x112>(x);
+    x += dpp_i<0x114>(x);
+    x += dpp_i<0x118>(x);
+    const int l = threadIdx.x;
+    const int32_t r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31),
+                  r2 = __builtin_amdgcn_readlane(x, 47);
+    return x + (l >= 16 ? r0 : 0) + (l >= 32 ? r1 : 0) + (l >= 48 ? r2 : 0);
 }
 __device__ __forceinline__ int64_t lane_get(int64_t x, int lane) {
     const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), lane));
@@ -856,23 +881,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     int lane = 0;   // (uniform) the lane holding the current sequence
     auto at = [&](int32_t x) { return static_cast<int64_t>(__builtin_amdgcn_readlane(x, lane)); };
 
-    if (p.batch <= 64 && H * wave_sum(nb_l > 0) <= W) {
+    const int64_t nstr = H * wave_sum(nb_l > 0);   // streams with blocks (first 64 sequences)
+    if (p.batch <= 64 && nstr <= W) {
         // Per-stream partition (every stream fits on its own waves): stream s
-        // gets n_s = ceil(nb_s / P) waves with near-equal contiguous block
-        // ranges, P the smallest block count per wave with sum_s n_s <= W.
-        // Each wave runs exactly one segment; the longest range is P blocks.
+        // gets n_s = ceil(nb_s / P) waves with contiguous block ranges, P the
+        // smallest block count per wave with sum_s n_s <= W.  Each wave runs
+        // exactly one segment.  Since sum_s ceil(nb_s / P) <= N / P + nstr,
+        // the search starts below ceil(N / (W - nstr)).
         int64_t lo = (N + W - 1) / W, hi = wave_max(nb_l);
         lo = (lo > p.min_blocks) ? lo : p.min_blocks;
+        if (nstr < W) {   // (any P >= ub fits; the answer is the first fit >= lo)
+            int64_t ub = (N + (W - nstr) - 1) / (W - nstr);
+            ub = (ub > lo) ? ub : lo;
+            hi = (ub < hi) ? ub : hi;
+        }
         lo = (lo < hi) ? lo : hi;
         while (lo < hi) {
             const int32_t mid = static_cast<int32_t>((lo + hi) / 2);
-            if (H * wave_sum((nb_l + mid - 1) / mid) <= W) hi = mid;
+            const int32_t ns = (nb_l + mid - 1) / mid;
+            if (H * wave_sum(ns < W + 1 ? ns : static_cast<int32_t>(W + 1)) <= W) hi = mid;
             else lo = mid + 1;
         }
         const int32_t P = static_cast<int32_t>(lo);
         const int32_t n_l = (nb_l + P - 1) / P;
-        const int64_t wincl = H * wave_incl_scan(n_l);   // waves of sequences 0 .. l
-        const int64_t w = blockIdx.x;
+        const int64_t wincl = H * static_cast<int64_t>(wave_incl_scan32(n_l));   // waves of sequences 0 .. l
+        // Wave index: even indices are the workgroups dispatched first
+        // (blockIdx < W/2: the first wave slot of every SIMD), odd ones the
+        // second; each stream's consecutive waves alternate between the two.
+        // The first-slot wave of a SIMD wins most issue conflicts with the
+        // other (measured: ~20% more blocks per unit time), so its ranges
+        // are longer by 5:4.
+        const int64_t bx = blockIdx.x;
+        const int64_t w = (W % 2) ? bx : (bx < W / 2) ? 2 * bx : 2 * (bx - W / 2) + 1;
         const uint64_t hit = __ballot(l < p.batch && wincl > w);
         if (!hit) return;   // a spare wave
         lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
@@ -880,7 +920,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int64_t r = w - (lane_get(wincl, lane) - H * n);
         const int kvh = static_cast<int>(r / n);
         const int64_t k = r - kvh * n;
-        const int64_t i0 = k * nb / n, i1 = (k + 1) * nb / n;
+        const int64_t w0 = w - k;   // the stream's first wave
+        auto cw = [&](int64_t j) {   // summed weight of the stream's waves 0 .. j-1
+            const int64_t first = (W % 2) ? 0 : (w0 + j + 1) / 2 - (w0 + 1) / 2;
+            return 5 * first + 4 * (j - first);
+        };
+        // Cost units: a packed block 1, a block of dense fp16 tokens 3 (its
+        // 32 KB per side are read without the prefetch pipeline).
+        const int64_t nkb = SCORES ? at(nv_l) : at(nk_l), nvb = at(nv_l);
+        int64_t nbp = (nkb < nvb) ? nkb : nvb;
+        nbp = (nbp < nb) ? nbp : nb;
+        const int64_t U = nbp + 3 * (nb - nbp), ctot = cw(n);
+        auto blk = [&](int64_t c) { return (c <= nbp) ? c : nbp + (c - nbp + 1) / 3; };
+        const int64_t i0 = blk(cw(k) * U / ctot), i1 = blk(cw(k + 1) * U / ctot);
         const int64_t T = at(t_l);
         if (n <= p.n_splits) {
             segment<BITS, QDT, SCORES, GRP>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
