@@ -316,6 +316,13 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t *dst) {
     const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
+// The same with a uniform 64-bit base (SGPRs) and a 32-bit lane offset: the
+// per-block address update is scalar and the lane offset loop-invariant.
+__device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t *dst) {
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Per-wave LDS.  Separate objects, so that the compiler can tell the DMA
@@ -364,15 +371,16 @@ template <int BITS, bool SCORES>
 __device__ __forceinline__ void dma_block(const FastParams &p, int64_t ibk, int64_t ibv, int l, bool kside, bool vside,
                                           uint32_t *kst, uint32_t *vst, uint32_t *mst) {
     constexpr int NB = packed_block_bytes(BITS);
+    const uint32_t off = 16u * static_cast<uint32_t>(l);
     if (!SCORES && kside) {
-        const uint8_t *kc = p.k.codes + ibk * NB + 16 * l;
+        const uint8_t *kc = p.k.codes + ibk * NB;
 #pragma unroll
-        for (int c = 0; c < NB / 1024; ++c) dma16(kc + 1024 * c, kst + 256 * c);
+        for (int c = 0; c < NB / 1024; ++c) dma16s(kc + 1024 * c, off, kst + 256 * c);
     }
     if (vside) {
-        const uint8_t *vc = p.v.codes + ibv * NB + 16 * l;
+        const uint8_t *vc = p.v.codes + ibv * NB;
 #pragma unroll
-        for (int c = 0; c < NB / 1024; ++c) dma16(vc + 1024 * c, vst + 256 * c);
+        for (int c = 0; c < NB / 1024; ++c) dma16s(vc + 1024 * c, off, vst + 256 * c);
     }
     // metadata: lanes 0-15 K scale, 16-31 K min, 32-47 K factor, 48-63 V scale;
     // then lanes 0-15 V min, 16-31 V factor
@@ -420,9 +428,19 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     const int64_t kend = SCORES ? t_end : nbk * kBlockTok;
     int64_t t_fast = (kend < nbv * kBlockTok) ? kend : nbv * kBlockTok;
     t_fast = (t_fast < t_end) ? t_fast : t_end;
-    if (t_begin < t_fast)
-        dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t_begin / kBlockTok,
-                                seqrow * p.v.block_cap + t_begin / kBlockTok, l, true, true, &sh.k0[0], &sh.v0[0],
+    // The fast blocks are walked from a per-wave starting offset (wrapping
+    // round): waves then do not sweep the same relative addresses in step,
+    // which measurably helps the HBM (~2 % on the C2 workload).
+    const int64_t nfb = (t_fast > t_begin) ? (t_fast - t_begin) / kBlockTok : 0;
+    const int64_t rot =
+        (nfb > 1) ? static_cast<int64_t>((static_cast<uint32_t>(blockIdx.x) * 2654435761u) >> 8) % nfb : 0;
+    auto fast_blk = [&](int64_t j) {   // token start of the j-th fast block walked
+        const int64_t x = j + rot;
+        return t_begin + ((x < nfb) ? x : x - nfb) * kBlockTok;
+    };
+    if (nfb > 0)
+        dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + fast_blk(0) / kBlockTok,
+                                seqrow * p.v.block_cap + fast_blk(0) / kBlockTok, l, true, true, &sh.k0[0], &sh.v0[0],
                                 &sh.m0[0]);
 
     // ---- operand buffer addressing (loop invariant)
@@ -437,7 +455,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     const int wgq = (l >> 2) & 3, wkk = l & 3;
     const int pch = 32 * wgq + 8 * wkk;
     bool bad_in = false;   // raw inputs read here (q, tail tokens): the fused finite check
-    float c1[NJ];                      // score scale: scale * log2(e) * 2^-sigma_h
+    float c1[NJ], c1s[NJ];             // score scale: scale * log2(e) * 2^-sigma_h (c1s: times 2^24)
     uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): q.m and dense keys
     uint32_t qkh[NJ][4], qkl[NJ][4];   // the same * 2^-kE: the coefficient rows
 #pragma unroll
@@ -460,6 +478,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
         const float pw = ldexpf(1.f, sigma);
         c1[j] = p.scale * kLog2e * ldexpf(1.f, -sigma);
+        c1s[j] = c1[j] * 16777216.f;
         float qs[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) qs[c] = qv[c] * pw;
@@ -498,15 +517,16 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 
     const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
 
-    // ---- software pipeline over the fully packed blocks [t_begin, t_fast):
-    // all data of block i+1 (codes and metadata of K and V) is moved into the
-    // other LDS stage by DMA while block i is computed, and waited for with
-    // one vmcnt(0) at the top of block i+1.  No prefetched data lives in
+    // ---- software pipeline over the fully packed blocks [t_begin, t_fast),
+    // walked in the rotated order above: all data of the next block (codes
+    // and metadata of K and V) is moved into the other LDS stage by DMA while
+    // the current one is computed, and waited for with one vmcnt(0) at the
+    // top of the next block.  No prefetched data lives in
     // registers, so the compiler never has to wait for it mid-block, and no
     // DMA is left in flight when the pipelined loop ends.  Blocks past t_fast
     // (fp16 tail, dense K or V) fetch their own data first.
 
-    auto block = [&](auto fast, auto stage_c, const int64_t t0) {
+    auto block = [&](auto fast, auto stage_c, const int64_t t0, const int64_t t_next) {
         constexpr bool FAST = decltype(fast)::value;
         constexpr int ST = decltype(stage_c)::value;
         uint32_t *const kst = ST ? &sh.k1[0] : &sh.k0[0];
@@ -519,8 +539,8 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
             dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t0 / kBlockTok, seqrow * p.v.block_cap + t0 / kBlockTok,
                                     l, kpacked, vpacked, kst, vst, mst);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // block i's stage is in
-        if (FAST && t0 + kBlockTok < t_fast) {   // ---- block i+1's data, before any compute on block i
-            const int64_t t1 = t0 + kBlockTok;
+        if (FAST && t_next >= 0) {   // ---- the next fast block's data, before any compute on this one
+            const int64_t t1 = t_next;
             dma_block<BITS, SCORES>(p, seqrow * p.k.block_cap + t1 / kBlockTok, seqrow * p.v.block_cap + t1 / kBlockTok,
                                     l, true, true, ST ? &sh.k0[0] : &sh.k1[0], ST ? &sh.v0[0] : &sh.v1[0],
                                     ST ? &sh.m0[0] : &sh.m1[0]);
@@ -571,7 +591,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                         d = __builtin_amdgcn_fdot2(as_h2(quh[j][i]), as_h2(m2[i]), d, false);
                         d = __builtin_amdgcn_fdot2(as_h2(qul[j][i]), as_h2(m2[i]), d, false);
                     }
-                    qm[j] = red16_sum(d);
+                    qm[j] = red16_sum(d) * (1.f / 16777216.f);   // (in units of the code scale 2^-24)
                     put_frag(j, wh, wl);
                 }
                 float fk[4];
@@ -596,7 +616,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                 for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
-                        s[j][nt] = (qm[j] + (C[nt][2 * j] + C[nt][2 * j + 1]) * 16777216.f) * (fk[nt] * c1[j]);
+                        s[j][nt] = ((C[nt][2 * j] + C[nt][2 * j + 1]) + qm[j]) * (fk[nt] * c1s[j]);
             } else {
                 // dense fp16 keys (tokens t0 - 64*nbk + tt of the tail buffer): the A rows are the
                 // query itself (q * 2^sigma, hi + lo), channels in the same element order
@@ -704,18 +724,18 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         for (int m = 0; m < 8; ++m) O[m] = zf;
         if (vpacked) {
             // the lane's 16 token words first (one LDS round trip), then unpack:
-            // w0 = code bits 0..31 of token 32*kk2 + 8*grp + e, w1 = bits 32..63
+            // w0 = code bits 0..31 of token 16*grp + i (i = 8*kk2 + e), w1 = bits 32..63
             uint32_t w0[16], w1[16];
-            const uint32_t *vs0 = vst + 8 * grp * VROW_DW + vdw;
+            const uint32_t *vs0 = vst + 16 * grp * VROW_DW + vdw;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const uint32_t *vp = vs0 + (32 * (i >> 3) + (i & 7)) * VROW_DW;
+                const uint32_t *vp = vs0 + i * VROW_DW;
                 w0[i] = __builtin_amdgcn_alignbit(vp[1], vp[0], vsh);
                 w1[i] = (BITS == 3) ? 0u : __builtin_amdgcn_alignbit(vp[2], vp[1], vsh);
             }
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; ++kk2) {
-                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (16 * kk2 + 4 * grp));
+                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (8 * grp + 4 * kk2));
                 const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
                 uint32_t D[8][4];   // [tile m][token pair k]
 #pragma unroll
@@ -739,16 +759,16 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         } else {
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; ++kk2) {
-                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (16 * kk2 + 4 * grp));
+                const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (8 * grp + 4 * kk2));
                 const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
                 uint32_t D[8][4];
-                // dense fp16 V: tokens 32*kk2 + 8*grp + e, channels 8*row .. 8*row+7.
+                // dense fp16 V: tokens 16*grp + 8*kk2 + e, channels 8*row .. 8*row+7.
                 // Tokens past `valid` read the last valid token (in bounds); their
                 // weights are zero.
                 const uint16_t *vrow = p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok) * kDim + 8 * row;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int ta = 32 * kk2 + 8 * grp + 2 * k, tb = ta + 1;
+                    const int ta = 16 * grp + 8 * kk2 + 2 * k, tb = ta + 1;
                     const uint4 xa4 = ld16(vrow + (ta < valid ? ta : valid - 1) * kDim);
                     const uint4 xb4 = ld16(vrow + (tb < valid ? tb : valid - 1) * kDim);
                     bad_in |= (f16x8_nonfinite(xa4) | f16x8_nonfinite(xb4)) != 0;
@@ -791,18 +811,16 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     using T_ = std::true_type;
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    int64_t t0 = t_begin;
-    if (t0 < t_fast) {   // (block t_begin is already in flight to stage 0)
-        for (;;) {
-            block(T_{}, S0{}, t0);
-            t0 += kBlockTok;
-            if (t0 >= t_fast) break;
-            block(T_{}, S1{}, t0);
-            t0 += kBlockTok;
-            if (t0 >= t_fast) break;
+    if (nfb > 0) {   // (block fast_blk(0) is already in flight to stage 0)
+        for (int64_t j = 0;;) {
+            block(T_{}, S0{}, fast_blk(j), (j + 1 < nfb) ? fast_blk(j + 1) : -1);
+            if (++j >= nfb) break;
+            block(T_{}, S1{}, fast_blk(j), (j + 1 < nfb) ? fast_blk(j + 1) : -1);
+            if (++j >= nfb) break;
         }
     }
-    for (; t0 < t_end; t0 += kBlockTok) block(F_{}, S0{}, t0);   // (no DMA in flight here)
+    for (int64_t t0 = (t_fast > t_begin) ? t_fast : t_begin; t0 < t_end; t0 += kBlockTok)
+        block(F_{}, S0{}, t0, -1);   // (no DMA in flight here)
 
     // ---------------------------------------------------------------- partials
 #pragma unroll
