@@ -8,6 +8,8 @@
 //                experiments/ac08/source/loop_kv_pk01_cache.py:7-42
 //   VF01 bridge materialize   experiments/ac08/source/loop_kv_vf01_kernel.py:47-54
 //   finite checks             experiments/ac08/source/loop_kv_vf01_checks.py:20-63
+#include <type_traits>
+
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -17,8 +19,19 @@ namespace nsn {
 //
 // Thread tid holds rows r0 + 16*j (r0 = tid / 16, j = 0..3) x channels
 // 8*cg .. 8*cg+7 (cg = tid % 16): each global load is 16 contiguous bytes
-// and a wave reads 1 KiB of consecutive input.  The block is also staged in
-// LDS (fp32) for the norm, whose summation order must be torch's.
+// and a wave reads 1 KiB of consecutive input.  The raw block is also staged
+// in LDS for the norm, whose summation order must be torch's.
+//
+// The kernel is bound by VALU issue, so the per-element work is kept to
+// about 10 instructions, every result still bit-exact:
+//   - d = x / n: three fma for fp16 input (Markstein's correction of
+//     x * RN(1/n)); one fp64 multiply by RN64(1/n) for bf16 / fp32 input;
+//   - per-channel min / max: min3 / max3 over the thread's 4 rows, then the
+//     16 row-group partials through LDS;
+//   - codes: t = d - m, RN32(t / s) by one fp64 multiply, the half-even
+//     rounding to an integer by adding 1.5 * 2^23, and a shift-add of that
+//     word straight into the row's bitstream;
+//   - no per-element finite test: a nonfinite input shows in its row norm.
 // =====================================================================
 
 struct EncodeParams {
@@ -34,6 +47,7 @@ struct EncodeParams {
     uint8_t *codes_unpacked;
     int32_t *status;
     int zero_flat_scale;
+    int grid2d;   // 1: blockIdx.y = outer row, blockIdx.x = block; 0: one flat index
 };
 
 constexpr int kXPadT = kDim + 8;  // LDS row pitch of the encode input block (elements; 16-byte rows)
@@ -127,65 +141,132 @@ __device__ __forceinline__ void block_factors_lds(const uint8_t *codes_s, const 
     }
 }
 
+constexpr float kRoundMagic = 12582912.f;   // 1.5 * 2^23: q + this rounds q half-even into the low mantissa bits
+
+typedef _Float16 enc_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float half_lo(uint32_t w) { return static_cast<float>(__builtin_bit_cast(enc_h2, w)[0]); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return static_cast<float>(__builtin_bit_cast(enc_h2, w)[1]); }
+
+// x / den correctly rounded, for x an fp16 value, den > 0 and rc = RN(1/den):
+// q0 = RN(x * rc) is a faithful quotient, e = q0 * den - x is exact, and
+// RN(q0 + e * -rc) is the IEEE quotient (Markstein's correction).  Checked for
+// every fp16 significand against every fp32 significand of den, signed zeros
+// included (tests/exact_div_check.c).  `neg0` is -0 hidden from the compiler:
+// it keeps the first step an fma that reads x as fp16 (v_fma_mix_f32), and
+// x = -0 keeps its sign through all three steps.
+__device__ __forceinline__ float div_f16_markstein(float x, float den, float rc, float neg0) {
+    const float q0 = __builtin_fmaf(x, rc, neg0);
+    const float e = __builtin_fmaf(q0, den, -x);
+    return __builtin_fmaf(e, -rc, q0);   // (negating rc, not e: -fma(.) -> fma(-., -.) would lose a -0)
+}
+
+// The constant the shift-add packing carries along: the sum over the codes k
+// that start in the row's low dword of (bits of 1.5 * 2^23) << (BITS * k),
+// mod 2^32 (all 8 codes at 3 and 4 bits; codes 0..6 at 5 bits).
+template <int BITS>
+__device__ __forceinline__ constexpr uint32_t magic_sum_lo() {
+    uint32_t c = 0;
+    for (int k = 0; k < 8; ++k)
+        if (BITS * k < 32) c += 0x4B400000u << (BITS * k);
+    return c;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(x)));
+}
+// acc + (a << SH) as one v_lshl_add_u32 (left to itself the compiler turns a
+// chain of these into separate shifts and three-input adds).
+template <int SH>
+__device__ __forceinline__ uint32_t lshl_add(uint32_t a, uint32_t acc) {
+    uint32_t r;
+    asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "n"(SH), "v"(acc));
+    return r;
+}
+// v_perm_b32: byte i of the result = byte sel[i] of {hi:lo} (0..3 = lo, 4..7 = hi, 0x0c = 0).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
 template <int DT, int BITS, int ORDER>
 __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     using T = typename Elem<DT>::T;
     constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
     // The input block (in its own type) is only read by the norm pass; the
-    // min/max partials and then the unpacked codes reuse its bytes.  Keeping
-    // the block at 2 bytes per element (fp16/bf16 inputs) holds the LDS to
-    // ~22 KB, so that six blocks share a CU.
+    // 16 row-group min/max partials and then the u8 codes reuse its bytes.
+    // Keeping the block at 2 bytes per element (fp16/bf16 inputs) holds the
+    // LDS to ~22 KB per workgroup.
     constexpr int kXBytes = kBlockTok * kXPadT * static_cast<int>(sizeof(T));
-    static_assert(kXBytes >= 8192 + 2 * 4 * kDim * 4, "LDS aliasing");
+    static_assert(kXBytes >= 2 * 16 * kDim * 4, "LDS aliasing");
     __shared__ __align__(16) uint8_t xraw[kXBytes];
     T *const xs = reinterpret_cast<T *>(xraw);
-    uint32_t *const codes_s = reinterpret_cast<uint32_t *>(xraw);                  // bytes [0, 8K): after the norms
-    float (*const redmin)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 8192);   // [8K, 10K)
-    float (*const redmax)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 10240);  // [10K, 12K)
-    __shared__ float nrm_s[kBlockTok];
+    float (*const pmin)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw);           // [16][128], after the norms
+    float (*const pmax)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 8192);    // [16][128]
+    uint32_t *const codes_s = reinterpret_cast<uint32_t *>(xraw);                  // u8 codes, after the partials
+    __shared__ float nrm_s[kBlockTok], den_s[kBlockTok], rcp_s[kBlockTok];
     __shared__ double rden_s[kBlockTok];
     __shared__ float m_s[kDim];
     __shared__ double rs_s[kDim];
     __shared__ float mh_s[kDim], sh_s[kDim], nh_s[kBlockTok];
-    __shared__ int bad_s;
+    __shared__ int bad_s, clamp_s;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int64_t blk = blockIdx.x;
-    const int64_t o = blk / p.n_blocks, i = blk - o * p.n_blocks;
+    int64_t o, i;
+    if (p.grid2d) {
+        o = blockIdx.y;
+        i = blockIdx.x;
+    } else {
+        const uint32_t b = blockIdx.x, nb = static_cast<uint32_t>(p.n_blocks);
+        o = b / nb;
+        i = b - static_cast<uint32_t>(o) * nb;
+    }
     const int64_t ob = o * p.out_outer_blocks + p.out_block_offset + i;
     const T *x = static_cast<const T *>(p.x) + o * p.x_outer_stride + (p.x_token_offset + i * kBlockTok) * kDim;
 
-    if (tid == 0) bad_s = 0;
+    if (tid == 0) {
+        bad_s = 0;
+        clamp_s = 0;
+    }
     const int cg = tid & 15, r0 = tid >> 4;
-    float v[4][8];
-    bool bad = false;
+
+    // ---- load: the thread's 4 rows x 8 channels as raw dwords, also staged in LDS
+    constexpr int NW = (DT == NSN_DTYPE_F32) ? 8 : 4;   // dwords per 8 values
+    uint32_t xw[4][NW];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = r0 + 16 * j;
-        const T *src = x + r * kDim + 8 * cg;
-        T *dst = xs + r * kXPadT + 8 * cg;
-        if constexpr (DT == NSN_DTYPE_F32) {
-            load_row8<DT>(src, v[j]);
-            *reinterpret_cast<float4 *>(dst) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
-            *reinterpret_cast<float4 *>(dst + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
-        } else {
-            const uint4 a = *reinterpret_cast<const uint4 *>(src);
-            *reinterpret_cast<uint4 *>(dst) = a;
-            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+        const uint4 *src = reinterpret_cast<const uint4 *>(x + r * kDim + 8 * cg);
+        uint4 *dst = reinterpret_cast<uint4 *>(xs + r * kXPadT + 8 * cg);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                v[j][2 * k] = Elem<DT>::load(static_cast<uint16_t>(w[k] & 0xffffu));
-                v[j][2 * k + 1] = Elem<DT>::load(static_cast<uint16_t>(w[k] >> 16));
-            }
+        for (int h = 0; h < NW / 4; ++h) {
+            const uint4 a = src[h];
+            dst[h] = a;
+            xw[j][4 * h] = a.x; xw[j][4 * h + 1] = a.y; xw[j][4 * h + 2] = a.z; xw[j][4 * h + 3] = a.w;
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bad |= !finite(v[j][e]);
     }
     __syncthreads();
-    if (bad) bad_s = 1;
 
-    // ---- token norms, in torch's order ----
+    // ---- token norms, in torch's order.  A nonfinite input makes its row's
+    // norm nonfinite; for fp16 the converse holds too (128 squares of finite
+    // fp16 values stay below 2^40), otherwise the row is scanned.
+    auto set_row = [&](int r, float n) {
+        nrm_s[r] = n;
+        const float den = clamp_eps(n);
+        const double rd = recip_rn(den);
+        den_s[r] = den;
+        rden_s[r] = rd;
+        rcp_s[r] = static_cast<float>(rd);   // RN32(RN64(1/den)) = RN32(1/den): 1/den is never that close to a tie
+        if (!finite(n)) {
+            bool row_bad = DT == NSN_DTYPE_F16;
+            if (!row_bad)
+                for (int c = 0; c < kDim; ++c) row_bad |= !finite(Elem<DT>::load(xs[r * kXPadT + c]));
+            if (row_bad) bad_s = 1;
+        }
+    };
     if constexpr (ORDER == NSN_NORM_LANES8) {
         const int r = tid >> 2, jp = (tid & 3) * 2;
         float a0 = 0.f, a1 = 0.f;
@@ -204,14 +285,13 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
             a0 = __builtin_fmaf(q0, q0, a0);
             a1 = __builtin_fmaf(q1, q1, a1);
         }
-        const float b0 = __shfl_down(a0, 1), b1 = __shfl_down(a1, 1);
-        const float c0 = __shfl_down(a0, 2), c1 = __shfl_down(a1, 2);
-        const float d0 = __shfl_down(a0, 3), d1 = __shfl_down(a1, 3);
+        // the row's 4 threads are one quad of lanes: lane 0 gathers lanes 1..3
+        const float b0 = dpp_f32<0xF9>(a0), b1 = dpp_f32<0xF9>(a1);   // quad_perm [1,2,3,3]
+        const float c0 = dpp_f32<0xFE>(a0), c1 = dpp_f32<0xFE>(a1);   // quad_perm [2,3,3,3]
+        const float d0 = dpp_f32<0xFF>(a0), d1 = dpp_f32<0xFF>(a1);   // quad_perm [3,3,3,3]
         if ((tid & 3) == 0) {
             const float acc[8] = {a0, a1, b0, b1, c0, c1, d0, d1};
-            const float n = sqrt_rn(lane8_sum(acc));
-            nrm_s[r] = n;
-            rden_s[r] = recip_rn(clamp_eps(n));
+            set_row(r, sqrt_rn(lane8_sum(acc)));
         }
     } else {
         if (tid < kBlockTok) {
@@ -220,54 +300,69 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
                 const float q = Elem<DT>::load(xs[tid * kXPadT + c]);
                 s = __builtin_fmaf(q, q, s);
             }
-            const float n = sqrt_rn(s);
-            nrm_s[tid] = n;
-            rden_s[tid] = recip_rn(clamp_eps(n));
+            set_row(tid, sqrt_rn(s));
         }
     }
     __syncthreads();
 
-    // ---- directions d = x / max(n, eps) and per-channel min / max ----
-    float mn[8], mx[8];
+    // ---- directions d = x / max(n, eps), and the thread's min / max per channel
+    float d[4][8];
+    const float neg0 = keep_f32(-0.f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const double rd = rden_s[r0 + 16 * j];
+        const int r = r0 + 16 * j;
+        if constexpr (DT == NSN_DTYPE_F16) {
+            const float dn = den_s[r], rc = rcp_s[r];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t w = xw[j][e >> 1];
+                d[j][e] = div_f16_markstein((e & 1) ? half_hi(w) : half_lo(w), dn, rc, neg0);
+            }
+        } else {
+            const double rd = rden_s[r];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float v;
+                if constexpr (DT == NSN_DTYPE_F32) v = __uint_as_float(xw[j][e]);
+                else v = __uint_as_float((e & 1) ? (xw[j][e >> 1] & 0xffff0000u) : (xw[j][e >> 1] << 16));
+                d[j][e] = div_by_recip(v, rd);
+            }
+        }
+    }
+    {
+        float mn[8], mx[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float d = div_by_recip(v[j][e], rd);
-            v[j][e] = d;
-            if (j == 0) { mn[e] = d; mx[e] = d; }
-            else { mn[e] = d < mn[e] ? d : mn[e]; mx[e] = d > mx[e] ? d : mx[e]; }
+            mn[e] = fminf(fminf(fminf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
+            mx[e] = fmaxf(fmaxf(fmaxf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
         }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-#pragma unroll
-        for (int off = 16; off <= 32; off <<= 1) {
-            const float a = __shfl_xor(mn[e], off), b = __shfl_xor(mx[e], off);
-            mn[e] = a < mn[e] ? a : mn[e];
-            mx[e] = b > mx[e] ? b : mx[e];
-        }
-    }
-    if ((tid & 63) < 16) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { redmin[wave][8 * cg + e] = mn[e]; redmax[wave][8 * cg + e] = mx[e]; }
+        float4 *pn = reinterpret_cast<float4 *>(&pmin[r0][8 * cg]);
+        float4 *px = reinterpret_cast<float4 *>(&pmax[r0][8 * cg]);
+        pn[0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+        pn[1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
+        px[0] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+        px[1] = make_float4(mx[4], mx[5], mx[6], mx[7]);
     }
     __syncthreads();
 
+    // ---- per-channel min / scale over the 16 row-group partials; fp16 metadata
     int meta_flags = 0;
     if (tid < kDim) {
-        float lo = redmin[0][tid], hi = redmax[0][tid];
+        float lo = pmin[0][tid], hi = pmax[0][tid];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            lo = redmin[w][tid] < lo ? redmin[w][tid] : lo;
-            hi = redmax[w][tid] > hi ? redmax[w][tid] : hi;
+        for (int w = 1; w < 16; ++w) {
+            lo = fminf(lo, pmin[w][tid]);
+            hi = fmaxf(hi, pmax[w][tid]);
         }
         const float s = div_by_recip(hi - lo, recip_rn(kLevels));
         m_s[tid] = lo;
         // 1/s; for s == 0 the reference divides by 1 (every d - m is 0 then),
         // or zeroes the codes when zero_flat_scale is set: a factor of 0
         rs_s[tid] = (s == 0.f) ? (p.zero_flat_scale ? 0.0 : 1.0) : recip_rn(s);
+        // With a subnormal s the quotient (d - m) / s can pass the top level
+        // (s then also underflows fp16, which the status word reports): the
+        // code pass clamps only in that case.
+        if (s != 0.f && !(s >= 1.17549435e-38f)) clamp_s = 1;
         const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
         p.mins[ob * kDim + tid] = hm;
         p.scales[ob * kDim + tid] = hs;
@@ -286,47 +381,80 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     }
     __syncthreads();
 
-    // ---- codes: clamp(round_half_even((d - m) / s), 0, 2^b - 1) ----
+    // ---- codes clamp(round_half_even((d - m) / s), 0, 2^b - 1), packed in place.
+    // q = RN32(t / s) lies in [0, 2^b - 1 + 2^-20] for a normal s, so q + 1.5*2^23
+    // rounds it half-even to an integer held in the low mantissa bits; the
+    // shift-add of those words into the bitstream carries the constant
+    // exponent bits along, removed once per row.
+    float mreg[8];
+    double rsreg[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int c = 8 * cg + e;
-            const float t = v[j][e] - m_s[c];
-            // clamp(round_half_even(t / s), 0, 2^b - 1); t is finite for valid input
-            const float qf = __builtin_amdgcn_fmed3f(__builtin_rintf(div_by_recip(t, rs_s[c])), 0.f, kLevels);
-            packed[e >> 2] |= static_cast<uint32_t>(qf) << (8 * (e & 3));
-        }
-        const int r = r0 + 16 * j;
-        codes_s[r * 32 + 2 * cg] = packed[0];
-        codes_s[r * 32 + 2 * cg + 1] = packed[1];
+    for (int e = 0; e < 8; ++e) {
+        mreg[e] = m_s[8 * cg + e];
+        rsreg[e] = rs_s[8 * cg + e];
     }
-    __syncthreads();
+    // the lane's first output word (row r0); row r0 + 16j is 16j rows further on
+    const int k4 = cg & 3, a4 = cg >> 2;
+    uint8_t *const cbase = p.codes + ob * packed_block_bytes(BITS) + r0 * (16 * BITS);
+    uint32_t *const cdst = reinterpret_cast<uint32_t *>(
+        cbase + (BITS == 4 ? 4 * cg : (BITS == 3 ? 12 * a4 : 20 * a4) + 4 * k4));
+    constexpr int kRowStride = 16 * 16 * BITS / 4;   // dwords per 16 rows
+    uint2 *const udst = p.codes_unpacked
+        ? reinterpret_cast<uint2 *>(p.codes_unpacked + (o * p.n_blocks + i) * (kBlockTok * kDim) + r0 * kDim + 8 * cg)
+        : nullptr;
+    uint2 *const sdst = reinterpret_cast<uint2 *>(&codes_s[r0 * 32 + 2 * cg]);
+    auto code_rows = [&](auto clamp_c) {
+        constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float t = d[j][e] - mreg[e];
+                float q = static_cast<float>(static_cast<double>(t) * rsreg[e]);
+                if (CLAMP) q = fminf(q, kLevels);
+                v[e] = __float_as_uint(q + kRoundMagic);
+            }
+            uint32_t lo = v[0] - magic_sum_lo<BITS>();
+            lo = lshl_add<BITS>(v[1], lo);
+            lo = lshl_add<2 * BITS>(v[2], lo);
+            lo = lshl_add<3 * BITS>(v[3], lo);
+            lo = lshl_add<4 * BITS>(v[4], lo);
+            lo = lshl_add<5 * BITS>(v[5], lo);
+            lo = lshl_add<6 * BITS>(v[6], lo);
+            if constexpr (BITS < 5) lo = lshl_add<7 * BITS>(v[7], lo);
+            uint32_t *const dst = cdst + kRowStride * j;
+            if constexpr (BITS == 3) {
+                // a quad of lanes holds 96 consecutive bits: lane k writes dword k < 3
+                const uint32_t nxt = dpp_u32<0xF9>(lo);   // quad_perm [1,2,3,3]: lane k+1
+                const uint32_t D = (lo >> (8 * k4)) | (nxt << (24 - 8 * k4));
+                if (k4 < 3) *dst = D;
+            } else if constexpr (BITS == 4) {
+                *dst = lo;
+            } else {
+                // 40 bits per lane, 160 per quad: lane k writes dword k, lane 3 also dword 4
+                const uint32_t hi = lshl_add<3>(v[7], (v[6] >> 2) - ((0x4B400000u >> 2) + (0x4B400000u << 3)));
+                const uint32_t plo = dpp_u32<0x90>(lo), phi = dpp_u32<0x90>(hi);   // quad_perm [0,0,1,2]: lane k-1
+                const uint64_t P = (static_cast<uint64_t>(phi) << 32) | plo;
+                *dst = static_cast<uint32_t>(P >> (40 - 8 * k4)) | (lo << (8 * k4));
+                if (k4 == 3) dst[1] = (lo >> 8) | (hi << 24);
+            }
+            if (p.factors || p.codes_unpacked) {
+                // u8 codes: the low byte of each word
+                const uint32_t b0 = perm_b32(v[1], v[0], 0x0C0C0400u) | perm_b32(v[3], v[2], 0x04000C0Cu);
+                const uint32_t b1 = perm_b32(v[5], v[4], 0x0C0C0400u) | perm_b32(v[7], v[6], 0x04000C0Cu);
+                if (udst) udst[256 * j] = make_uint2(b0, b1);
+                if (p.factors) sdst[256 * j] = make_uint2(b0, b1);
+            }
+        }
+    };
+    if (clamp_s) code_rows(std::true_type{});
+    else code_rows(std::false_type{});
 
-    // ---- pack: thread g packs codes 32g .. 32g+31 (row g/4) into BITS dwords ----
-    {
-        const int g = tid;
-        uint32_t c[32];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t w4 = codes_s[g * 8 + k];
-            c[4 * k] = w4 & 0xffu; c[4 * k + 1] = (w4 >> 8) & 0xffu;
-            c[4 * k + 2] = (w4 >> 16) & 0xffu; c[4 * k + 3] = w4 >> 24;
-        }
-        uint32_t w[BITS];
-        pack32<BITS>(c, w);
-        uint32_t *dst = reinterpret_cast<uint32_t *>(p.codes + ob * packed_block_bytes(BITS)) + g * BITS;
-#pragma unroll
-        for (int k = 0; k < BITS; ++k) dst[k] = w[k];
-        if (p.codes_unpacked) {
-            uint4 *du = reinterpret_cast<uint4 *>(p.codes_unpacked + (o * p.n_blocks + i) * (kBlockTok * kDim)) + 2 * g;
-            du[0] = make_uint4(codes_s[g * 8], codes_s[g * 8 + 1], codes_s[g * 8 + 2], codes_s[g * 8 + 3]);
-            du[1] = make_uint4(codes_s[g * 8 + 4], codes_s[g * 8 + 5], codes_s[g * 8 + 6], codes_s[g * 8 + 7]);
-        }
-    }
-    if (p.factors)
+    if (p.factors) {
+        __syncthreads();
         block_factors_lds(reinterpret_cast<const uint8_t *>(codes_s), mh_s, sh_s, nh_s, p.factors + ob * kBlockTok);
+    }
     if (tid == 0 && p.headers) {
         const uint64_t tok = static_cast<uint64_t>(p.header_start_token + i * kBlockTok);
         uint32_t *h = reinterpret_cast<uint32_t *>(p.headers + ob * 12);
@@ -680,10 +808,12 @@ int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blo
     if (out_outer_blocks < out_block_offset + n_blocks) return NSN_EINVAL;
     const int64_t total = n_outer * n_blocks;
     if (total > 0x7fffffff) return NSN_EINVAL;
+    const int grid2d = n_outer <= 65535;
     EncodeParams p{x, n_blocks, x_outer_stride, x_token_offset, codes, norms, mins, scales, headers, factors,
                    out_outer_blocks, out_block_offset, header_start_token, codes_unpacked, status,
-                   zero_flat_scale};
-    const dim3 grid(static_cast<unsigned>(total));
+                   zero_flat_scale, grid2d};
+    const dim3 grid = grid2d ? dim3(static_cast<unsigned>(n_blocks), static_cast<unsigned>(n_outer))
+                             : dim3(static_cast<unsigned>(total));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (x_dtype == NSN_DTYPE_F16) encode_dispatch_bits<NSN_DTYPE_F16>(bits, norm_order, grid, s, p);
     else if (x_dtype == NSN_DTYPE_BF16) encode_dispatch_bits<NSN_DTYPE_BF16>(bits, norm_order, grid, s, p);

@@ -23,6 +23,11 @@
  *   - tensor division is IEEE fp32 division; torch.round is round-half-even;
  *     .to(float16) / .to(bfloat16) are round-to-nearest-even.
  *   - m + s*q is an unfused multiply then add.
+ *   - the per-channel min / max treat -0 as below +0 (IEEE 754-2019 minimum /
+ *     maximum).  Only the sign of a zero m or mx depends on this.  torch's
+ *     own reductions keep whichever zero their (vector-width and
+ *     backend dependent) order meets last, so no single reference rule
+ *     exists for a tie of signed zeros; this one does not depend on order.
  * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off -mfma; fmaf is called
  * explicitly where torch fuses).
  */
@@ -159,7 +164,9 @@ int oracle_nsn_encode(const float *x, int64_t nblocks, int bits, int zero_flat_s
             for (int t = 1; t < NSN_BLOCK; ++t) {
                 float v = d[t * NSN_DIM + c];
                 if (isnan(v) || v < lo) lo = (isnan(lo) ? lo : v);
+                else if (v == lo && signbit(v) && !signbit(lo)) lo = v;   /* -0 < +0 */
                 if (isnan(v) || v > hi) hi = (isnan(hi) ? hi : v);
+                else if (v == hi && !signbit(v) && signbit(hi)) hi = v;   /* +0 > -0 */
             }
             mn[c] = lo;
             sc[c] = (hi - lo) / levels;

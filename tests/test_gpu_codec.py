@@ -207,3 +207,61 @@ def test_restore_v_with_tail_matches_oracle():
     want = np.concatenate([O.nsn_decode(q_o, n_o, m_o, s_o, "float16").reshape(1, H, n * 64, 128),
                            tail.view(np.uint16)], axis=2)
     assert np.array_equal(u16(out), want.reshape(-1))
+
+
+def _edge_blocks():
+    """Blocks that take the encoder's rare paths, as fp32 [n, 64, 128] arrays
+    keyed by name, with the source dtypes each one is meaningful in."""
+    rng = np.random.default_rng(7)
+    out = {}
+    # signed-zero ties: channel 3 has min 0 reached by both +0 and -0, channel 9 max 0
+    x = np.abs(rng.standard_normal((64, 128))).astype(np.float32) + 0.25
+    x[:, 3] = np.abs(rng.standard_normal(64)) + 0.5
+    x[[5, 9, 40], 3] = 0.0
+    x[[2, 17, 33], 3] = -0.0
+    x[:, 9] = -np.abs(rng.standard_normal(64)) - 0.5
+    x[[1, 30], 9] = -0.0
+    x[[12, 50], 9] = 0.0
+    out["zero_ties"] = (x[None], ("float16", "bfloat16", "float32"))
+    z = np.zeros((2, 64, 128), np.float32)
+    z[1] = -0.0
+    out["all_zero"] = (z, ("float16", "bfloat16", "float32"))
+    # subnormal scale: quotients (d - m) / s past the top level, clamped
+    t = np.arange(64)[:, None]
+    c = np.arange(128)[None, :]
+    sub = (((t * 7 + c) % 5) * 1e-38).astype(np.float32)
+    sub[:, 0] = 1.0
+    out["subnormal_scale"] = (sub[None], ("bfloat16", "float32"))
+    # a row norm that overflows fp32 from finite inputs: not a nonfinite input
+    ov = rng.standard_normal((64, 128)).astype(np.float32)
+    ov[4, :2] = 2e38
+    out["norm_overflow"] = (ov[None], ("bfloat16", "float32"))
+    # nonfinite inputs
+    nf = rng.standard_normal((3, 64, 128)).astype(np.float32)
+    nf[0, 6, 77] = np.inf
+    nf[1, 0, 0] = np.nan
+    nf[2, 63, 127] = -np.inf
+    out["nonfinite"] = (nf, ("float16", "bfloat16", "float32"))
+    return out
+
+
+@pytest.mark.parametrize("bits", [3, 4, 5])
+def test_encode_edge_blocks_vs_oracle(bits):
+    """Signed-zero ties, zero blocks, a subnormal scale (the clamped code
+    path), a norm that overflows from finite inputs, and nonfinite inputs:
+    metadata, codes and status bits against the oracle."""
+    from nsn_amd import _dev
+    for name, (x, dtypes) in _edge_blocks().items():
+        for dt in dtypes:
+            xt = torch.from_numpy(x).to(getattr(torch, dt))
+            q_o, n_o, m_o, s_o, err = O.nsn_encode(xt.float().numpy(), bits)
+            st = _dev.new_status(DEV)
+            g = codec.encode_group(xt.to(DEV).reshape(1, 1, -1, 64, 128), 0, bits=bits, status=st, check=False)
+            status = _dev.read_status(st)
+            assert status == err, (name, dt, status, err)
+            if err & O.ERR_NONFINITE_INPUT:
+                continue   # outputs of a block with nonfinite input are unspecified (the reference raises)
+            assert np.array_equal(u16(g["metas"][0]), n_o.reshape(-1)), (name, dt)
+            assert np.array_equal(u16(g["metas"][1]), m_o.reshape(-1)), (name, dt)
+            assert np.array_equal(u16(g["metas"][2]), s_o.reshape(-1)), (name, dt)
+            assert np.array_equal(g["codes"].cpu().numpy().reshape(-1), O.pack_codes(q_o, bits)), (name, dt)
