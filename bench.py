@@ -61,9 +61,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
-    p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4"],
+    p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "k1c"],
                    help="c2: the headline line (default); c3 / c4: the 5-bit and streaming-cache "
-                        "configurations, one line each")
+                        "configurations, one line each; k1c: the K-score grid against the reference's "
+                        "published cells")
+    p.add_argument("--k1c-model", default="Qwen3-30B-A3B", choices=["Qwen3-30B-A3B", "Gemma4-26B-A4B"])
     p.add_argument("--slots", type=int, default=2, help="c4: attention slots measured (each the same work)")
     p.add_argument("--stats-summary", metavar="DIR",
                    help="c3 / c4: turn a rocprofv3 --kernel-trace --stats run of that workload under DIR "
@@ -496,6 +498,89 @@ def main_c3(args):
     print(json.dumps(result), flush=True)
 
 
+K1C_MODELS = {"Qwen3-30B-A3B": dict(n_kv=8, head_dim=128, n_q=32), "Gemma4-26B-A4B": dict(n_kv=8, head_dim=256, n_q=32)}
+K1C_BATCH = [1, 8, 32, 64]
+K1C_CTX = [2048, 8192, 32768, 65536]
+K1C_RECIPES = [("nsn", 5, False), ("kivi", 5, False), ("kivi", 4, False), ("nsn", 4, False), ("fp16", 16, False),
+               ("nsn", 5, True), ("nsn", 3, True)]   # (recipe, bits, bit-packed codes)
+K1C_HEADLINE = (32, 32768, "nsn", 5)
+
+
+def main_k1c(args):
+    """The reference's K-score grid (experiments/kernels/phase_k1c_triton_fused_kernel.py:
+    Qwen3-30B-A3B or Gemma4 shape, B in {1, 8, 32, 64}, ctx in {2K .. 64K}, recipes
+    NSN5 / KIVI5 / KIVI4 / NSN4 / fp16 on u8 codes, plus NSN5 and NSN3 on
+    bit-packed codes), timed as the reference times it (30 warm-up calls, then
+    the median of 100 calls each bracketed by events), against the published
+    latencies (tests/golden/k1c_published.json, RTX PRO 6000 Blackwell).  K is
+    N(0,1) from a GPU generator (the reference draws the same distribution on
+    the CPU); the store is built on the GPU.  One JSON line: value = the
+    B=32 / 32K / NSN5 cell."""
+    import torch
+    from nsn_amd import kscore
+    dev = torch.device("cuda:0")
+    model = K1C_MODELS[args.k1c_model]
+    n_kv, hd, n_q = model["n_kv"], model["head_dim"], model["n_q"]
+    pub = json.loads((ROOT / "tests" / "golden" / "k1c_published.json").read_text())
+    published = {(c["batch"], c["ctx"], c["recipe"], c["bits"]): c["latency_ms_median"]
+                 for c in pub["cells"] if c["model"] == args.k1c_model}
+    stream = torch.cuda.current_stream()
+    cells = []
+    for B in K1C_BATCH:
+        for T in K1C_CTX:
+            gen = torch.Generator(device=dev).manual_seed(20260510 + B * 131 + T)
+            q = torch.randn((B, n_q, hd), generator=gen, device=dev).to(torch.float16)
+            k = torch.randn((B, T, n_kv * hd), generator=gen, device=dev)
+            for recipe, bits, packed in K1C_RECIPES:
+                ref, ts = kscore.make_store(k, bits, recipe, n_kv, hd, dev)
+                del ref
+                if packed:
+                    ts = kscore.pack_store(ts, bits)
+                out = torch.empty((B, n_q, T), dtype=torch.float32, device=dev)
+                fn = lambda: kscore.decode_scores(q, ts, n_q, n_kv, hd, out=out)
+                for _ in range(30):
+                    fn()
+                torch.cuda.synchronize()
+                samples = []
+                for _ in range(100):
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    fn()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    samples.append(e0.elapsed_time(e1))
+                med = sorted(samples)[len(samples) // 2]
+                nbytes = (ts["code"].numel() * ts["code"].element_size() + out.numel() * 4 + q.numel() * 2
+                          + (0 if recipe == "fp16" else 2 * 2 * B * n_kv * hd)
+                          + (2 * B * n_kv * T if recipe == "nsn" else 0))
+                pm = None if packed else published.get((B, T, recipe, bits))
+                cell = {"batch": B, "ctx": T, "recipe": recipe, "bits": bits, "codes": "packed" if packed else
+                        ("fp16" if recipe == "fp16" else "u8"), "ms": round(med, 5), "gbs": round(nbytes / med / 1e6, 1),
+                        "published_ms": pm, "ratio_vs_published": round(med / pm, 4) if pm else None}
+                cells.append(cell)
+                log(f"[bench] k1c B={B:>2} T={T:>5} {recipe}{bits}{'p' if packed else ' '}: {med * 1e3:8.1f} us "
+                    f"{cell['gbs']:7.1f} GB/s" + (f"  published {pm * 1e3:8.1f} us  x{pm / med:5.2f}" if pm else ""))
+                del ts, out
+            del q, k
+            torch.cuda.empty_cache()
+    hb, ht, hr, hbits = K1C_HEADLINE
+    head = next(c for c in cells if (c["batch"], c["ctx"], c["recipe"], c["bits"], c["codes"]) == (hb, ht, hr, hbits, "u8"))
+    result = {
+        "metric": f"K1c K-score ms/call ({args.k1c_model}: {n_q}q/{n_kv}kv, d={hd}; B={hb}, ctx {ht}, NSN{hbits} u8 codes)",
+        "value": head["ms"], "unit": "ms", "n_gpus": 1, "steps": 100, "warmup": 30, "ms_per_step": head["ms"],
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": head["ratio_vs_published"],
+        "baseline": {"value": head["published_ms"], "device": pub["device"], "source": pub["source"]},
+        "dtype": "f16", "data": "synthetic (K ~ N(0,1), GPU generator; the store built on the GPU)",
+        "config": {"workload": "K1c K-score grid", "model": args.k1c_model, "heads_q": n_q, "heads_kv": n_kv,
+                   "head_dim": hd},
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "kscore (u8 NSN5)"},
+        "grid": cells,
+    }
+    print(json.dumps(result), flush=True)
+
+
 C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
 
 
@@ -664,6 +749,9 @@ def main():
         return
     if args.workload == "c4":
         main_c4(args)
+        return
+    if args.workload == "k1c":
+        main_k1c(args)
         return
     import numpy as np
     import torch

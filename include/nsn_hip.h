@@ -261,6 +261,41 @@ int nsn_tail_append(const void *k_new, const void *v_new, int64_t rows, int64_t 
 int nsn_finite_scan(int n_arrays, const void *const *ptrs, const int64_t *counts,
                     const int *dtypes, int32_t *flags, int32_t *status, nsn_stream_t stream);
 
+/*
+ * K-score decode (the K side of one decode query, scores only) over the K1c
+ * cache layout.  Replaces `_fused_score_kernel` and its launcher
+ * `triton_decode_scores` (experiments/kernels/phase_k1c_triton_fused_kernel.py:207-281):
+ *   out[b, h, t] = scale * en[b, hkv, t] * sum_d q[b, h, d] * (code[b, t, hkv*D + d] * step[b, hkv*D + d]
+ *                                                              + min[b, hkv*D + d]),   hkv = h / (Hq / Hkv)
+ * with en = 1 when eff_norm is NULL (KIVI), and K itself for NSN_KS_FP16.
+ * Layouts (all contiguous):
+ *   q        fp16 [B, Hq, D]
+ *   codes    NSN_KS_U8:     u8 [B, T, Hkv*D] (one code per byte, the reference's layout)
+ *            NSN_KS_PACKED: the same codes bit-packed LSB-first along each token
+ *                           row, [B, T, Hkv*D*bits/8] (bits 3, 4, 5)
+ *            NSN_KS_FP16:   fp16 K [B, T, Hkv*D]
+ *   mins, steps  fp16 [B, Hkv*D] (unused for NSN_KS_FP16)
+ *   eff_norm fp16 [B, Hkv, T] or NULL
+ *   out      fp32 [B, Hq, T]
+ * D is 128 or 256; Hq / Hkv <= 8.  codes 16-byte aligned when a lane's D/4
+ * channels span a multiple of 16 bytes (u8, 4-bit, fp16), else 4-byte.
+ */
+enum { NSN_KS_U8 = 0, NSN_KS_PACKED = 1, NSN_KS_FP16 = 2 };
+
+typedef struct {
+    const void *q;
+    int64_t batch, heads_q, heads_kv, head_dim, T;
+    int mode;                /* NSN_KS_* */
+    int bits;                /* NSN_KS_PACKED: 3, 4 or 5 */
+    const void *codes;
+    const void *mins, *steps;
+    const void *eff_norm;
+    float scale;             /* 1 / sqrt(D) in the reference */
+    float *out;
+} nsn_kscore_args;
+
+int nsn_kscore(const nsn_kscore_args *args, nsn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

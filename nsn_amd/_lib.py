@@ -54,6 +54,14 @@ class PrefillArgs(ctypes.Structure):
                 ("k_chunk", P), ("v_chunk", P), ("out", P), ("status", P)]
 
 
+class KScoreArgs(ctypes.Structure):
+    _fields_ = [("q", P), ("batch", I64), ("heads_q", I64), ("heads_kv", I64), ("head_dim", I64), ("T", I64),
+                ("mode", I32), ("bits", I32), ("codes", P), ("mins", P), ("steps", P), ("eff_norm", P),
+                ("scale", ctypes.c_float), ("out", P)]
+
+
+KS_U8, KS_PACKED, KS_FP16 = 0, 1, 2
+
 # symbol -> (restype, argtypes); must cover every function include/nsn_hip.h declares
 SIGNATURES = {
     "nsn_version": (ctypes.c_char_p, []),
@@ -68,6 +76,7 @@ SIGNATURES = {
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
     "nsn_prefill_attention": (I32, [ctypes.POINTER(PrefillArgs), P]),
     "nsn_tail_append": (I32, [P, P, I64, I64, I64, P, P, I64, I64, I32, P]),
+    "nsn_kscore": (I32, [ctypes.POINTER(KScoreArgs), P]),
 }
 
 _lib = None

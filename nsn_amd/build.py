@@ -18,7 +18,7 @@ PKG = Path(__file__).resolve().parent
 SRC = PKG / "csrc"
 OUT_DIR = PKG / "_build"
 LIB = OUT_DIR / "libnsn_hip.so"
-SOURCES = ["nsn_codec.hip", "nsn_attn.hip", "nsn_fast.hip", "nsn_prefill.hip", "nsn_cache.hip"]
+SOURCES = ["nsn_codec.hip", "nsn_attn.hip", "nsn_fast.hip", "nsn_prefill.hip", "nsn_cache.hip", "nsn_kscore.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

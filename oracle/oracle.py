@@ -305,3 +305,29 @@ def restore_blocks_f32(codes_packed, n16, m16, s16, bits):
     q = unpack_codes(cp.reshape(-1), nb * BLOCK * DIM, bits).reshape(lead + (BLOCK, DIM))
     return nsn_decode_f32(q, n16.reshape(lead + (BLOCK, 1)), m16.reshape(lead + (1, DIM)),
                           s16.reshape(lead + (1, DIM)))
+
+
+def kscore64(q, code, mins, steps, eff_norm, n_kv, head_dim):
+    """fp64 K-score oracle of the K1c component (reference
+    ``experiments/kernels/phase_k1c_triton_fused_kernel.py``: dequant
+    ``code * step + min`` (:112-113, :240-241), per-token ``eff_norm`` (:104-108,
+    :244-247), scores ``q . k / sqrt(D)`` with the GQA map ``hkv = h // (Hq/Hkv)``
+    (:150-164, :230)).
+
+    q [B, Hq, D]; code [B, T, Hkv*D] (codes, or K itself with mins = None);
+    mins / steps [B, Hkv*D] or None; eff_norm [B, Hkv, T] or None.
+    Returns float64 scores [B, Hq, T].  Pinned in tests/test_oracle.py by
+    brute-force loops, closed forms (zero codes, one-hot queries) and the GQA
+    repeat invariant."""
+    q = np.asarray(q, np.float64)
+    B, Hq, D = q.shape
+    c = np.asarray(code, np.float64)
+    T = c.shape[1]
+    k = c if mins is None else c * np.asarray(steps, np.float64)[:, None, :] + np.asarray(mins, np.float64)[:, None, :]
+    k = k.reshape(B, T, n_kv, head_dim)
+    G = Hq // n_kv
+    qx = q.reshape(B, n_kv, G, D)
+    s = np.einsum("bngd,btnd->bngt", qx, k) / np.sqrt(head_dim)
+    if eff_norm is not None:
+        s = s * np.asarray(eff_norm, np.float64)[:, :, None, :]
+    return s.reshape(B, Hq, T)
