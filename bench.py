@@ -66,6 +66,7 @@ def parse():
                         "configurations, one line each; k1c: the K-score grid against the reference's "
                         "published cells")
     p.add_argument("--k1c-model", default="Qwen3-30B-A3B", choices=["Qwen3-30B-A3B", "Gemma4-26B-A4B"])
+    p.add_argument("--k1c-quick", action="store_true", help="k1c: only ctx 32768 at B = 8 and 32")
     p.add_argument("--slots", type=int, default=2, help="c4: attention slots measured (each the same work)")
     p.add_argument("--stats-summary", metavar="DIR",
                    help="c3 / c4: turn a rocprofv3 --kernel-trace --stats run of that workload under DIR "
@@ -526,8 +527,8 @@ def main_k1c(args):
                  for c in pub["cells"] if c["model"] == args.k1c_model}
     stream = torch.cuda.current_stream()
     cells = []
-    for B in K1C_BATCH:
-        for T in K1C_CTX:
+    for B in ([8, 32] if args.k1c_quick else K1C_BATCH):
+        for T in ([32768] if args.k1c_quick else K1C_CTX):
             gen = torch.Generator(device=dev).manual_seed(20260510 + B * 131 + T)
             q = torch.randn((B, n_q, hd), generator=gen, device=dev).to(torch.float16)
             k = torch.randn((B, T, n_kv * hd), generator=gen, device=dev)

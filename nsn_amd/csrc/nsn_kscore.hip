@@ -25,7 +25,7 @@
 // owns token column l % 16 and the contiguous channel block g*D/4 .. of lane
 // group g = l / 16 (the MFMA k order is permuted to match, in A and B alike),
 // so each lane reads D/4 consecutive codes of its token per tile.  Four tiles
-// are in flight per wave.
+// are in flight per wave; the kv-heads of one chunk are consecutive waves.
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -116,15 +116,17 @@ __device__ __forceinline__ void b_frags(const Tile<D, MODE, BITS> &r, u32x4 (&B)
 }
 
 template <int D, int MODE, int BITS, bool NSN>
-__global__ __launch_bounds__(256) void kscore_kernel(KsParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 4 : 2))) void kscore_kernel(KsParams p) {
     using SH = Shape<D, MODE, BITS>;
     constexpr int CPL = SH::CPL, NK = SH::NK, NW = SH::NW, PF = SH::PF;
     const int l = threadIdx.x & 63;
+    // wave -> (sequence, chunk, kv-head), kv-head fastest: the waves of one
+    // chunk read the same token rows, each its kv-head's slice, together whole rows
     const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int64_t s = wid / p.n_chunks, chunk = wid - s * p.n_chunks;
-    if (s >= p.batch * p.heads_kv) return;   // (whole wave)
-    const int64_t b = s / p.heads_kv;
-    const int hkv = static_cast<int>(s - b * p.heads_kv);
+    const int64_t sc = wid / p.heads_kv;
+    const int hkv = static_cast<int>(wid - sc * p.heads_kv);
+    const int64_t b = sc / p.n_chunks, chunk = sc - b * p.n_chunks;
+    if (b >= p.batch) return;   // (whole wave)
     const int G = p.group;
     const int row = l & 15, grp = l >> 4;
     const int64_t T = p.T;
