@@ -67,6 +67,9 @@ def parse():
                         "published cells")
     p.add_argument("--k1c-model", default="Qwen3-30B-A3B", choices=["Qwen3-30B-A3B", "Gemma4-26B-A4B"])
     p.add_argument("--k1c-quick", action="store_true", help="k1c: only ctx 32768 at B = 8 and 32")
+    p.add_argument("--k1c-summary", metavar="DIR",
+                   help="turn a rocprofv3 --kernel-trace run of `--workload k1c --k1c-quick` under DIR "
+                        "into profiles/kscore_k1c.md")
     p.add_argument("--slots", type=int, default=2, help="c4: attention slots measured (each the same work)")
     p.add_argument("--stats-summary", metavar="DIR",
                    help="c3 / c4: turn a rocprofv3 --kernel-trace --stats run of that workload under DIR "
@@ -582,6 +585,50 @@ def main_k1c(args):
     print(json.dumps(result), flush=True)
 
 
+def k1c_summary(d):
+    """profiles/kscore_k1c.md from the kernel trace of `bench.py --workload k1c
+    --k1c-quick`: the kernel's own duration per cell (its 130 launches in
+    order: 30 warm-up, then the 100 timed ones, whose median is reported)."""
+    rows = _rows((Path(d), "**/*kernel_trace.csv"))
+    ks = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in rows
+                 if "kscore_kernel" in r["Kernel_Name"]))
+    model = K1C_MODELS["Qwen3-30B-A3B"]
+    pub = json.loads((ROOT / "tests" / "golden" / "k1c_published.json").read_text())
+    published = {(c["batch"], c["ctx"], c["recipe"], c["bits"]): c["latency_ms_median"]
+                 for c in pub["cells"] if c["model"] == "Qwen3-30B-A3B"}
+    cells = [(B, 32768, r, b, pk) for B in (8, 32) for r, b, pk in K1C_RECIPES]
+    if len(ks) != 130 * len(cells):
+        raise SystemExit(f"expected {130 * len(cells)} kscore dispatches, found {len(ks)}")
+    L = ["# kscore_kernel on the K1c grid (Qwen3-30B-A3B shape: 32q/8kv, d=128, ctx 32768)", "",
+         "Command (repository root, one MI355X; `OUT` = an output folder):", "", "```",
+         "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload k1c --k1c-quick",
+         "python3 bench.py --k1c-summary OUT      # writes this file", "```", "",
+         "Kernel duration from the trace: the median of each cell's 100 timed launches (after 30 warm-up "
+         "launches).  Bytes: codes + scores (fp32) + q + min/step + eff_norm.  Published: the reference's "
+         f"Triton kernel on {pub['device']} (event-timed calls, median of 100).", "",
+         "| B | recipe | codes | kernel | us (median) | GB/s | % of 8 TB/s | published us |", "|---|---|---|---|---|---|---|---|"]
+    n_kv, hd, n_q = model["n_kv"], model["head_dim"], model["n_q"]
+    for i, (B, T, recipe, bits, packed) in enumerate(cells):
+        part = ks[130 * i + 30:130 * (i + 1)]
+        durs = sorted((e - b0) / 1e3 for b0, e, _ in part)
+        med = durs[len(durs) // 2]
+        name = part[0][2]
+        kern = name[name.index("<"):name.index(">") + 1] if "<" in name else name
+        code_b = B * T * n_kv * hd * (2 if recipe == "fp16" else (bits / 8 if packed else 1))
+        nbytes = code_b + B * n_q * T * 4 + B * n_q * hd * 2 + (0 if recipe == "fp16" else 4 * B * n_kv * hd) + \
+            (2 * B * n_kv * T if recipe == "nsn" else 0)
+        pm = None if packed else published.get((B, T, recipe, bits))
+        L.append(f"| {B} | {recipe}{bits if recipe != 'fp16' else ''} | {'packed' if packed else ('fp16' if recipe == 'fp16' else 'u8')} "
+                 f"| `{kern}` | {med:.1f} | {nbytes / med / 1e3:.0f} | {nbytes / med / 1e3 / HBM_PEAK_GBS * 100:.1f} | "
+                 f"{pm * 1e3:.1f} |" if pm else
+                 f"| {B} | {recipe}{bits if recipe != 'fp16' else ''} | {'packed' if packed else ('fp16' if recipe == 'fp16' else 'u8')} "
+                 f"| `{kern}` | {med:.1f} | {nbytes / med / 1e3:.0f} | {nbytes / med / 1e3 / HBM_PEAK_GBS * 100:.1f} | -- |")
+    L.append("")
+    out = ROOT / "profiles" / "kscore_k1c.md"
+    out.write_text("\n".join(L))
+    print("\n".join(L))
+
+
 C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
 
 
@@ -750,6 +797,9 @@ def main():
         return
     if args.workload == "c4":
         main_c4(args)
+        return
+    if args.k1c_summary:
+        k1c_summary(args.k1c_summary)
         return
     if args.workload == "k1c":
         main_k1c(args)
