@@ -34,7 +34,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kQTile = 128;   // chunk queries per workgroup
+constexpr int kWaves = 8;                // waves per workgroup
+constexpr int kQTile = 32 * kWaves;      // chunk queries per workgroup
 constexpr int kKP = 136;      // K' row pitch (halves): 272 B rows
 constexpr int kVP = 72;       // V'^T row pitch (halves): 144 B rows
 constexpr float kLog2e = 1.4426950408889634f;
@@ -139,13 +140,13 @@ template <int BITS> struct Stage {
 };
 
 // DMA of packed block ib of (b, kvh) into one stage; instruction i of the
-// block is issued by wave i % 4.
+// block is issued by wave i % kWaves.
 template <int BITS>
 __device__ __forceinline__ void stage_block(const PrefillParams &p, int64_t rk, int64_t rv, int wave, int l,
                                             uint8_t *st) {
     using S = Stage<BITS>;
     const int q = l & 15;
-    for (int i = wave; i < S::NI; i += 4) {
+    for (int i = wave; i < S::NI; i += kWaves) {
         if (i < S::NB / 1024) {
             dma16(p.k.codes + rk * S::NB + 1024 * i + 16 * l, st + 1024 * i);
         } else if (i < 2 * S::NB / 1024) {
@@ -162,114 +163,128 @@ __device__ __forceinline__ void stage_block(const PrefillParams &p, int64_t rk, 
     }
 }
 
-// Fill K' and V'^T from a dense token source x (row pitch 128, `valid` rows;
-// rows past it are zero).  Thread: tokens 4*rg .. 4*rg+3, channels 8*cg ..
+// The block buffer compute reads: K' [64 tok][kKP], V'^T [128 ch][kVP], and
+// (when the factors are not folded in) the K / V decode factors.
+struct KV {
+    uint16_t *kt, *vt;
+    float *fac;   // [K 64 | V 64]
+};
+
+// Fill one side of a KV buffer from a dense token source x (row pitch 128,
+// `valid` rows; rows past it are zero).  Thread: tokens 4*rg .. 4*rg+3,
+// channels 8*cg .. 8*cg+7; side 0 writes K' rows, side 1 V'^T columns.
+// (Dense tokens carry no decode factor: compute applies kv.fac to packed
+// blocks only.)
 template <int BITS, int DT>
-__device__ __forceinline__ void fill_dense(const uint16_t *xk, const uint16_t *xv, int valid, int rg, int cg,
-                                          uint16_t *kt, uint16_t *vt) {
+__device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int side, int rg, int cg, const KV &kv) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
     float vprev[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = 4 * rg + i;
-        float kf[8], vf[8];
+        float f[8];
         if (t < valid) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(xk + static_cast<int64_t>(t) * kDim + 8 * cg);
-            const uint4 c = *reinterpret_cast<const uint4 *>(xv + static_cast<int64_t>(t) * kDim + 8 * cg);
-            const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wc[4] = {c.x, c.y, c.z, c.w};
+            const uint4 a = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(t) * kDim + 8 * cg);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t ka = static_cast<uint16_t>(wa[e >> 1] >> (16 * (e & 1)));
-                const uint16_t va = static_cast<uint16_t>(wc[e >> 1] >> (16 * (e & 1)));
-                kf[e] = Elem<DT>::load(ka);
-                vf[e] = Elem<DT>::load(va);
-            }
+            for (int e = 0; e < 8; ++e) f[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kf[e] = vf[e] = 0.f;
+            for (int e = 0; e < 8; ++e) f[e] = 0.f;
         }
-        uint4 kw;
-        kw.x = pk16(kf[O::chE[0]], kf[O::chE[1]]);
-        kw.y = pk16(kf[O::chE[2]], kf[O::chE[3]]);
-        kw.z = pk16(kf[O::chE[4]], kf[O::chE[5]]);
-        kw.w = pk16(kf[O::chE[6]], kf[O::chE[7]]);
-        *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) = kw;
+        if (side == 0) {
+            *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
+                uint4{pk16(f[O::chE[0]], f[O::chE[1]]), pk16(f[O::chE[2]], f[O::chE[3]]),
+                      pk16(f[O::chE[4]], f[O::chE[5]]), pk16(f[O::chE[6]], f[O::chE[7]])};
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            if (i & 1) vcol[e][i >> 1] = pk16(vprev[e], vf[e]);
-            else vprev[e] = vf[e];
+            for (int e = 0; e < 8; ++e) {
+                if (i & 1) vcol[e][i >> 1] = pk16(vprev[e], f[e]);
+                else vprev[e] = f[e];
+            }
         }
     }
+    if (side == 1) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<u32x2 *>(vt + (8 * cg + e) * kVP + 4 * rg) = u32x2{vcol[e][0], vcol[e][1]};
+        for (int e = 0; e < 8; ++e)
+            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + e) * kVP + 4 * rg) = u32x2{vcol[e][0], vcol[e][1]};
+    }
 }
 
-// Fill K' and V'^T from a staged packed block: direction m + s*z per element
-// (one fma with the code as an exact fp16 subnormal, scaled back by 2^(24-k)).
-template <int BITS>
-__device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, uint16_t *kt, uint16_t *vt) {
+// Fill one side of a KV buffer from a staged packed block: direction m + s*z
+// per element (one fma with the code as an exact fp16 subnormal, scaled back
+// by 2^(24-k)), times the token's decode factor when FOLD (fp16 data: the
+// product is the reconstructed value itself, within fp16 range by
+// construction); otherwise the factors go to kv.fac for the compute phase.
+template <int BITS, bool FOLD>
+__device__ __forceinline__ void fill_packed(const uint8_t *st, int side, int rg, int cg, const KV &kv) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
     constexpr int ROWB = BITS * 16;   // code bytes per token row
-    const uint4 km4 = *reinterpret_cast<const uint4 *>(st + S::META + 16 * cg);
-    const uint4 ks4 = *reinterpret_cast<const uint4 *>(st + S::META + 256 + 16 * cg);
-    const uint4 vm4 = *reinterpret_cast<const uint4 *>(st + S::META + 512 + 16 * cg);
-    const uint4 vs4 = *reinterpret_cast<const uint4 *>(st + S::META + 768 + 16 * cg);
-    const uint32_t KM[4] = {km4.x, km4.y, km4.z, km4.w}, KS[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
-    const uint32_t VM[4] = {vm4.x, vm4.y, vm4.z, vm4.w}, VS[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
-    float kmE[8], ksE[8], vmE[8], vsE[8];   // per element p (channel chE[p])
+    const uint4 m4 = *reinterpret_cast<const uint4 *>(st + S::META + 512 * side + 16 * cg);
+    const uint4 s4 = *reinterpret_cast<const uint4 *>(st + S::META + 512 * side + 256 + 16 * cg);
+    const float4 f4 = *reinterpret_cast<const float4 *>(st + S::META + 1024 + 256 * side + 16 * rg);
+    const float fac[4] = {f4.x, f4.y, f4.z, f4.w};
+    const uint32_t M[4] = {m4.x, m4.y, m4.z, m4.w}, SC[4] = {s4.x, s4.y, s4.z, s4.w};
+    float mE[8], sE[8];   // per element p (channel chE[p])
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
         const int c = O::chE[p];
-        const float sc = static_cast<float>(1u << (24 - O::kE[p]));
-        kmE[p] = h16(KM[c >> 1], c & 1);
-        ksE[p] = h16(KS[c >> 1], c & 1) * sc;
-        vmE[p] = h16(VM[c >> 1], c & 1);
-        vsE[p] = h16(VS[c >> 1], c & 1) * sc;
+        mE[p] = h16(M[c >> 1], c & 1);
+        sE[p] = h16(SC[c >> 1], c & 1) * static_cast<float>(1u << (24 - O::kE[p]));
     }
-    uint32_t vcol[8][2];   // V'^T: per channel, tokens (4rg, 4rg+1), (4rg+2, 4rg+3) as fp16 pairs
+    const uint8_t *codes = st + S::NB * side;
+    uint32_t vcol[8][2];
+    float vprev[8];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        float vd[2][8];
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * rg + i;
+        uint32_t b[4];
+        codes8<BITS>(codes + t * ROWB, cg, b);
+        float d[8];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int t = 4 * rg + 2 * k + h;
-            uint32_t bk[4], bv[4];
-            codes8<BITS>(st + t * ROWB, cg, bk);
-            codes8<BITS>(st + S::NB + t * ROWB, cg, bv);
-            float kd[8];
+        for (int p = 0; p < 8; ++p) {
+            d[p] = __builtin_fmaf(h16(b[p >> 1], p & 1), sE[p], mE[p]);
+            if (FOLD) d[p] *= fac[i];
+        }
+        if (side == 0) {
+            *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
+                uint4{pk16(d[0], d[1]), pk16(d[2], d[3]), pk16(d[4], d[5]), pk16(d[6], d[7])};
+        } else {
 #pragma unroll
             for (int p = 0; p < 8; ++p) {
-                kd[p] = __builtin_fmaf(h16(bk[p >> 1], p & 1), ksE[p], kmE[p]);
-                vd[h][p] = __builtin_fmaf(h16(bv[p >> 1], p & 1), vsE[p], vmE[p]);
+                if (i & 1) vcol[p][i >> 1] = pk16(vprev[p], d[p]);
+                else vprev[p] = d[p];
             }
-            *reinterpret_cast<uint4 *>(kt + t * kKP + 8 * cg) =
-                uint4{pk16(kd[0], kd[1]), pk16(kd[2], kd[3]), pk16(kd[4], kd[5]), pk16(kd[6], kd[7])};
         }
-#pragma unroll
-        for (int p = 0; p < 8; ++p) vcol[p][k] = pk16(vd[0][p], vd[1][p]);
     }
+    if (side == 1) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
-        *reinterpret_cast<u32x2 *>(vt + (8 * cg + O::chE[p]) * kVP + 4 * rg) = u32x2{vcol[p][0], vcol[p][1]};
+        for (int p = 0; p < 8; ++p)
+            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + O::chE[p]) * kVP + 4 * rg) = u32x2{vcol[p][0], vcol[p][1]};
+    }
+    if (!FOLD && cg == 0) *reinterpret_cast<float4 *>(kv.fac + 64 * side + 4 * rg) = f4;
 }
 
 template <int BITS, int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
-    __shared__ __align__(16) uint16_t kt[kBlockTok * kKP];
-    __shared__ __align__(16) uint16_t vt[kDim * kVP];
+    // fp16 data: the decode factors are folded into K' / V'^T when they are filled
+    constexpr bool FOLD = DT == NSN_DTYPE_F16;
+    __shared__ __align__(16) uint16_t kt[2][kBlockTok * kKP];
+    __shared__ __align__(16) uint16_t vt[2][kDim * kVP];
+    __shared__ __align__(16) float fac[2][2 * kBlockTok];
     __shared__ __align__(16) uint8_t stg[2][S::BYTES];
 
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: the DMA targets are scalar)
     const int row = l & 15, g = l >> 4;
-    // fill role: each 16-lane LDS pass covers all 16 token groups of one channel
-    // group, so its transposed V'^T writes are one contiguous 128-byte row
-    const int rg = tid & 15, cg = tid >> 4;
+    // fill role: threads 0..255 fill K', 256..511 V'^T; each 16-lane LDS pass covers
+    // all 16 token groups of one channel group (V'^T writes: one contiguous 128-byte row)
+    const int side = tid >> 8;
+    const int rg = tid & 15, cg = (tid >> 4) & 15;
     const int b = blockIdx.z, hq = blockIdx.y;
     const int kvh = hq / p.group;
     const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQTile;
@@ -322,35 +337,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     bool bad = false;
 
-    if (nb > 0) stage_block<BITS>(p, seqrow * p.k.block_cap, seqrow * p.v.block_cap, wave, l, stg[0]);
-
-    for (int64_t j = 0; j < nblk; ++j) {
-        // staged block j (all waves' DMA) is in; K'/V'^T are free
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const bool packed = j < nb;
-        if (j + 1 < nb)
-            stage_block<BITS>(p, seqrow * p.k.block_cap + j + 1, seqrow * p.v.block_cap + j + 1, wave, l,
-                              stg[(j + 1) & 1]);
-        // token range of block j: positions relative to its source
-        int valid;            // rows of the block in use
-        int64_t cpos = -1;    // chunk position of the block's first token (chunk blocks), else -1
-        if (packed) {
+    // Block j: packed (j < nb), tail (nb <= j < nb + nt_blk), or chunk; its rows
+    // in use and (chunk blocks) the chunk position of its first token.
+    auto block_rows = [&](int64_t j, int &valid, int64_t &cpos) {
+        cpos = -1;
+        if (j < nb) {
             valid = kBlockTok;
-            fill_packed<BITS>(stg[j & 1], rg, cg, kt, vt);
         } else if (j < nb + nt_blk) {
             const int64_t t0 = (j - nb) * kBlockTok;
             valid = static_cast<int>((ntail - t0 < kBlockTok) ? ntail - t0 : kBlockTok);
-            fill_dense<BITS, DT>(p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim,
-                                 p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim, valid, rg, cg, kt, vt);
         } else {
             cpos = (j - nb - nt_blk) * kBlockTok;
             valid = static_cast<int>((qend - cpos < kBlockTok) ? qend - cpos : kBlockTok);
-            fill_dense<BITS, DT>(p.kc + (seqrow * p.n_q + cpos) * kDim, p.vc + (seqrow * p.n_q + cpos) * kDim,
-                                 valid, rg, cg, kt, vt);
         }
+    };
+    // Fill block j into KV buffer j & 1 (its raw stage j & 1 when packed).
+    auto fill = [&](int64_t j) {
+        const KV kv{kt[j & 1], vt[j & 1], fac[j & 1]};
+        if (j < nb) {
+            fill_packed<BITS, FOLD>(stg[j & 1], side, rg, cg, kv);
+        } else {
+            int valid;
+            int64_t cpos;
+            block_rows(j, valid, cpos);
+            const uint16_t *src;
+            if (cpos < 0) {
+                const int64_t t0 = (j - nb) * kBlockTok;
+                src = side ? p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim : p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim;
+            } else {
+                src = (side ? p.vc : p.kc) + (seqrow * p.n_q + cpos) * kDim;
+            }
+            fill_dense<BITS, DT>(src, valid, side, rg, cg, kv);
+        }
+    };
+
+    // ---- prologue: raw block 0 staged and filled, raw block 1 in flight
+    if (nb > 0) stage_block<BITS>(p, seqrow * p.k.block_cap, seqrow * p.v.block_cap, wave, l, stg[0]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (nb > 1) stage_block<BITS>(p, seqrow * p.k.block_cap + 1, seqrow * p.v.block_cap + 1, wave, l, stg[1]);
+    fill(0);
+
+    // ---- one barrier per block: compute block j from KV buffer j & 1 while
+    // filling block j + 1 into the other and staging raw block j + 2
+    for (int64_t j = 0; j < nblk; ++j) {
+        // KV buffer j & 1 is filled, raw block j + 1 is in, buffer (j + 1) & 1
+        // and raw stage j & 1 are free
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if (j + 2 < nb)
+            stage_block<BITS>(p, seqrow * p.k.block_cap + j + 2, seqrow * p.v.block_cap + j + 2, wave, l,
+                              stg[j & 1]);
+        if (j + 1 < nblk) fill(j + 1);
         if (qw >= p.n_q) continue;   // (a wave past the chunk end only helps fill)
+        const bool packed = j < nb;
+        int valid;
+        int64_t cpos;
+        block_rows(j, valid, cpos);
+        const uint16_t *ktj = kt[j & 1];
+        const uint16_t *vtj = vt[j & 1];
 
         // ---- S^T[token][query] = K' Q^T
         f32x4 s[4][2];
@@ -360,15 +405,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             for (int qt = 0; qt < 2; ++qt) s[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(kt + (16 * tt + row) * kKP + 32 * ks + 8 * g);
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(ktj + (16 * tt + row) * kKP + 32 * ks + 8 * g);
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) s[tt][qt] = mfma(a, qf[qt][ks], s[tt][qt]);
             }
         }
-        // per-token factors of this lane's tokens 16*tt + 4*g + i (packed blocks)
+        // per-token factors of this lane's tokens 16*tt + 4*g + i (not folded: bf16 data)
         float fk[4][4], fv[4][4];
-        {
-            const float *fks = reinterpret_cast<const float *>(stg[j & 1] + S::META + 1024);
+        if (!FOLD) {
+            const float *fks = fac[j & 1];
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
                 const float4 a = *reinterpret_cast<const float4 *>(fks + 16 * tt + 4 * g);
@@ -384,7 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            if (packed) {
+            if (!FOLD && packed) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
@@ -423,7 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
                 for (int i = 0; i < 4; ++i) {
                     const float e = __builtin_amdgcn_exp2f(s[tt][qt][i] - msafe);
                     ls += e;
-                    pw[tt][i] = packed ? e * fv[tt][i] : e;
+                    pw[tt][i] = (!FOLD && packed) ? e * fv[tt][i] : e;
                 }
             l_run[qt] += ls;
 #pragma unroll
@@ -437,7 +482,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const uint16_t *vr = vt + (16 * ct + row) * kVP + 32 * ks2 + 4 * g;
+                const uint16_t *vr = vtj + (16 * ct + row) * kVP + 32 * ks2 + 4 * g;
                 const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr);
                 const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16);
                 const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
@@ -526,11 +571,11 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool bf = a->dtype == NSN_DTYPE_BF16;
     if (a->bits == 3) {
-        if (bf) hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_BF16>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_F16>), grid, dim3(256), 0, st, p);
+        if (bf) hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p);
+        else hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);
     } else {
-        if (bf) hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_BF16>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_F16>), grid, dim3(256), 0, st, p);
+        if (bf) hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p);
+        else hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);
     }
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }
