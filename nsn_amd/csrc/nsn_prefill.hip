@@ -163,6 +163,14 @@ __device__ __forceinline__ void stage_block(const PrefillParams &p, int64_t rk, 
     }
 }
 
+// V'^T keeps each channel's 64 tokens in the k order of the PV product:
+// token t = 32a + 16h + 4g + i sits at position 32a + 8g + 4h + i, so the 8
+// tokens that lane group g of 32-token step a contracts (4g..4g+3 of both
+// 16-token tiles) are one 16-byte read.  Groups of 4 tokens stay together.
+__device__ __forceinline__ int vpos(int t) {
+    return (t & 32) | ((t & 12) << 1) | ((t & 16) >> 2) | (t & 3);
+}
+
 // The block buffer compute reads: K' [64 tok][kKP], V'^T [128 ch][kVP], and
 // (when the factors are not folded in) the K / V decode factors.
 struct KV {
@@ -175,8 +183,8 @@ struct KV {
 // channels 8*cg .. 8*cg+7; side 0 writes K' rows, side 1 V'^T columns.
 // (Dense tokens carry no decode factor: compute applies kv.fac to packed
 // blocks only.)
-template <int BITS, int DT>
-__device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int side, int rg, int cg, const KV &kv) {
+template <int BITS, int DT, int side>
+__device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg, int cg, const KV &kv) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
     float vprev[8];
@@ -193,7 +201,7 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int sid
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = 0.f;
         }
-        if (side == 0) {
+        if constexpr (side == 0) {
             *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
                 uint4{pk16(f[O::chE[0]], f[O::chE[1]]), pk16(f[O::chE[2]], f[O::chE[3]]),
                       pk16(f[O::chE[4]], f[O::chE[5]]), pk16(f[O::chE[6]], f[O::chE[7]])};
@@ -205,10 +213,10 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int sid
             }
         }
     }
-    if (side == 1) {
+    if constexpr (side == 1) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + e) * kVP + 4 * rg) = u32x2{vcol[e][0], vcol[e][1]};
+            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + e) * kVP + vpos(4 * rg)) = u32x2{vcol[e][0], vcol[e][1]};
     }
 }
 
@@ -217,8 +225,8 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int sid
 // by 2^(24-k)), times the token's decode factor when FOLD (fp16 data: the
 // product is the reconstructed value itself, within fp16 range by
 // construction); otherwise the factors go to kv.fac for the compute phase.
-template <int BITS, bool FOLD>
-__device__ __forceinline__ void fill_packed(const uint8_t *st, int side, int rg, int cg, const KV &kv) {
+template <int BITS, bool FOLD, int side>
+__device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, const KV &kv) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
     constexpr int ROWB = BITS * 16;   // code bytes per token row
@@ -235,34 +243,46 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int side, int rg,
         sE[p] = h16(SC[c >> 1], c & 1) * static_cast<float>(1u << (24 - O::kE[p]));
     }
     const uint8_t *codes = st + S::NB * side;
+    // V side (lanes = token groups): rows 4*rg are 48 B = 16 banks apart, so
+    // the lanes of a pass alternate the order of their two token pairs
+    // (4-way instead of 8-way bank sharing on the code reads).  Register slot
+    // s holds pair s ^ pfirst; only the addresses change.
+    const int pfirst = (side == 1) ? ((rg >> 1) & 1) : 0;
     uint32_t vcol[8][2];
     float vprev[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = 4 * rg + i;
-        uint32_t b[4];
-        codes8<BITS>(codes + t * ROWB, cg, b);
-        float d[8];
+    for (int slot = 0; slot < 2; ++slot) {
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            d[p] = __builtin_fmaf(h16(b[p >> 1], p & 1), sE[p], mE[p]);
-            if (FOLD) d[p] *= fac[i];
-        }
-        if (side == 0) {
-            *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
-                uint4{pk16(d[0], d[1]), pk16(d[2], d[3]), pk16(d[4], d[5]), pk16(d[6], d[7])};
-        } else {
+        for (int h = 0; h < 2; ++h) {
+            const int t = 4 * rg + 2 * (slot ^ pfirst) + h;
+            const float ft = pfirst ? fac[2 * (slot ^ 1) + h] : fac[2 * slot + h];
+            uint32_t b[4];
+            codes8<BITS>(codes + t * ROWB, cg, b);
+            float d[8];
 #pragma unroll
             for (int p = 0; p < 8; ++p) {
-                if (i & 1) vcol[p][i >> 1] = pk16(vprev[p], d[p]);
-                else vprev[p] = d[p];
+                d[p] = __builtin_fmaf(h16(b[p >> 1], p & 1), sE[p], mE[p]);
+                if (FOLD) d[p] *= ft;
+            }
+            if constexpr (side == 0) {
+                *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
+                    uint4{pk16(d[0], d[1]), pk16(d[2], d[3]), pk16(d[4], d[5]), pk16(d[6], d[7])};
+            } else {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    if (h) vcol[p][slot] = pk16(vprev[p], d[p]);
+                    else vprev[p] = d[p];
+                }
             }
         }
     }
-    if (side == 1) {
+    if constexpr (side == 1) {
 #pragma unroll
-        for (int p = 0; p < 8; ++p)
-            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + O::chE[p]) * kVP + 4 * rg) = u32x2{vcol[p][0], vcol[p][1]};
+        for (int p = 0; p < 8; ++p) {
+            uint16_t *dst = kv.vt + (8 * cg + O::chE[p]) * kVP + vpos(4 * rg);
+            *reinterpret_cast<uint32_t *>(dst + 2 * pfirst) = vcol[p][0];
+            *reinterpret_cast<uint32_t *>(dst + 2 * (pfirst ^ 1)) = vcol[p][1];
+        }
     }
     if (!FOLD && cg == 0) *reinterpret_cast<float4 *>(kv.fac + 64 * side + 4 * rg) = f4;
 }
@@ -281,10 +301,12 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: the DMA targets are scalar)
     const int row = l & 15, g = l >> 4;
-    // fill role: threads 0..255 fill K', 256..511 V'^T; each 16-lane LDS pass covers
-    // all 16 token groups of one channel group (V'^T writes: one contiguous 128-byte row)
-    const int side = tid >> 8;
-    const int rg = tid & 15, cg = (tid >> 4) & 15;
+    // fill role: threads 0..255 fill K' (lanes over channel groups: each pass
+    // writes whole K' rows), 256..511 V'^T (lanes over token groups: each pass
+    // writes one contiguous V'^T row)
+    const int side = __builtin_amdgcn_readfirstlane(tid >> 8);   // (wave-uniform)
+    const int rg = side ? (tid & 15) : ((tid >> 4) & 15);
+    const int cg = side ? ((tid >> 4) & 15) : (tid & 15);
     const int b = blockIdx.z, hq = blockIdx.y;
     const int kvh = hq / p.group;
     const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQTile;
@@ -355,7 +377,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     auto fill = [&](int64_t j) {
         const KV kv{kt[j & 1], vt[j & 1], fac[j & 1]};
         if (j < nb) {
-            fill_packed<BITS, FOLD>(stg[j & 1], side, rg, cg, kv);
+            if (side) fill_packed<BITS, FOLD, 1>(stg[j & 1], rg, cg, kv);
+            else fill_packed<BITS, FOLD, 0>(stg[j & 1], rg, cg, kv);
         } else {
             int valid;
             int64_t cpos;
@@ -367,7 +390,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             } else {
                 src = (side ? p.vc : p.kc) + (seqrow * p.n_q + cpos) * kDim;
             }
-            fill_dense<BITS, DT>(src, valid, side, rg, cg, kv);
+            if (side) fill_dense<BITS, DT, 1>(src, valid, rg, cg, kv);
+            else fill_dense<BITS, DT, 0>(src, valid, rg, cg, kv);
         }
     };
 
@@ -482,10 +506,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const uint16_t *vr = vtj + (16 * ct + row) * kVP + 32 * ks2 + 4 * g;
-                const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr);
-                const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16);
-                const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(vtj + (16 * ct + row) * kVP + 32 * ks2 + 8 * g);
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma(a, pb[ks2][qt], acc[ct][qt]);
             }
