@@ -27,6 +27,7 @@
 // so each lane reads D/4 consecutive codes of its token per tile.  Four tiles
 // are in flight per wave; the kv-heads of one chunk are consecutive waves.
 #include "nsn_common.hpp"
+#include "nsn_unpack.hpp"
 
 namespace nsn {
 namespace ks {
@@ -73,18 +74,19 @@ struct Tile {
     uint32_t en;   // fp16 bits of en[t] (NSN)
 };
 
-// Unpack 32 LSB-first BITS-bit codes from BITS dwords.
-template <int BITS>
-__device__ __forceinline__ void unpack32(const uint32_t *w, uint32_t (&c)[32]) {
-    constexpr uint32_t mask = (1u << BITS) - 1u;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const int pos = i * BITS, d = pos >> 5, sh = pos & 31;
-        uint32_t v = w[d] >> sh;
-        if (sh + BITS > 32) v |= w[d + 1] << (32 - sh);
-        c[i] = v & mask;
-    }
-}
+// Element order of a K-step's B operand: element e holds channel 8kk + ch(e)
+// of the lane's block, at bit k(e) of its half (identity and 0 for u8 codes
+// and fp16 K; the unpack's windows for bit-packed codes).
+template <int MODE, int BITS, bool PACKED = (MODE == MODE_PACKED)>
+struct Elems {
+    static constexpr int ch(int e) { return e; }
+    static constexpr int k(int) { return 0; }
+};
+template <int MODE, int BITS>
+struct Elems<MODE, BITS, true> {
+    static constexpr int ch(int e) { return unpack::Layout<BITS>::chE[e]; }
+    static constexpr int k(int e) { return unpack::Layout<BITS>::kE[e]; }
+};
 
 // B operands (NK k-steps) of one tile from the lane's raw code dwords.
 template <int D, int MODE, int BITS>
@@ -102,15 +104,16 @@ __device__ __forceinline__ void b_frags(const Tile<D, MODE, BITS> &r, u32x4 (&B)
                           __builtin_amdgcn_perm(y, y, 0x0C010C00u), __builtin_amdgcn_perm(y, y, 0x0C030C02u)};
         }
     } else {
-        // 32 codes per BITS dwords
+        // 32 codes per BITS dwords: byte windows and one AND per pair of codes
 #pragma unroll
         for (int g = 0; g < NK / 4; ++g) {
-            uint32_t c[32];
-            unpack32<BITS>(r.w + g * BITS, c);
+            uint32_t u[BITS];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                B[4 * g + k] = u32x4{c[8 * k] | (c[8 * k + 1] << 16), c[8 * k + 2] | (c[8 * k + 3] << 16),
-                                     c[8 * k + 4] | (c[8 * k + 5] << 16), c[8 * k + 6] | (c[8 * k + 7] << 16)};
+            for (int k = 0; k < BITS; ++k) u[k] = r.w[g * BITS + k];
+            u32x4 Bg[4];
+            unpack::kunpack(u, Bg);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) B[4 * g + k] = Bg[k];
         }
     }
 }
@@ -170,11 +173,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
     u32x4 A[NK];
     {
         const float pw = ldexpf(1.f, sigma);
+        using EL = Elems<MODE, BITS>;
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float a = wv[8 * kk + 2 * j] * pw, c = wv[8 * kk + 2 * j + 1] * pw;
+                // (the code of element e sits at bit k(e): its coefficient carries 2^-k(e))
+                const float a = wv[8 * kk + EL::ch(2 * j)] * ldexpf(pw, -EL::k(2 * j));
+                const float c = wv[8 * kk + EL::ch(2 * j + 1)] * ldexpf(pw, -EL::k(2 * j + 1));
                 uint32_t v;
                 if constexpr (MODE == MODE_FP16) {
                     v = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, c));   // q is fp16: exact

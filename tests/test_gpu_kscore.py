@@ -1,6 +1,6 @@
 """GPU parity of the K-score kernel (nsn_kscore) against the fp64 oracle, for
 the reference's recipes (NSN, KIVI, fp16 K) on u8 codes and on bit-packed
-codes; ragged token counts, GQA 4 and 8, head_dim 128 and 256."""
+codes (3, 4, 5 bits); ragged token counts, GQA 4 and 8, head_dim 128 and 256."""
 import numpy as np
 import pytest
 import torch
@@ -44,9 +44,13 @@ def test_kscore_qwen3_shape(recipe, bits):
         want = _oracle(q, ts, n_kv, D)
         _check(got, want)
         if recipe != "fp16":
-            # the same codes bit-packed: the same B operands, so the same scores bit for bit
+            # the same codes bit-packed (each code at a per-element bit position, its
+            # coefficient scaled by 2^-k to match): the oracle's scores, and the u8
+            # kernel's up to the order of the fp32 sums and the lo parts that the
+            # 2^-k scaling moves into the fp16 subnormal range (~3e-6 of max|score|)
             gp = kscore.decode_scores(q.to(DEV), kscore.pack_store(ts, bits), n_q, n_kv, D)
-            assert torch.equal(gp, got)
+            _check(gp, want)
+            assert (gp - got).abs().max().item() <= 1e-5 * got.abs().max().item()
 
 
 @pytest.mark.parametrize("recipe,bits", [("nsn", 5), ("kivi", 4), ("fp16", 16)])
@@ -57,7 +61,7 @@ def test_kscore_gqa8_and_head_dim_256(recipe, bits):
         _check(got, _oracle(q, ts, n_kv, D))
         if recipe != "fp16":
             gp = kscore.decode_scores(q.to(DEV), kscore.pack_store(ts, bits), n_q, n_kv, D)
-            assert torch.equal(gp, got)
+            _check(gp, _oracle(q, ts, n_kv, D))
 
 
 def test_kscore_long_context():
