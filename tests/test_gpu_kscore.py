@@ -87,3 +87,29 @@ def test_kscore_matches_materialised_reference_scores():
     got = kscore.decode_scores(q.to(DEV), ts, n_q, n_kv, D).cpu()
     rel = ((got - want).abs().max() / want.abs().max()).item()
     assert rel < 1e-4
+
+
+@pytest.mark.parametrize("recipe,bits", [("nsn", 5), ("kivi", 4), ("fp16", 16)])
+def test_kscore_reference_golden_scores(recipe, bits):
+    """The kernel on the reference's own store (tests/golden/k1c.npz, written
+    from phase_k1c_triton_fused_kernel.py) against the reference's fp32
+    scores."""
+    from pathlib import Path
+    G = np.load(Path(__file__).resolve().parent / "golden" / "k1c.npz")
+    key = f"{recipe}{bits}|"
+    f16 = lambda a: torch.from_numpy(np.asarray(a, np.uint16).view(np.int16)).view(torch.float16).to(DEV)
+    q = f16(G[key + "q"]).contiguous()
+    B, n_q, D = q.shape
+    T = G["k"].shape[1]
+    if recipe == "fp16":
+        ts = {"code": f16(G[key + "code"]).contiguous(), "is_fp16": True, "is_nsn": False, "T": T,
+              "n_kv": 8, "head_dim": D}
+    else:
+        ts = {"code": torch.from_numpy(G[key + "code"]).to(DEV).contiguous(), "is_fp16": False,
+              "is_nsn": recipe == "nsn", "min": f16(G[key + "min"]).contiguous(),
+              "step": f16(G[key + "step"]).contiguous(), "T": T, "n_kv": 8, "head_dim": D}
+        if recipe == "nsn":
+            ts["eff_norm"] = f16(G[key + "eff_norm"]).contiguous()
+    got = kscore.decode_scores(q, ts, n_q, 8, D).cpu().double().numpy()
+    ref = G[key + "scores"].astype(np.float64)
+    assert np.abs(got - ref).max() <= REL_MAX * np.abs(ref).max()

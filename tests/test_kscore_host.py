@@ -130,3 +130,45 @@ def test_decode_scores_requires_gpu_tensors():
           "T": 4, "n_kv": 8, "head_dim": 128}
     with pytest.raises(IntegrityError):
         kscore.decode_scores(q, ts, 32, 8, 128)
+
+
+K1C = Path(__file__).resolve().parent / "golden" / "k1c.npz"
+K1C_CELLS = [("nsn", 5), ("kivi", 4), ("fp16", 16)]
+
+
+def _f16(bits):
+    return np.asarray(bits, np.uint16).view(np.float16)
+
+
+@pytest.mark.parametrize("recipe,bits", K1C_CELLS)
+def test_store_matches_reference_goldens(recipe, bits):
+    """The store builders reproduce the reference's make_triton_store bit for
+    bit on its own seeded inputs (tests/golden/make_k1c_goldens.py)."""
+    G = np.load(K1C)
+    key = f"{recipe}{bits}|"
+    k = torch.from_numpy(G["k"])
+    _, ts = kscore.make_store(k, bits, recipe, 8, 128, "cpu")
+    if recipe == "fp16":
+        assert np.array_equal(ts["code"].view(torch.int16).numpy().view(np.uint16), G[key + "code"])
+        return
+    assert np.array_equal(ts["code"].numpy(), G[key + "code"])
+    assert np.array_equal(ts["min"].view(torch.int16).numpy().view(np.uint16), G[key + "min"])
+    assert np.array_equal(ts["step"].view(torch.int16).numpy().view(np.uint16), G[key + "step"])
+    if recipe == "nsn":
+        assert np.array_equal(ts["eff_norm"].view(torch.int16).numpy().view(np.uint16), G[key + "eff_norm"])
+
+
+@pytest.mark.parametrize("recipe,bits", K1C_CELLS)
+def test_oracle_matches_reference_scores(recipe, bits):
+    """The fp64 oracle against the reference's own fp32 dequantise-then-score
+    path (_torch_decode_scores) on the golden stores."""
+    G = np.load(K1C)
+    key = f"{recipe}{bits}|"
+    q = _f16(G[key + "q"]).astype(np.float64)
+    if recipe == "fp16":
+        s = O.kscore64(q, _f16(G[key + "code"]), None, None, None, 8, 128)
+    else:
+        en = _f16(G[key + "eff_norm"]) if recipe == "nsn" else None
+        s = O.kscore64(q, G[key + "code"], _f16(G[key + "min"]), _f16(G[key + "step"]), en, 8, 128)
+    ref = G[key + "scores"].astype(np.float64)
+    assert np.abs(s - ref).max() <= 1e-6 * np.abs(ref).max()
