@@ -1,0 +1,329 @@
+"""Decode-time connection of the packed K/V path into a Hugging Face
+transformers model (the reference's AC08 connection, rebuilt).
+
+The reference patches the attention modules of its Ouro model so that a
+single-token decode step appends K/V to its packed cache and reads them back
+through a fused kernel instead of a restored dense copy
+(experiments/ac08/source/loop_kv_ac08_attention.py:46-96); prefill and every
+call without the packed cache keep the original forward.  Here:
+
+- ``PackedKVCache`` is a ``transformers.Cache`` whose per-slot layers are the
+  GPU-resident ``StreamingKVCache`` (preallocated packed blocks + an fp16
+  tail, compressed in place by the reference's policy:
+  ``post_prefill`` / ``post_decode``, loop_kv_pk01_cache.py:122-127).
+  ``update`` (the native route, used by prefill) appends and returns the
+  exact dense reconstruction (restore of the packed blocks + the tail,
+  loop_kv_pk01_cache.py:97-110); ``append_for_attention`` appends without
+  it (loop_kv_ac08_attention.py:20-24).
+- ``install(model)`` patches every ``model.model.layers[i].self_attn`` and
+  returns a function that restores the original bound methods
+  (loop_kv_ac08_attention.py:46-96).  Decode arms
+  (loop_kv_ac08_attention.py:73-85):
+
+  * ``NATIVE``: dense restore of K and V, then the model's own sdpa;
+  * ``PACKED_GROUPED``: packed K, V restored dense (the bridge);
+  * ``PACKED_KV_FUSED``: packed K and V read by the fused MFMA kernel;
+  * ``PACKED_KV_EXACT``: packed K and V read by the exact-order kernel,
+    reconstructions rounded to the query dtype as the reference's
+    ``read_v`` does (loop_kv_vf01_kernel.py:15-44).
+
+Unlike the reference (batch 1, MHA, explicit all-zero mask), any batch,
+GQA group and the model's attention scale are taken; sliding-window
+attention, training mode and beam reordering are refused.  Slots are
+``current_ut * num_hidden_layers + layer_idx`` (looped models pass
+``current_ut``; others use loop 0).
+
+Nothing here synchronises with the device when ``strict=False``: the
+position / mask checks (host syncs in the reference) are then skipped and
+nonfinite flags accumulate in the cache's status word, read by
+``check_status()``.
+"""
+from __future__ import annotations
+
+import sys
+import types
+from collections import Counter
+
+import torch
+
+from . import _dev, _lib, kernels, primitives
+from .errors import IntegrityError, NumericalFailure, require
+from .kernels import BLOCK, DIM, PackedKV
+from .stream_cache import StreamingKVCache
+
+ARMS = ("NATIVE", "PACKED_GROUPED", "PACKED_KV_FUSED", "PACKED_KV_EXACT")
+
+try:   # transformers is optional: only the adapter needs it
+    from transformers.cache_utils import Cache, CacheLayerMixin
+except ImportError:   # pragma: no cover - the image ships transformers
+    Cache, CacheLayerMixin = object, object
+
+
+class _PackedLayer(CacheLayerMixin):
+    """One slot of the packed cache seen through transformers' layer API."""
+
+    is_sliding = False
+    is_compileable = False
+
+    def __init__(self, owner, slot):
+        super().__init__()
+        self.owner, self.slot = owner, slot
+        self.is_initialized = True
+
+    def lazy_initialization(self, key_states, value_states):
+        pass
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        return self.owner.update_slot(self.slot, key_states, value_states, kwargs.get("cache_kwargs") or kwargs)
+
+    def get_mask_sizes(self, query_length):
+        return self.get_seq_length() + query_length, 0
+
+    def get_seq_length(self):
+        return self.owner.store.length[self.slot]
+
+    def get_max_length(self):
+        return self.owner.max_tokens
+
+    def reset(self):
+        raise IntegrityError("Packed cache reset not supported: build a new cache")
+
+    def reorder_cache(self, beam_idx):
+        raise IntegrityError("Packed cache beam reorder not supported")
+
+
+class PackedKVCache(Cache):
+    """Packed K/V for every (loop, layer) slot of ``config``'s attention layers.
+
+    batch, max_tokens: sequences and the token capacity per slot;
+    max_prefill: the longest single append (the prompt) before compression.
+    The packed side is ``bits``-bit NSN codes; the tail is fp16 (the fused
+    kernel's tail format; bf16 activations convert exactly in fp16's normal
+    range).
+    """
+
+    nsn_connection = True
+
+    def __init__(self, config, batch, max_tokens, *, loops=1, bits=3, arm="PACKED_KV_FUSED", max_prefill=512,
+                 strict=True, device=None):
+        require(arm in ARMS, "Unknown connection arm")
+        heads_q = config.num_attention_heads
+        heads = getattr(config, "num_key_value_heads", None) or heads_q
+        head_dim = getattr(config, "head_dim", None) or config.hidden_size // heads_q
+        require(head_dim == DIM, "Packed cache needs head_dim 128")
+        require(heads_q % heads == 0, "GQA group")
+        self.n_layers, self.loops = config.num_hidden_layers, loops
+        self.heads_q, self.heads = heads_q, heads
+        self.batch, self.max_tokens, self.arm, self.strict = batch, max_tokens, arm, strict
+        self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
+                                      dtype=torch.float16, max_append=max(max_prefill, 1),
+                                      device=device or torch.device("cuda:0"))
+        super().__init__(layers=[_PackedLayer(self, s) for s in range(self.n_layers * loops)])
+        self.status = _dev.new_status(self.store.device)   # attention flags (strict=False)
+        self.connection_calls = Counter()
+        self.capture = None
+        self._ws = None
+
+    # ------------------------------------------------------------------ lengths
+    def get_seq_length(self, layer_idx=0):
+        i = 0 if layer_idx is None else layer_idx
+        return self.store.length[i] if 0 <= i < self.store.slots else 0
+
+    def slot(self, layer_idx, current_ut=0):
+        s = current_ut * self.n_layers + layer_idx
+        require(0 <= layer_idx < self.n_layers and 0 <= s < self.store.slots, "Packed KV coordinates")
+        return s
+
+    # ------------------------------------------------------------------ appends
+    def _append(self, slot, key, value):
+        require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
+                and key.shape[3] == DIM, "Packed KV coordinates")
+        self.store.append(slot, key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous())
+
+    def _check_position(self, slot, n, kwargs):
+        pos = kwargs.get("cache_position")
+        if pos is None:
+            pos = kwargs.get("position_ids")
+        if pos is not None and self.strict:
+            old = self.store.length[slot]
+            want = torch.arange(old, old + n, device=pos.device)
+            require(bool(torch.equal(pos.reshape(-1, n)[0].to(want.dtype), want)), "Packed append position")
+
+    def update_slot(self, slot, key, value, kwargs=None):
+        """The native route: append, then the dense K/V of the whole slot in
+        the key's dtype (loop_kv_pk01_cache.py:97-110)."""
+        self._check_position(slot, key.shape[2], kwargs or {})
+        self._append(slot, key, value)
+        return self.materialize(slot, "K", key.dtype), self.materialize(slot, "V", key.dtype)
+
+    def append_for_attention(self, slot, key, value, kwargs=None):
+        """Append the step's K/V without the dense restore (loop_kv_ac08_attention.py:20-24)."""
+        self._check_position(slot, key.shape[2], kwargs or {})
+        self._append(slot, key, value)
+
+    def materialize(self, slot, name, dtype):
+        """Dense [B, H, L, 128] of one side: packed blocks restored exactly
+        (nsn_decode, rounded to ``dtype``) followed by the tail."""
+        kv = self.store.side(slot, name)
+        L, C = self.store.length[slot], self.store.compressed[slot]
+        out = torch.empty((self.batch, self.heads, L, DIM), dtype=dtype, device=self.store.device)
+        st = _dev.new_status(self.store.device) if self.strict else self.status
+        rc = _lib.lib().nsn_restore_blocks(
+            kv.codes.data_ptr(), 0, kv.norm.data_ptr(), kv.min.data_ptr(), kv.scale.data_ptr(),
+            self.batch * self.heads, C // BLOCK, self.store.block_cap, kv.bits, out.data_ptr(),
+            _dev.dtype_code(dtype), L, kv.tail.data_ptr(), _dev.dtype_code(kv.tail.dtype), L - C,
+            self.store.tail_cap, st.data_ptr(), _dev.stream())
+        _lib.check(rc, "nsn_restore_blocks")
+        if self.strict:
+            primitives._restore_raise(_dev.read_status(st))
+        return out
+
+    # ------------------------------------------------------------------ policy
+    def post_prefill(self):
+        self.store.post_prefill()
+
+    def post_decode(self):
+        self.store.post_decode()
+
+    def check_status(self):
+        """Raise on any flag raised since the cache was built (syncs)."""
+        self.store.check_status()
+        s = _dev.read_status(self.status)
+        if s & _lib.ST_NONFINITE_ATTN_INPUT:
+            raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
+        if s:
+            raise NumericalFailure("Nonfinite attention intermediate/output")
+
+    # ------------------------------------------------------------------ attention
+    def attend(self, slot, q, scale):
+        """Decode attention of q [B, Hq, 128] over the slot by the cache's arm
+        (not NATIVE); returns the bf16 output [B, Hq, 128]."""
+        L = self.store.length[slot]
+        kside, vside = self.store.side(slot, "K"), self.store.side(slot, "V")
+        kw = dict(max_seq_len=L, scale=scale, check=self.strict, status=None if self.strict else self.status)
+        if self.arm == "PACKED_GROUPED":
+            vd = PackedKV(None, None, None, None, None, None, self.materialize(slot, "V", torch.float16), kside.bits)
+            kw.update(kernel="fast", workspace=self._workspace(L))
+            out, _ = kernels.decode_attention(q, kside, vd, self.store.lengths(slot), **kw)
+        elif self.arm == "PACKED_KV_FUSED":
+            kw.update(kernel="fast", workspace=self._workspace(L))
+            out, _ = kernels.decode_attention(q, kside, vside, self.store.lengths(slot), **kw)
+        else:
+            kw.update(kernel="reference", kv_round_dtype=q.dtype)
+            out, _ = kernels.decode_attention(q, kside, vside, self.store.lengths(slot), **kw)
+        return out
+
+    def _workspace(self, L):
+        _, n = kernels.default_split(self.batch, self.heads, L)
+        need = kernels.workspace_floats(self.batch, self.heads_q, max(2, n))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(max(need, 2 * (0 if self._ws is None else self._ws.numel())),
+                                   dtype=torch.float32, device=self.store.device)
+        return self._ws
+
+
+def check_decode(module, q, cache, slot, position, mask):
+    """Preconditions of the packed decode route (loop_kv_ac08_attention.py:26-33):
+    eval mode, no sliding window, q [B, Hq, 1, 128] bf16/fp16, and (strict
+    mode) the step's position equal to the last cached token and the mask
+    allowing every cached token.  Returns the slot's length."""
+    total = cache.store.length[slot]
+    require(not module.training and getattr(module, "sliding_window", None) is None,
+            "Packed decode requires eval and no sliding window")
+    require(q.ndim == 4 and tuple(q.shape) == (cache.batch, cache.heads_q, 1, DIM)
+            and q.dtype in (torch.bfloat16, torch.float16), "Decode query shape/dtype")
+    if cache.strict:
+        if position is not None:
+            require(position.numel() >= 1 and int(position.reshape(-1)[-1].item()) == total - 1,
+                    "Decode must append at current last position")
+        if mask is not None:
+            require(mask.shape[-1] == total, "Decode mask length")
+            m = mask[..., -1:, :]
+            allowed = bool(m.all()) if m.dtype == torch.bool else bool((m == 0).all())
+            require(allowed, "Packed decode requires an all-allowed decode mask")
+    return total
+
+
+def _modeling(attn):
+    return sys.modules[type(attn).__module__]
+
+
+def install(model, module=None):
+    """Patch the attention of every decoder layer (instances only) and return
+    ``restore()``, which puts every original bound method back
+    (loop_kv_ac08_attention.py:46-96).  ``module`` is the model's modeling
+    module (for ``apply_rotary_pos_emb``); by default the attention class's own."""
+    changed = []
+    for layer in model.model.layers:
+        attn = layer.self_attn
+        original = attn.forward
+        mod = module if module is not None else _modeling(attn)
+
+        def forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
+                    current_ut=0, _original=original, _mod=mod, **kwargs):
+            cache = past_key_values
+            if not getattr(cache, "nsn_connection", False):
+                return _original(hidden_states, position_embeddings, attention_mask, past_key_values=past_key_values,
+                                 **kwargs)
+            input_shape = hidden_states.shape[:-1]
+            hidden_shape = (*input_shape, -1, self.head_dim)
+            q = self.q_proj(hidden_states).view(hidden_shape)
+            k = self.k_proj(hidden_states).view(hidden_shape)
+            if hasattr(self, "q_norm"):
+                q, k = self.q_norm(q), self.k_norm(k)
+            q, k = q.transpose(1, 2), k.transpose(1, 2)
+            v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+            cos, sin = position_embeddings
+            q, k = _mod.apply_rotary_pos_emb(q, k, cos, sin)
+            slot = cache.slot(self.layer_idx, current_ut)
+            if hidden_states.shape[1] != 1:
+                # prefill: the native route over the slot's dense K/V
+                kd, vd = cache.update_slot(slot, k, v, kwargs)
+                fn = _mod.ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
+                                                                _mod.eager_attention_forward)
+                out, _ = fn(self, q, kd, vd, attention_mask, dropout=0.0, scaling=self.scaling, **kwargs)
+            else:
+                cache.append_for_attention(slot, k, v, kwargs)
+                q = q.contiguous()
+                total = check_decode(self, q, cache, slot, kwargs.get("position_ids"), attention_mask)
+                if cache.arm == "NATIVE":
+                    kd = cache.materialize(slot, "K", q.dtype)
+                    vd = cache.materialize(slot, "V", q.dtype)
+                    fn = _mod.ALL_ATTENTION_FUNCTIONS["sdpa"]
+                    out, _ = fn(self, q, kd, vd, attention_mask, dropout=0.0, scaling=self.scaling, **kwargs)
+                    if cache.strict and not bool(torch.isfinite(out).all()):
+                        raise NumericalFailure("Nonfinite attention output")
+                else:
+                    o = cache.attend(slot, q[:, :, 0], self.scaling)           # [B, Hq, 128] bf16
+                    out = o.to(q.dtype).unsqueeze(1)                          # [B, 1, Hq, 128]
+                cache.connection_calls[slot] += 1
+                if cache.capture is not None:
+                    cache.capture(slot, total, q[:, :, 0], out[:, 0])
+            out = out.reshape(*input_shape, -1).contiguous()
+            return self.o_proj(out), None
+
+        changed.append((attn, original))
+        attn.forward = types.MethodType(forward, attn)
+
+    def restore():
+        for a, orig in changed:
+            a.forward = orig
+    return restore
+
+
+def greedy(model, cache, input_ids, steps):
+    """Prefill ``input_ids`` [B, P], then ``steps`` greedy decode steps through
+    ``cache``, running the compression policy after each forward.  Returns
+    (tokens [B, steps], logits [steps, B, vocab] fp32)."""
+    toks, logits = [], []
+    with torch.no_grad():
+        out = model(input_ids=input_ids, past_key_values=cache, use_cache=True)
+        cache.post_prefill()
+        for _ in range(steps):
+            lg = out.logits[:, -1].float()
+            nxt = lg.argmax(-1, keepdim=True)
+            toks.append(nxt)
+            logits.append(lg)
+            out = model(input_ids=nxt, past_key_values=cache, use_cache=True)
+            cache.post_decode()
+    return torch.cat(toks, 1), torch.stack(logits)

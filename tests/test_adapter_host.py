@@ -1,0 +1,91 @@
+"""Host-side checks of the transformers connection (no GPU): the patch is a
+pass-through without the packed cache and is fully undone by restore(); the
+decode preconditions refuse what the reference refuses
+(experiments/ac08/source/loop_kv_ac08_attention.py:26-33,46-96)."""
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+from transformers import LlamaConfig, LlamaForCausalLM  # noqa: E402
+
+from nsn_amd import adapter  # noqa: E402
+from nsn_amd.errors import IntegrityError  # noqa: E402
+
+
+def tiny_llama(seed=0):
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=2, num_key_value_heads=1, head_dim=128, max_position_embeddings=512)
+    return LlamaForCausalLM(cfg).eval()
+
+
+def test_install_is_passthrough_without_packed_cache_and_restore_undoes_it():
+    m = tiny_llama()
+    ids = torch.randint(0, 64, (2, 9), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        ref = m(input_ids=ids).logits
+        originals = [l.self_attn.forward for l in m.model.layers]
+        restore = adapter.install(m)
+        assert all(l.self_attn.forward != o for l, o in zip(m.model.layers, originals))
+        got = m(input_ids=ids).logits                      # DynamicCache: the original forward
+        restore()
+        assert [l.self_attn.forward for l in m.model.layers] == originals
+        again = m(input_ids=ids).logits
+    assert torch.equal(ref, got) and torch.equal(ref, again)
+
+
+def _stub_cache(length=10, strict=True, batch=1, heads_q=2):
+    return SimpleNamespace(store=SimpleNamespace(length=[length]), batch=batch, heads_q=heads_q, strict=strict)
+
+
+def _module(training=False, window=None):
+    return SimpleNamespace(training=training, sliding_window=window)
+
+
+def test_check_decode_accepts_the_decode_step():
+    q = torch.zeros(1, 2, 1, 128, dtype=torch.bfloat16)
+    assert adapter.check_decode(_module(), q, _stub_cache(), 0, torch.tensor([[9]]), None) == 10
+    assert adapter.check_decode(_module(), q, _stub_cache(), 0, torch.tensor([[9]]), torch.zeros(1, 1, 1, 10)) == 10
+    assert adapter.check_decode(_module(), q, _stub_cache(), 0, None, torch.ones(1, 1, 1, 10, dtype=torch.bool)) == 10
+
+
+@pytest.mark.parametrize("case", ["training", "window", "shape", "dtype", "position", "mask_len", "mask_blocked"])
+def test_check_decode_refusals(case):
+    q = torch.zeros(1, 2, 1, 128, dtype=torch.bfloat16)
+    mod, pos, mask = _module(), torch.tensor([[9]]), None
+    if case == "training":
+        mod = _module(training=True)
+    elif case == "window":
+        mod = _module(window=128)
+    elif case == "shape":
+        q = torch.zeros(1, 2, 2, 128, dtype=torch.bfloat16)
+    elif case == "dtype":
+        q = q.float()
+    elif case == "position":
+        pos = torch.tensor([[8]])
+    elif case == "mask_len":
+        mask = torch.zeros(1, 1, 1, 9)
+    elif case == "mask_blocked":
+        mask = torch.zeros(1, 1, 1, 10)
+        mask[..., 3] = float("-inf")
+    with pytest.raises(IntegrityError):
+        adapter.check_decode(mod, q, _stub_cache(), 0, pos, mask)
+
+
+def test_check_decode_non_strict_skips_the_synchronising_checks():
+    q = torch.zeros(1, 2, 1, 128, dtype=torch.bfloat16)
+    mask = torch.zeros(1, 1, 1, 10)
+    mask[..., 3] = float("-inf")
+    assert adapter.check_decode(_module(), q, _stub_cache(strict=False), 0, torch.tensor([[3]]), mask) == 10
+
+
+def test_unknown_arm_and_head_dim_refused():
+    cfg = SimpleNamespace(num_attention_heads=2, num_key_value_heads=1, head_dim=128, hidden_size=256,
+                          num_hidden_layers=2)
+    with pytest.raises(IntegrityError):
+        adapter.PackedKVCache(cfg, 1, 256, arm="TILE_MATERIALIZE")
+    cfg.head_dim = 64
+    with pytest.raises(IntegrityError):
+        adapter.PackedKVCache(cfg, 1, 256)
