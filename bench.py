@@ -61,10 +61,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
-    p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "k1c"],
+    p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "k1c", "adapter"],
                    help="c2: the headline line (default); c3 / c4: the 5-bit and streaming-cache "
                         "configurations, one line each; k1c: the K-score grid against the reference's "
-                        "published cells")
+                        "published cells; adapter: a transformers model decoding through the packed cache")
     p.add_argument("--k1c-model", default="Qwen3-30B-A3B", choices=["Qwen3-30B-A3B", "Gemma4-26B-A4B"])
     p.add_argument("--k1c-quick", action="store_true", help="k1c: only ctx 32768 at B = 8 and 32")
     p.add_argument("--k1c-summary", metavar="DIR",
@@ -75,6 +75,11 @@ def parse():
                    help="c3 / c4: turn a rocprofv3 --kernel-trace --stats run of that workload under DIR "
                         "into profiles/<workload>.md")
     p.add_argument("--decode-steps", type=int, default=64, help="c4: decode steps timed (of the 256)")
+    p.add_argument("--adapter-arms", default="hf_dense,graph,PACKED_KV_FUSED,NATIVE",
+                   help="adapter: the runs, in order (the first packed one that ran gives the value)")
+    p.add_argument("--adapter-summary", metavar="DIR",
+                   help="turn a rocprofv3 --kernel-trace run of `--workload adapter --adapter-arms graph` under DIR "
+                        "into profiles/adapter_decode_graph.md")
     return p.parse_args()
 
 
@@ -759,6 +764,184 @@ STATS_DOC = {
 }
 
 
+ADAPTER = dict(layers=24, hidden=2048, heads=16, inter=5632, vocab=49152, B=32, T=8192, chunk=512)
+
+
+def main_adapter(args):
+    """The transformers connection (nsn_amd.adapter) on an Ouro-1.4B-shaped
+    Llama with random-init bf16 weights (24 layers = one loop of the C4 slot
+    map, 16 MHA heads, d=128, B=32; torch seed 5): an 8192-token chunked
+    prefill (chunks of 512, compressed after each), then `--steps` decode
+    steps (fixed synthetic tokens; the compression policy after each step).
+    The same step four ways: the packed cache with the fused arm replayed as
+    one HIP graph per step (the value), the same arm run eagerly, the NATIVE
+    arm (dense restore + sdpa), and transformers' own DynamicCache (dense
+    bf16 K/V).  One JSON line."""
+    import gc
+    import time
+
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from transformers.cache_utils import DynamicCache
+
+    from nsn_amd import adapter
+
+    a = ADAPTER
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    b_, T, ch = a["B"], a["T"], a["chunk"]
+    steps, warm = args.steps, args.warmup
+    cfg = LlamaConfig(vocab_size=a["vocab"], hidden_size=a["hidden"], intermediate_size=a["inter"],
+                      num_hidden_layers=a["layers"], num_attention_heads=a["heads"], num_key_value_heads=a["heads"],
+                      head_dim=D, max_position_embeddings=T + steps + warm + 64)
+    torch.manual_seed(5)
+    with torch.device(dev):
+        m = LlamaForCausalLM(cfg)
+    m = m.to(torch.bfloat16).eval()
+    n_embed = a["vocab"] * a["hidden"]
+    weight_bytes = 2 * (sum(p.numel() for p in m.parameters()) - n_embed)   # the embedding is gathered, not read
+    gen = torch.Generator(device=dev).manual_seed(5)
+    ids = torch.randint(0, a["vocab"], (b_, T), generator=gen, device=dev)
+    toks = torch.randint(0, a["vocab"], (b_, warm + steps), generator=gen, device=dev)
+    log(f"[bench] adapter: {a['layers']} layers, {a['heads']} heads, B={b_}, prefill {T} (chunk {ch}), "
+        f"{steps} decode steps; weights {weight_bytes / 1e9:.2f} GB read per step")
+    restore = adapter.install(m)
+
+    def run(kind):
+        packed = kind != "hf_dense"
+        graph = kind == "graph"
+        arm = "PACKED_KV_FUSED" if graph else kind
+        cache = (adapter.PackedKVCache(cfg, b_, T + warm + steps + 64, arm=arm, max_prefill=ch, strict=False,
+                                       device=dev) if packed else DynamicCache(config=cfg))
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            for c in range(T // ch):
+                m(input_ids=ids[:, c * ch:(c + 1) * ch], past_key_values=cache, use_cache=True, logits_to_keep=1)
+                if packed:
+                    cache.post_prefill()
+            torch.cuda.synchronize()
+            pre_s = time.perf_counter() - t0
+            i = [0]
+            dg = adapter.DecodeGraph(m, cache) if graph else None
+
+            def step():
+                if graph:
+                    dg.step(toks[:, i[0]:i[0] + 1])
+                else:
+                    m(input_ids=toks[:, i[0]:i[0] + 1], past_key_values=cache, use_cache=True, logits_to_keep=1)
+                    if packed:
+                        cache.post_decode()
+                i[0] += 1
+            for _ in range(warm):
+                step()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            h0 = time.perf_counter()
+            e0.record(stream)
+            for _ in range(steps):
+                step()
+            e1.record(stream)
+            host_ms = (time.perf_counter() - h0) * 1e3 / steps
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+        kv_bytes = 0
+        if packed:
+            cache.check_status()
+            st = cache.store
+            L, C = st.length[0], st.compressed[0]
+            kv_bytes = a["layers"] * b_ * a["heads"] * 2 * (C * 58 + (L - C) * 256)
+        # the graph (and its memory pool) and the step closure hold the cache:
+        # drop all of them before handing the memory back
+        dg = None
+        del cache, step
+        gc.collect()
+        torch.cuda.empty_cache()
+        free = torch.cuda.mem_get_info()[0] / 2**30
+        log(f"[bench] adapter {kind}: prefill {pre_s:.1f} s, decode {ms:.2f} ms/step (host issue {host_ms:.2f} "
+            f"ms/step); {free:.0f} GiB free after release")
+        return ms, host_ms, kv_bytes
+
+    arms = args.adapter_arms.split(",")
+    require_arms = {"hf_dense", "graph", "PACKED_KV_FUSED", "NATIVE"}
+    if not arms or not set(arms) <= require_arms or "graph" not in arms:
+        raise SystemExit(f"--adapter-arms: a comma list of {sorted(require_arms)} that includes graph")
+    res = {}
+    try:
+        for kind in arms:                          # hf_dense first by default: the largest footprint, fresh memory
+            res[kind] = run(kind)
+    finally:
+        restore()
+    graph_ms, graph_host, kv_bytes = res["graph"]
+    fused_ms, fused_host = res.get("PACKED_KV_FUSED", (None, None, 0))[:2]
+    native_ms = res.get("NATIVE", (None,))[0]
+    dense_ms = res.get("hf_dense", (None,))[0]
+    nbytes = weight_bytes + kv_bytes
+    achieved = nbytes / (graph_ms * 1e-3) / 1e9
+    result = {
+        "metric": "HF-connected decode ms/step (Ouro-1.4B-shaped Llama, 24 layers, B=32, ctx 8192, INT3 packed K/V)",
+        "value": round(graph_ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(graph_ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random-init weights, torch seed 5; tokens from GPU generator seed 5)",
+        "config": {"workload": "transformers connection: whole-model decode step through the packed cache",
+                   "layers": a["layers"], "hidden": a["hidden"], "heads_q": a["heads"], "heads_kv": a["heads"],
+                   "head_dim": D, "batch": b_, "prefill": T, "chunk": ch, "bits": 3,
+                   "arm": "PACKED_KV_FUSED, step replayed as a HIP graph"},
+        "comparators": {"fused_eager_ms": _r(fused_ms), "fused_eager_host_issue_ms": _r(fused_host),
+                        "graph_host_issue_ms": _r(graph_host), "native_arm_ms": _r(native_ms),
+                        "hf_dynamic_cache_ms": _r(dense_ms)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole decode step (weights + packed K/V of 24 layers)", "algorithmic_bytes": nbytes},
+    }
+    print(json.dumps(result), flush=True)
+
+
+def _r(x, nd=3):
+    return None if x is None else round(x, nd)
+
+
+ADAPTER_DOC = ("rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- "
+               "python3 bench.py --workload adapter --adapter-arms graph")
+
+
+def adapter_summary(d):
+    """profiles/adapter_decode_graph.md from the kernel trace of
+    `bench.py --workload adapter --adapter-arms graph`: the kernels from the
+    first device-position tail append on (the decode phase: one eager warm-up
+    step, then warmup + steps graph replays), grouped by name, per step."""
+    rows = _rows((Path(d), "**/*kernel_trace.csv"))
+    ks = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in rows)
+    first = next(i for i, k in enumerate(ks) if "tail_append_to_kernel" in k[2])
+    dec = ks[first:]
+    n_append = sum("tail_append_to_kernel" in k[2] for k in dec)
+    layers = ADAPTER["layers"]
+    if n_append % layers:
+        raise SystemExit(f"{n_append} tail appends is not a multiple of {layers} layers")
+    nstep = n_append // layers
+    agg = {}
+    for s0, s1, name in dec:
+        a = agg.setdefault(name, [0, 0])
+        a[0] += 1
+        a[1] += s1 - s0
+    busy = sum(v[1] for v in agg.values())
+    wall = dec[-1][1] - dec[0][0]
+    L = ["# Transformers connection: one decode step as a HIP graph (adapter workload)", "",
+         "Ouro-1.4B-shaped Llama (24 layers, 16 MHA heads, d=128), random-init bf16 weights; B=32, 8192-token "
+         "context in the packed cache (INT3 blocks + fp16 tail); the fused arm, the step captured once and "
+         "replayed.", "", "Command (from the repository root on one MI355X, `OUT` = an output folder), then "
+         "`python3 bench.py --adapter-summary OUT/kt`:", "", "```", ADAPTER_DOC, "```", "",
+         f"Decode phase: {nstep} steps ({len(dec)} kernels, {len(dec) / nstep:.0f} per step); kernel busy "
+         f"{busy / nstep / 1e6:.3f} ms per step, first start to last end {wall / nstep / 1e6:.3f} ms per step "
+         "(the gaps are dispatch between the graph's small kernels).", "",
+         "| kernel | per step | avg us | us per step | share of busy |", "|---|---|---|---|---|"]
+    for name, (cnt, tot) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:16]:
+        L.append(f"| `{name[:100]}` | {cnt / nstep:.0f} | {tot / cnt / 1e3:.1f} | {tot / nstep / 1e3:.1f} | "
+                 f"{tot / busy:.1%} |")
+    L.append("")
+    (ROOT / "profiles" / "adapter_decode_graph.md").write_text("\n".join(L))
+    print("\n".join(L))
+
+
 def stats_summary(d, workload):
     """profiles/<name>.md from the kernel statistics of one rocprofv3 run."""
     name, title, cmd = STATS_DOC[workload]
@@ -789,6 +972,9 @@ def main():
     if args.stats_summary:
         stats_summary(args.stats_summary, args.workload)
         return
+    if args.adapter_summary:
+        adapter_summary(args.adapter_summary)
+        return
     if args.profile:
         profile_run(args)
         return
@@ -803,6 +989,9 @@ def main():
         return
     if args.workload == "k1c":
         main_k1c(args)
+        return
+    if args.workload == "adapter":
+        main_adapter(args)
         return
     import numpy as np
     import torch

@@ -46,6 +46,7 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 #define NSN_ST_NONFINITE_ATTN 0x20    /* attention: nonfinite score/weights  */
 #define NSN_ST_NONFINITE_OUTPUT 0x40  /* attention merge: nonfinite context  */
 #define NSN_ST_NONFINITE_SCAN 0x80    /* finite scan: nonfinite raw input    */
+#define NSN_ST_TAIL_RANGE 0x200 /* tail append: device end position outside [n, tail_cap] */
 #define NSN_ST_NONFINITE_ATTN_INPUT 0x100 /* attention: nonfinite raw input read by the kernel
                                              (q, tail tokens; block metadata in the REFERENCE kernel) */
 
@@ -251,6 +252,19 @@ int nsn_prefill_attention(const nsn_prefill_args *args, nsn_stream_t stream);
  */
 int nsn_tail_append(const void *k_new, const void *v_new, int64_t rows, int64_t n, int64_t new_row_stride,
                     void *k_tail, void *v_tail, int64_t tail_cap, int64_t offset, int dtype, nsn_stream_t stream);
+
+/*
+ * nsn_tail_append with the position in device memory: the n new tokens of
+ * each row go to [*tail_end - n, *tail_end).  The launch then has no host
+ * argument that changes from step to step, so a captured HIP graph of a
+ * decode step replays it unchanged while the caller advances *tail_end on
+ * the device.  An end outside [n, tail_cap] writes nothing and raises
+ * NSN_ST_TAIL_RANGE in *status.  Replaces the same tail concatenation
+ * (experiments/ac08/source/loop_kv_pk01_cache.py:101-102) under graph replay.
+ */
+int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t rows, int64_t n, int64_t new_row_stride,
+                       void *k_tail, void *v_tail, int64_t tail_cap, const int32_t *tail_end, int dtype,
+                       int32_t *status, nsn_stream_t stream);
 
 /*
  * NaN/Inf scan over up to 16 arrays; array i sets bit i of flags[0] (int32)

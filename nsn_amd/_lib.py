@@ -26,6 +26,7 @@ ST_NONFINITE_ATTN = 0x20
 ST_NONFINITE_OUTPUT = 0x40
 ST_NONFINITE_SCAN = 0x80
 ST_NONFINITE_ATTN_INPUT = 0x100
+ST_TAIL_RANGE = 0x200
 
 NSN_OK, NSN_EINVAL, NSN_ELAUNCH = 0, -1, -2
 
@@ -76,6 +77,7 @@ SIGNATURES = {
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
     "nsn_prefill_attention": (I32, [ctypes.POINTER(PrefillArgs), P]),
     "nsn_tail_append": (I32, [P, P, I64, I64, I64, P, P, I64, I64, I32, P]),
+    "nsn_tail_append_to": (I32, [P, P, I64, I64, I64, P, P, I64, P, I32, P, P]),
     "nsn_kscore": (I32, [ctypes.POINTER(KScoreArgs), P]),
 }
 

@@ -123,6 +123,11 @@ class PackedKVCache(Cache):
         self.connection_calls = Counter()
         self.capture = None
         self._ws = None
+        # device-position mode (DecodeGraph): int32 [B sequence lengths | tail end],
+        # shared by every slot (the policy keeps all slots at one length)
+        self.graph_mode = False
+        self.counters = torch.zeros(batch + 1, dtype=torch.int32, device=self.store.device)
+        self.cap_len = self.store.block_cap * BLOCK + self.store.tail_cap
 
     # ------------------------------------------------------------------ lengths
     def get_seq_length(self, layer_idx=0):
@@ -157,9 +162,24 @@ class PackedKVCache(Cache):
         return self.materialize(slot, "K", key.dtype), self.materialize(slot, "V", key.dtype)
 
     def append_for_attention(self, slot, key, value, kwargs=None):
-        """Append the step's K/V without the dense restore (loop_kv_ac08_attention.py:20-24)."""
-        self._check_position(slot, key.shape[2], kwargs or {})
-        self._append(slot, key, value)
+        """Append the step's K/V without the dense restore (loop_kv_ac08_attention.py:20-24).
+        In device-position mode the tokens go to [tail_end - n, tail_end) with
+        tail_end read from ``counters`` on the device, and the host lengths
+        are left to the caller (DecodeGraph)."""
+        if not self.graph_mode:
+            self._check_position(slot, key.shape[2], kwargs or {})
+            self._append(slot, key, value)
+            return
+        require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
+                and key.shape[3] == DIM, "Packed KV coordinates")
+        k16, v16 = key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous()
+        kt, vt = self.store.side(slot, "K").tail, self.store.side(slot, "V").tail
+        n = key.shape[2]
+        rc = _lib.lib().nsn_tail_append_to(k16.data_ptr(), v16.data_ptr(), self.batch * self.heads, n, n,
+                                           kt.data_ptr(), vt.data_ptr(), self.store.tail_cap,
+                                           self.counters.data_ptr() + 4 * self.batch, _lib.DTYPE_F16,
+                                           self.status.data_ptr(), _dev.stream())
+        _lib.check(rc, "nsn_tail_append_to")
 
     def materialize(self, slot, name, dtype):
         """Dense [B, H, L, 128] of one side: packed blocks restored exactly
@@ -200,17 +220,23 @@ class PackedKVCache(Cache):
         (not NATIVE); returns the bf16 output [B, Hq, 128]."""
         L = self.store.length[slot]
         kside, vside = self.store.side(slot, "K"), self.store.side(slot, "V")
+        seq = self.store.lengths(slot)
+        if self.graph_mode:
+            # lengths from the device counters, the capacity as the bound: no
+            # launch argument changes from step to step
+            require(self.arm == "PACKED_KV_FUSED" and not self.strict, "Device positions: fused arm, strict=False")
+            L, seq = self.cap_len, self.counters[:self.batch]
         kw = dict(max_seq_len=L, scale=scale, check=self.strict, status=None if self.strict else self.status)
         if self.arm == "PACKED_GROUPED":
             vd = PackedKV(None, None, None, None, None, None, self.materialize(slot, "V", torch.float16), kside.bits)
             kw.update(kernel="fast", workspace=self._workspace(L))
-            out, _ = kernels.decode_attention(q, kside, vd, self.store.lengths(slot), **kw)
+            out, _ = kernels.decode_attention(q, kside, vd, seq, **kw)
         elif self.arm == "PACKED_KV_FUSED":
             kw.update(kernel="fast", workspace=self._workspace(L))
-            out, _ = kernels.decode_attention(q, kside, vside, self.store.lengths(slot), **kw)
+            out, _ = kernels.decode_attention(q, kside, vside, seq, **kw)
         else:
             kw.update(kernel="reference", kv_round_dtype=q.dtype)
-            out, _ = kernels.decode_attention(q, kside, vside, self.store.lengths(slot), **kw)
+            out, _ = kernels.decode_attention(q, kside, vside, seq, **kw)
         return out
 
     def _workspace(self, L):
@@ -296,8 +322,10 @@ def install(model, module=None):
                 else:
                     o = cache.attend(slot, q[:, :, 0], self.scaling)           # [B, Hq, 128] bf16
                     out = o.to(q.dtype).unsqueeze(1)                          # [B, 1, Hq, 128]
-                cache.connection_calls[slot] += 1
+                if not cache.graph_mode:
+                    cache.connection_calls[slot] += 1
                 if cache.capture is not None:
+                    require(not cache.graph_mode, "No capture hook under device positions")
                     cache.capture(slot, total, q[:, :, 0], out[:, 0])
             out = out.reshape(*input_shape, -1).contiguous()
             return self.o_proj(out), None
@@ -309,6 +337,93 @@ def install(model, module=None):
         for a, orig in changed:
             a.forward = orig
     return restore
+
+
+class DecodeGraph:
+    """One decode step of ``model`` through ``cache`` (fused arm, strict=False,
+    one loop) captured as a HIP graph and replayed per step.
+
+    Every launch argument of the step is fixed: the token and position ids
+    sit in static buffers, the tail append and the attention read the
+    sequence lengths and the tail end from ``cache.counters`` (advanced by
+    one device op at the start of the step), and the attention's length
+    bound is the cache capacity.  Between replays the host advances its own
+    lengths, runs the compression policy eagerly and, after a compression,
+    reloads the counters.  The first call runs the step once eagerly on a
+    side stream (library warm-up; its tail writes are the ones the real step
+    repeats), rewinds the counters, captures, then replays.  With
+    ``use_graph=False`` the same step runs eagerly each call (the reference
+    the replays are tested against).  Not a counterpart of anything in the
+    reference, whose decode step is eager Python (loop_kv_ac08_attention.py:46-96).
+    """
+
+    def __init__(self, model, cache, use_graph=True):
+        require(cache.arm == "PACKED_KV_FUSED" and not cache.strict and cache.loops == 1 and cache.capture is None,
+                "Decode graph: fused arm, strict=False, one loop, no capture hook")
+        self.model, self.cache, self.use_graph = model, cache, use_graph
+        dev = cache.store.device
+        self.ids = torch.zeros((cache.batch, 1), dtype=torch.long, device=dev)
+        self.pos = torch.zeros((cache.batch, 1), dtype=torch.long, device=dev)
+        self.graph = None
+        self.logits = None
+        self.replays = 0
+        cache._workspace(cache.cap_len)
+        self._reload = True
+
+    def _load_counters(self):
+        st, B = self.cache.store, self.cache.batch
+        L, C = st.length[0], st.compressed[0]
+        require(all(x == L for x in st.length) and all(c == C for c in st.compressed), "Slots at one length")
+        require(L - C + 1 <= st.tail_cap and L + 1 <= self.cache.cap_len, "Cache capacity exceeded")
+        self.cache.counters[:B].fill_(L)
+        self.cache.counters[B:].fill_(L - C)
+        self.pos.fill_(L - 1)
+
+    def _body(self):
+        self.cache.counters.add_(1)
+        self.pos.add_(1)
+        out = self.model(input_ids=self.ids, position_ids=self.pos, past_key_values=self.cache, use_cache=True,
+                         logits_to_keep=1)
+        return out.logits
+
+    def step(self, tokens):
+        """Decode ``tokens`` [B, 1] (int64, on the device).  Returns the logits
+        [B, 1, vocab]; under replay this is the graph's static output buffer,
+        overwritten by the next step."""
+        st = self.cache.store
+        self.ids.copy_(tokens)
+        if self._reload:
+            self._load_counters()
+            self._reload = False
+        self.cache.graph_mode = True
+        try:
+            with torch.no_grad():
+                if not self.use_graph:
+                    logits = self._body()
+                else:
+                    if self.graph is None:
+                        side = torch.cuda.Stream()
+                        side.wait_stream(torch.cuda.current_stream())
+                        with torch.cuda.stream(side):
+                            self._body()
+                        torch.cuda.current_stream().wait_stream(side)
+                        self._load_counters()
+                        self.graph = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(self.graph):
+                            self.logits = self._body()
+                    self.graph.replay()
+                    self.replays += 1
+                    logits = self.logits
+        finally:
+            self.cache.graph_mode = False
+        for s in range(st.slots):
+            st.length[s] += 1
+            self.cache.connection_calls[s] += 1
+        before = st.compressed[0]
+        self.cache.post_decode()
+        if st.compressed[0] != before:
+            self._reload = True
+        return logits
 
 
 def greedy(model, cache, input_ids, steps):

@@ -134,3 +134,38 @@ def test_native_arm_prefill_matches_unpatched_model():
     # significand), so only the rare K/V element below that moves, by < 2^-24
     err = (got.float() - ref.float()).abs().max().item()
     assert err <= 1e-3 * ref.float().abs().max().item(), err
+
+
+def test_decode_graph_replays_match_eager_steps():
+    """The fused step captured as a HIP graph: every replay (with eager work
+    and a synchronisation between replays) equals the same device-position
+    step run eagerly, bit for bit, across a compression; both agree with the
+    host-position fused arm to the arms' tolerance."""
+    m, cfg, ids = model()
+    n = 80
+    tokens = torch.randint(0, 256, (B, n), generator=torch.Generator().manual_seed(3)).to(DEV)
+    restore = adapter.install(m)
+    outs = {}
+    try:
+        for use_graph in (False, True):
+            cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P, strict=False)
+            with torch.no_grad():
+                m(input_ids=ids, past_key_values=cache, use_cache=True)
+            cache.post_prefill()
+            dg = adapter.DecodeGraph(m, cache, use_graph=use_graph)
+            steps = []
+            for i in range(n):
+                steps.append(dg.step(tokens[:, i:i + 1])[:, -1].float().clone())
+                torch.cuda.synchronize()
+            cache.check_status()
+            assert cache.store.length == [P + n] * 2 and cache.store.compressed == [128, 128]
+            assert all(cache.connection_calls[s] == n for s in (0, 1))
+            assert dg.replays == (n if use_graph else 0)
+            outs[use_graph] = torch.stack(steps)
+        ref = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P), ids,
+                            tokens)
+    finally:
+        restore()
+    assert torch.equal(outs[True], outs[False])
+    err = (outs[True][:-1] - ref[1:]).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item() + 1e-3, err
