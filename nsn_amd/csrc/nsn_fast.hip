@@ -153,6 +153,7 @@ struct FastParams {
     int64_t scores_cap;
     float *partials;
     int32_t *status;
+    int weighted;              // the grid is two waves per SIMD: weight first-slot waves 5:4
 };
 
 // Reductions over the 16 lanes of a row with DPP (quad_perm [1,0,3,2],
@@ -873,7 +874,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         // other (measured: ~20% more blocks per unit time), so its ranges
         // are longer by 5:4.
         const int64_t bx = blockIdx.x;
-        const int64_t w = (W % 2) ? bx : (bx < W / 2) ? 2 * bx : 2 * (bx - W / 2) + 1;
+        const bool wt = p.weighted && W % 2 == 0;
+        const int64_t w = !wt ? bx : (bx < W / 2) ? 2 * bx : 2 * (bx - W / 2) + 1;
         const uint64_t hit = __ballot(l < p.batch && wincl > w);
         if (!hit) return;   // a spare wave
         lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
@@ -883,7 +885,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int64_t k = r - kvh * n;
         const int64_t w0 = w - k;   // the stream's first wave
         auto cw = [&](int64_t j) {   // summed weight of the stream's waves 0 .. j-1
-            const int64_t first = (W % 2) ? 0 : (w0 + j + 1) / 2 - (w0 + 1) / 2;
+            const int64_t first = !wt ? 0 : (w0 + j + 1) / 2 - (w0 + 1) / 2;
             return 5 * first + 4 * (j - first);
         };
         // Cost units: a packed block 1, a block of dense fp16 tokens 3 (its
@@ -1004,13 +1006,19 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     p.scores_cap = a->scores_cap;
     p.partials = a->partials;
     p.status = a->status;
-    // two resident waves per SIMD: one wave per (CU, SIMD, slot)
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NSN_ELAUNCH;
     if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return NSN_ELAUNCH;
-    const dim3 grid(static_cast<unsigned>(8 * (cus[dev] > 0 ? cus[dev] : 256)));
+    // 3-bit: two resident waves per SIMD, one per (CU, SIMD, slot).  5-bit:
+    // the double-buffered 5 KB stages (26.8 KB of LDS per wave) leave room
+    // for 6 waves per CU, so a grid of 8 per CU would run its last quarter
+    // as a second, mostly idle round.
+    // (Measured on C3: 6 per CU 84 us, 4 or 5 per CU 87 us, 8 per CU 100 us.)
+    const int per_cu = (a->bits == 3) ? 8 : 6;
+    p.weighted = per_cu == 8;
+    const dim3 grid(static_cast<unsigned>(per_cu * (cus[dev] > 0 ? cus[dev] : 256)));
     const bool bf = a->q_dtype == NSN_DTYPE_BF16;
 #define NSN_FAST_LAUNCH1(B_, Q_, S_, G_) hipLaunchKernelGGL((attn_fast_kernel<B_, Q_, S_, G_>), grid, dim3(64), 0, st, p)
 #define NSN_FAST_LAUNCH(B_, Q_, S_)                                   \
