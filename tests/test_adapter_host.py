@@ -8,21 +8,24 @@ import pytest
 import torch
 
 transformers = pytest.importorskip("transformers")
-from transformers import LlamaConfig, LlamaForCausalLM  # noqa: E402
+from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM  # noqa: E402
 
 from nsn_amd import adapter  # noqa: E402
 from nsn_amd.errors import IntegrityError  # noqa: E402
 
 
-def tiny_llama(seed=0):
+def tiny_model(family="llama", seed=0):
     torch.manual_seed(seed)
-    cfg = LlamaConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2,
-                      num_attention_heads=2, num_key_value_heads=1, head_dim=128, max_position_embeddings=512)
-    return LlamaForCausalLM(cfg).eval()
+    kw = dict(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2,
+              num_attention_heads=2, num_key_value_heads=1, head_dim=128, max_position_embeddings=512)
+    if family == "qwen3":
+        return Qwen3ForCausalLM(Qwen3Config(**kw)).eval()
+    return LlamaForCausalLM(LlamaConfig(**kw)).eval()
 
 
-def test_install_is_passthrough_without_packed_cache_and_restore_undoes_it():
-    m = tiny_llama()
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+def test_install_is_passthrough_without_packed_cache_and_restore_undoes_it(family):
+    m = tiny_model(family)
     ids = torch.randint(0, 64, (2, 9), generator=torch.Generator().manual_seed(1))
     with torch.no_grad():
         ref = m(input_ids=ids).logits

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 transformers = pytest.importorskip("transformers")
-from transformers import LlamaConfig, LlamaForCausalLM  # noqa: E402
+from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM  # noqa: E402
 
 from nsn_amd import adapter  # noqa: E402
 from oracle import oracle as O  # noqa: E402
@@ -27,11 +27,18 @@ DEV = torch.device("cuda:0")
 B, P, STEPS = 2, 150, 60
 
 
-def model():
+def model(family="llama"):
+    """Random-init 2-layer GQA decoder (8 q-heads / 2 kv-heads, d=128, bf16).
+    qwen3 adds per-head RMS norms on q and k before the rotary embedding."""
     torch.manual_seed(0)
-    cfg = LlamaConfig(vocab_size=256, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
-                      num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=1024)
-    m = LlamaForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+    kw = dict(vocab_size=256, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
+              num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=1024)
+    if family == "qwen3":
+        cfg = Qwen3Config(**kw)
+        m = Qwen3ForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+    else:
+        cfg = LlamaConfig(**kw)
+        m = LlamaForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
     ids = torch.randint(0, 256, (B, P), generator=torch.Generator().manual_seed(1)).to(DEV)
     return m, cfg, ids
 
@@ -59,8 +66,9 @@ def slot_kv_oracle(cache, slot):
     return out
 
 
-def test_fused_arm_every_layer_and_step_vs_oracle():
-    m, cfg, ids = model()
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+def test_fused_arm_every_layer_and_step_vs_oracle(family):
+    m, cfg, ids = model(family)
     cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P)
     scale = m.model.layers[0].self_attn.scaling
     worst = [0.0]
@@ -102,9 +110,10 @@ def forced_logits(m, cache, ids, tokens):
     return torch.stack(outs)
 
 
-@pytest.mark.parametrize("arm", ["PACKED_KV_FUSED", "PACKED_GROUPED", "PACKED_KV_EXACT"])
-def test_arms_agree_with_native(arm):
-    m, cfg, ids = model()
+@pytest.mark.parametrize("family,arm", [("llama", "PACKED_KV_FUSED"), ("llama", "PACKED_GROUPED"),
+                                        ("llama", "PACKED_KV_EXACT"), ("qwen3", "PACKED_KV_FUSED")])
+def test_arms_agree_with_native(family, arm):
+    m, cfg, ids = model(family)
     tokens = torch.randint(0, 256, (B, 40), generator=torch.Generator().manual_seed(2)).to(DEV)
     restore = adapter.install(m)
     try:
