@@ -92,3 +92,15 @@ def test_unknown_arm_and_head_dim_refused():
     cfg.head_dim = 64
     with pytest.raises(IntegrityError):
         adapter.PackedKVCache(cfg, 1, 256)
+
+
+def test_slot_of_looped_layers():
+    """Slots of a looped model: current_ut * num_hidden_layers + layer_idx
+    (loop_kv_ac08_attention.py:67); out-of-range layers or loops refused."""
+    fake = SimpleNamespace(n_layers=24, store=SimpleNamespace(slots=96))
+    assert adapter.PackedKVCache.slot(fake, 0) == 0
+    assert adapter.PackedKVCache.slot(fake, 3, 2) == 51
+    assert adapter.PackedKVCache.slot(fake, 23, 3) == 95
+    for layer, ut in ((24, 0), (0, 4), (-1, 0)):
+        with pytest.raises(IntegrityError):
+            adapter.PackedKVCache.slot(fake, layer, ut)
