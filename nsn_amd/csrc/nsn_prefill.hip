@@ -8,17 +8,20 @@
 // here the packed blocks are dequantised tile by tile into LDS and never reach
 // HBM in dense form.
 //
-// Workgroup = 4 waves = 128 consecutive chunk queries of one (b, q-head);
+// Workgroup = 8 waves = 256 consecutive chunk queries of one (b, q-head);
 // each wave owns 32 queries (two 16-query MFMA column tiles).  Per 64-token
 // block:
 //   1. the raw block (K/V codes, K/V min and scale, K/V decode factors) is
-//      staged into LDS by DMA one block ahead;
-//   2. the 256 threads dequantise it once for the workgroup into
-//      K' [64 tok][128 ch] and V'^T [128 ch][64 tok] (fp16; the directions
-//      m + s*z, without the per-token factor);
+//      staged into LDS by DMA two blocks ahead;
+//   2. the 512 threads dequantise it once for the workgroup (threads 0-255
+//      K', 256-511 V'^T) into K' [64 tok][128 ch] and V'^T [128 ch][64 tok]
+//      (fp16; for fp16 data the per-token factor is folded in, for bf16
+//      data the directions m + s*z are stored and the factor is applied
+//      below), double-buffered so that the fill of the next block overlaps
+//      the products of this one;
 //   3. each wave computes S^T = K' Q^T and O^T += V'^T P^T on
-//      v_mfma_f32_16x16x32_f16, the per-token factors applied to the scores
-//      (K) and to the softmax weights (V) -- the transposed products keep P
+//      v_mfma_f32_16x16x32_f16 (bf16 data: the per-token factors applied to
+//      the scores (K) and to the softmax weights (V)) -- the transposed products keep P
 //      in registers: the C layout of S^T is already the B layout of P^T for
 //      a token order in which lane group g of a 32-token step holds tokens
 //      4g..4g+3 of both 16-token tiles.
