@@ -209,6 +209,8 @@ class PackedKVCache(Cache):
         """Raise on any flag raised since the cache was built (syncs)."""
         self.store.check_status()
         s = _dev.read_status(self.status)
+        if s & _lib.ST_TAIL_RANGE:
+            raise IntegrityError("Tail append position out of range")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s:

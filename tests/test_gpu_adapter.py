@@ -178,3 +178,83 @@ def test_decode_graph_replays_match_eager_steps():
     assert torch.equal(outs[True], outs[False])
     err = (outs[True][:-1] - ref[1:]).abs().max().item()
     assert err <= 1e-2 * ref.abs().max().item() + 1e-3, err
+
+
+def test_tail_append_to_places_like_tail_append_and_refuses_out_of_range():
+    """nsn_tail_append_to through the C ABI: the tokens land at
+    [end - n, end) of every row, bit for bit what nsn_tail_append writes at
+    offset end - n; an end outside [n, tail_cap] writes nothing and raises
+    NSN_ST_TAIL_RANGE (the kernel's own range check, set from the host)."""
+    from nsn_amd import _dev, _lib
+    lib = _lib.lib()
+    rows, n, cap = 6, 3, 20
+    g = torch.Generator(device=DEV).manual_seed(7)
+    k = torch.randn((rows, n, 128), generator=g, device=DEV).to(torch.float16)
+    v = torch.randn((rows, n, 128), generator=g, device=DEV).to(torch.float16)
+    stream = _dev.stream()
+    for end in (n, 11, cap):
+        kt_a = torch.zeros((rows, cap, 128), dtype=torch.float16, device=DEV)
+        vt_a, kt_b, vt_b = kt_a.clone(), kt_a.clone(), kt_a.clone()
+        end_t = torch.tensor([end], dtype=torch.int32, device=DEV)
+        st = _dev.new_status(DEV)
+        assert lib.nsn_tail_append_to(k.data_ptr(), v.data_ptr(), rows, n, n, kt_a.data_ptr(), vt_a.data_ptr(), cap,
+                                      end_t.data_ptr(), _lib.DTYPE_F16, st.data_ptr(), stream) == 0
+        assert lib.nsn_tail_append(k.data_ptr(), v.data_ptr(), rows, n, n, kt_b.data_ptr(), vt_b.data_ptr(), cap,
+                                   end - n, _lib.DTYPE_F16, stream) == 0
+        assert _dev.read_status(st) == 0
+        assert torch.equal(kt_a.view(torch.int16), kt_b.view(torch.int16))
+        assert torch.equal(vt_a.view(torch.int16), vt_b.view(torch.int16))
+        assert torch.equal(kt_a[:, end - n:end], k) and torch.equal(vt_a[:, end - n:end], v)
+    for end in (n - 1, cap + 1):
+        kt = torch.zeros((rows, cap, 128), dtype=torch.float16, device=DEV)
+        vt = kt.clone()
+        end_t = torch.tensor([end], dtype=torch.int32, device=DEV)
+        st = _dev.new_status(DEV)
+        assert lib.nsn_tail_append_to(k.data_ptr(), v.data_ptr(), rows, n, n, kt.data_ptr(), vt.data_ptr(), cap,
+                                      end_t.data_ptr(), _lib.DTYPE_F16, st.data_ptr(), stream) == 0
+        assert _dev.read_status(st) == _lib.ST_TAIL_RANGE
+        assert not kt.any() and not vt.any()
+
+
+def test_strict_decode_raises_on_nonfinite_tail():
+    """A nonfinite K token in the tail reaches the fused kernel's input flag:
+    the strict decode step raises NumericalFailure (the reference raises at
+    its finite check, loop_kv_ac08_attention.py:70-72)."""
+    from nsn_amd.errors import NumericalFailure
+    m, cfg, ids = model()
+    cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P)
+    restore = adapter.install(m)
+    try:
+        with torch.no_grad():
+            out = m(input_ids=ids, past_key_values=cache, use_cache=True)
+            cache.post_prefill()
+            cache.store.side(1, "K").tail[1, 0, 5, 17] = float("inf")
+            with pytest.raises(NumericalFailure):
+                m(input_ids=out.logits[:, -1:].argmax(-1), past_key_values=cache, use_cache=True)
+    finally:
+        restore()
+
+
+def test_check_status_reports_a_tail_range_flag():
+    """A device-position step whose tail end was pushed past the tail
+    capacity (from the host) appends nothing; check_status raises
+    IntegrityError for it."""
+    from nsn_amd.errors import IntegrityError
+    m, cfg, ids = model()
+    cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P, strict=False)
+    restore = adapter.install(m)
+    try:
+        with torch.no_grad():
+            m(input_ids=ids, past_key_values=cache, use_cache=True)
+        cache.post_prefill()
+        dg = adapter.DecodeGraph(m, cache, use_graph=False)
+        dg.step(ids[:, :1])
+        cache.check_status()
+        dg._load_counters()
+        cache.counters[B:].fill_(cache.store.tail_cap)   # the step's add makes it tail_cap + 1
+        dg.step(ids[:, 1:2])
+        torch.cuda.synchronize()
+        with pytest.raises(IntegrityError):
+            cache.check_status()
+    finally:
+        restore()
