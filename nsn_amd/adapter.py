@@ -14,7 +14,9 @@ call without the packed cache keep the original forward.  Here:
   ``update`` (the native route, used by prefill) appends and returns the
   exact dense reconstruction (restore of the packed blocks + the tail,
   loop_kv_pk01_cache.py:97-110); ``append_for_attention`` appends without
-  it (loop_kv_ac08_attention.py:20-24).
+  it (loop_kv_ac08_attention.py:20-24).  With ``prefill="packed"`` a
+  prefill chunk instead attends the packed context directly on the MFMA
+  prefill kernel (no dense K/V; the reference has no such route).
 - ``install(model)`` patches every ``model.model.layers[i].self_attn`` and
   returns a function that restores the original bound methods
   (loop_kv_ac08_attention.py:46-96).  Decode arms
@@ -105,8 +107,9 @@ class PackedKVCache(Cache):
     nsn_connection = True
 
     def __init__(self, config, batch, max_tokens, *, loops=1, bits=3, arm="PACKED_KV_FUSED", max_prefill=512,
-                 strict=True, device=None):
+                 strict=True, prefill="native", device=None):
         require(arm in ARMS, "Unknown connection arm")
+        require(prefill in ("native", "packed") and (prefill == "native" or arm != "NATIVE"), "Prefill route")
         heads_q = config.num_attention_heads
         heads = getattr(config, "num_key_value_heads", None) or heads_q
         head_dim = getattr(config, "head_dim", None) or config.hidden_size // heads_q
@@ -115,6 +118,7 @@ class PackedKVCache(Cache):
         self.n_layers, self.loops = config.num_hidden_layers, loops
         self.heads_q, self.heads = heads_q, heads
         self.batch, self.max_tokens, self.arm, self.strict = batch, max_tokens, arm, strict
+        self.prefill = prefill
         self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
                                       dtype=torch.float16, max_append=max(max_prefill, 1),
                                       device=device or torch.device("cuda:0"))
@@ -160,6 +164,25 @@ class PackedKVCache(Cache):
         self._check_position(slot, key.shape[2], kwargs or {})
         self._append(slot, key, value)
         return self.materialize(slot, "K", key.dtype), self.materialize(slot, "V", key.dtype)
+
+    def prefill_slot(self, slot, q, key, value, scale, kwargs=None):
+        """The packed prefill route: the chunk's queries attend the slot's
+        packed blocks + tail and the chunk's own K/V causally on the MFMA
+        prefill kernel (no dense K/V), then the chunk is appended.  Returns
+        [B, Hq, n, 128] in q's dtype.  The caller compresses between chunks
+        (post_prefill) so that every chunk fits the tail."""
+        self._check_position(slot, key.shape[2], kwargs or {})
+        require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
+                and key.shape[3] == DIM, "Packed KV coordinates")
+        q16 = q.to(torch.float16).contiguous()
+        k16, v16 = key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous()
+        has_ctx = self.store.length[slot] > 0
+        out = kernels.prefill_attention(q16, self.store.side(slot, "K") if has_ctx else None,
+                                        self.store.side(slot, "V") if has_ctx else None, self.store.lengths(slot),
+                                        k16, v16, scale=scale, check=self.strict,
+                                        status=None if self.strict else self.status)
+        self.store.append(slot, k16, v16)
+        return out.to(q.dtype)
 
     def append_for_attention(self, slot, key, value, kwargs=None):
         """Append the step's K/V without the dense restore (loop_kv_ac08_attention.py:20-24).
@@ -252,14 +275,16 @@ class PackedKVCache(Cache):
 
 def check_decode(module, q, cache, slot, position, mask):
     """Preconditions of the packed decode route (loop_kv_ac08_attention.py:26-33):
-    eval mode, no sliding window, q [B, Hq, 1, 128] bf16/fp16, and (strict
+    eval mode, no sliding window, q [B, Hq, 1, 128] bf16/fp16 (fp32 too on
+    the NATIVE arm, which is dense sdpa), and (strict
     mode) the step's position equal to the last cached token and the mask
     allowing every cached token.  Returns the slot's length."""
     total = cache.store.length[slot]
     require(not module.training and getattr(module, "sliding_window", None) is None,
             "Packed decode requires eval and no sliding window")
-    require(q.ndim == 4 and tuple(q.shape) == (cache.batch, cache.heads_q, 1, DIM)
-            and q.dtype in (torch.bfloat16, torch.float16), "Decode query shape/dtype")
+    dtypes = (torch.bfloat16, torch.float16) + ((torch.float32,) if cache.arm == "NATIVE" else ())
+    require(q.ndim == 4 and tuple(q.shape) == (cache.batch, cache.heads_q, 1, DIM) and q.dtype in dtypes,
+            "Decode query shape/dtype")
     if cache.strict:
         if position is not None:
             require(position.numel() >= 1 and int(position.reshape(-1)[-1].item()) == total - 1,
@@ -270,6 +295,19 @@ def check_decode(module, q, cache, slot, position, mask):
             allowed = bool(m.all()) if m.dtype == torch.bool else bool((m == 0).all())
             require(allowed, "Packed decode requires an all-allowed decode mask")
     return total
+
+
+def _require_causal(mask, n, past):
+    """A prefill mask (if any) must be the plain causal one over past + n
+    tokens: chunk query i sees tokens 0 .. past + i (synchronises)."""
+    if mask is None:
+        return
+    require(mask.ndim == 4 and tuple(mask.shape[-2:]) == (n, past + n), "Prefill mask shape")
+    i = torch.arange(n, device=mask.device)[:, None]
+    j = torch.arange(past + n, device=mask.device)[None, :]
+    want = j <= past + i
+    allowed = mask if mask.dtype == torch.bool else mask == 0
+    require(bool((allowed == want).all()), "Packed prefill requires a plain causal mask (no padding)")
 
 
 def _modeling(attn):
@@ -304,7 +342,13 @@ def install(model, module=None):
             cos, sin = position_embeddings
             q, k = _mod.apply_rotary_pos_emb(q, k, cos, sin)
             slot = cache.slot(self.layer_idx, current_ut)
-            if hidden_states.shape[1] != 1:
+            if hidden_states.shape[1] != 1 and cache.prefill == "packed":
+                # prefill over the packed context on the MFMA prefill kernel,
+                # which applies the causal mask itself (no padding)
+                if cache.strict:
+                    _require_causal(attention_mask, hidden_states.shape[1], cache.store.length[slot])
+                out = cache.prefill_slot(slot, q, k, v, self.scaling, kwargs).transpose(1, 2)
+            elif hidden_states.shape[1] != 1:
                 # prefill: the native route over the slot's dense K/V
                 kd, vd = cache.update_slot(slot, k, v, kwargs)
                 fn = _mod.ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,

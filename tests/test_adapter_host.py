@@ -39,8 +39,9 @@ def test_install_is_passthrough_without_packed_cache_and_restore_undoes_it(famil
     assert torch.equal(ref, got) and torch.equal(ref, again)
 
 
-def _stub_cache(length=10, strict=True, batch=1, heads_q=2):
-    return SimpleNamespace(store=SimpleNamespace(length=[length]), batch=batch, heads_q=heads_q, strict=strict)
+def _stub_cache(length=10, strict=True, batch=1, heads_q=2, arm="PACKED_KV_FUSED"):
+    return SimpleNamespace(store=SimpleNamespace(length=[length]), batch=batch, heads_q=heads_q, strict=strict,
+                           arm=arm)
 
 
 def _module(training=False, window=None):
@@ -104,3 +105,10 @@ def test_slot_of_looped_layers():
     for layer, ut in ((24, 0), (0, 4), (-1, 0)):
         with pytest.raises(IntegrityError):
             adapter.PackedKVCache.slot(fake, layer, ut)
+
+
+def test_check_decode_takes_fp32_queries_on_the_native_arm_only():
+    q = torch.zeros(1, 2, 1, 128, dtype=torch.float32)
+    assert adapter.check_decode(_module(), q, _stub_cache(arm="NATIVE"), 0, None, None) == 10
+    with pytest.raises(IntegrityError):
+        adapter.check_decode(_module(), q, _stub_cache(), 0, None, None)

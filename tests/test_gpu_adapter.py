@@ -258,3 +258,52 @@ def test_check_status_reports_a_tail_range_flag():
             cache.check_status()
     finally:
         restore()
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+def test_packed_prefill_is_as_accurate_as_the_native_route(family):
+    """A 600-token prompt in chunks of 200 (compressed after each), then 20
+    forced decode steps.  The packed prefill route (chunk queries attend the
+    packed context on the fp16 MFMA prefill kernel) and the reference's
+    native route (dense bf16 restore + sdpa) both run the bf16 model; the
+    truth is the same model in fp32 through the NATIVE arm (fp32 restore of
+    the same packed storage, fp32 sdpa).  The packed route's logits must be
+    no further from the truth than 1.5x the native route's, and layer 0's
+    packed blocks (independent of any attention) are bitwise equal."""
+    prompt = torch.randint(0, 256, (B, 600), generator=torch.Generator().manual_seed(4)).to(DEV)
+    tokens = torch.randint(0, 256, (B, 20), generator=torch.Generator().manual_seed(5)).to(DEV)
+    runs = {}
+    for name, route, arm, fp32 in (("native", "native", "PACKED_KV_FUSED", False),
+                                   ("packed", "packed", "PACKED_KV_FUSED", False),
+                                   ("truth", "native", "NATIVE", True)):
+        m, cfg, _ = model(family)
+        if fp32:
+            m = m.float()
+        restore = adapter.install(m)
+        try:
+            cache = adapter.PackedKVCache(cfg, B, 1024, arm=arm, max_prefill=200, prefill=route)
+            logits = []
+            with torch.no_grad():
+                for c in range(3):
+                    out = m(input_ids=prompt[:, 200 * c:200 * (c + 1)], past_key_values=cache, use_cache=True)
+                    cache.post_prefill()
+                    logits.append(out.logits.float())
+                for i in range(tokens.shape[1]):
+                    out = m(input_ids=tokens[:, i:i + 1], past_key_values=cache, use_cache=True)
+                    cache.post_decode()
+                    logits.append(out.logits.float())
+            cache.check_status()
+        finally:
+            restore()
+        runs[name] = (torch.cat([x.reshape(-1, x.shape[-1]) for x in logits]), cache)
+    truth = runs["truth"][0]
+    e_native = (runs["native"][0] - truth).abs().max().item()
+    e_packed = (runs["packed"][0] - truth).abs().max().item()
+    print(f"{family}: max |logit - fp32 truth|: native route {e_native:.4f}, packed route {e_packed:.4f}")
+    assert e_packed <= 1.5 * e_native + 1e-3, (e_packed, e_native)
+    c_ref, c_got = runs["native"][1], runs["packed"][1]
+    assert c_ref.store.compressed == c_got.store.compressed == [512, 512]
+    for name in ("K", "V"):
+        a, b = c_ref.store.side(0, name), c_got.store.side(0, name)
+        assert torch.equal(a.codes[:, :, :8], b.codes[:, :, :8])
+        assert torch.equal(a.norm[:, :, :8].view(torch.int16), b.norm[:, :, :8].view(torch.int16))
