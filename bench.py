@@ -811,8 +811,11 @@ def main_adapter(args):
         packed = kind != "hf_dense"
         graph = kind == "graph"
         arm = "PACKED_KV_FUSED" if graph else kind
+        # the graph run is the full packed path (prefill over the packed context
+        # on the MFMA prefill kernel); the eager fused run keeps the native prefill
         cache = (adapter.PackedKVCache(cfg, b_, T + warm + steps + 64, arm=arm, max_prefill=ch, strict=False,
-                                       device=dev) if packed else DynamicCache(config=cfg))
+                                       prefill="packed" if graph else "native", device=dev)
+                 if packed else DynamicCache(config=cfg))
         with torch.no_grad():
             t0 = time.perf_counter()
             for c in range(T // ch):
@@ -857,9 +860,9 @@ def main_adapter(args):
         gc.collect()
         torch.cuda.empty_cache()
         free = torch.cuda.mem_get_info()[0] / 2**30
-        log(f"[bench] adapter {kind}: prefill {pre_s:.1f} s, decode {ms:.2f} ms/step (host issue {host_ms:.2f} "
+        log(f"[bench] adapter {kind}: prefill {pre_s:.2f} s, decode {ms:.2f} ms/step (host issue {host_ms:.2f} "
             f"ms/step); {free:.0f} GiB free after release")
-        return ms, host_ms, kv_bytes
+        return ms, host_ms, kv_bytes, pre_s
 
     arms = args.adapter_arms.split(",")
     require_arms = {"hf_dense", "graph", "PACKED_KV_FUSED", "NATIVE"}
@@ -871,10 +874,10 @@ def main_adapter(args):
             res[kind] = run(kind)
     finally:
         restore()
-    graph_ms, graph_host, kv_bytes = res["graph"]
-    fused_ms, fused_host = res.get("PACKED_KV_FUSED", (None, None, 0))[:2]
+    graph_ms, graph_host, kv_bytes, graph_pre = res["graph"]
+    fused_ms, fused_host, _, fused_pre = res.get("PACKED_KV_FUSED", (None, None, 0, None))
     native_ms = res.get("NATIVE", (None,))[0]
-    dense_ms = res.get("hf_dense", (None,))[0]
+    dense_ms, _, _, dense_pre = res.get("hf_dense", (None, None, 0, None))
     nbytes = weight_bytes + kv_bytes
     achieved = nbytes / (graph_ms * 1e-3) / 1e9
     result = {
@@ -885,10 +888,12 @@ def main_adapter(args):
         "config": {"workload": "transformers connection: whole-model decode step through the packed cache",
                    "layers": a["layers"], "hidden": a["hidden"], "heads_q": a["heads"], "heads_kv": a["heads"],
                    "head_dim": D, "batch": b_, "prefill": T, "chunk": ch, "bits": 3,
-                   "arm": "PACKED_KV_FUSED, step replayed as a HIP graph"},
+                   "arm": "PACKED_KV_FUSED, step replayed as a HIP graph; packed prefill route"},
         "comparators": {"fused_eager_ms": _r(fused_ms), "fused_eager_host_issue_ms": _r(fused_host),
                         "graph_host_issue_ms": _r(graph_host), "native_arm_ms": _r(native_ms),
-                        "hf_dynamic_cache_ms": _r(dense_ms)},
+                        "hf_dynamic_cache_ms": _r(dense_ms),
+                        "prefill_s": {"packed_route": _r(graph_pre, 2), "native_route": _r(fused_pre, 2),
+                                      "hf_dynamic_cache": _r(dense_pre, 2)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole decode step (weights + packed K/V of 24 layers)", "algorithmic_bytes": nbytes},
