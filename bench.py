@@ -77,6 +77,9 @@ def parse():
     p.add_argument("--decode-steps", type=int, default=64, help="c4: decode steps timed (of the 256)")
     p.add_argument("--adapter-arms", default="hf_dense,graph,PACKED_KV_FUSED,NATIVE",
                    help="adapter: the runs, in order (the first packed one that ran gives the value)")
+    p.add_argument("--adapter-loops", type=int, default=1,
+                   help="adapter: apply the 24 layers this many times (Ouro-like looped model, 24*N slots); "
+                        "above 1 only the packed runs (graph, PACKED_KV_FUSED) with the packed prefill route")
     p.add_argument("--adapter-summary", metavar="DIR",
                    help="turn a rocprofv3 --kernel-trace run of `--workload adapter --adapter-arms graph` under DIR "
                         "into profiles/adapter_decode_graph.md")
@@ -767,6 +770,37 @@ STATS_DOC = {
 ADAPTER = dict(layers=24, hidden=2048, heads=16, inter=5632, vocab=49152, B=32, T=8192, chunk=512)
 
 
+def _Looped(base, loops):
+    """An Ouro-like looped model over a transformers Llama: the decoder
+    layers applied `loops` times with shared weights, the attention of loop
+    ut, layer i in cache slot ut * layers + i (it gets `current_ut`).  The
+    attention mask is left to the packed routes (causal, no padding)."""
+    import types
+
+    import torch
+
+    class Looped(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.base = base
+
+        def forward(self, input_ids, position_ids=None, past_key_values=None, use_cache=True, logits_to_keep=1):
+            mdl = self.base.model
+            h = mdl.embed_tokens(input_ids)
+            if position_ids is None:
+                past = past_key_values.get_seq_length()
+                position_ids = torch.arange(past, past + input_ids.shape[1], device=h.device)[None]
+            pe = mdl.rotary_emb(h, position_ids=position_ids)
+            for ut in range(loops):
+                for layer in mdl.layers:
+                    h = layer(h, attention_mask=None, position_ids=position_ids, past_key_values=past_key_values,
+                              use_cache=use_cache, position_embeddings=pe, current_ut=ut)
+            h = mdl.norm(h)
+            return types.SimpleNamespace(logits=self.base.lm_head(h[:, -logits_to_keep:]))
+
+    return Looped().eval()
+
+
 def main_adapter(args):
     """The transformers connection (nsn_amd.adapter) on an Ouro-1.4B-shaped
     Llama with random-init bf16 weights (24 layers = one loop of the C4 slot
@@ -798,14 +832,20 @@ def main_adapter(args):
     with torch.device(dev):
         m = LlamaForCausalLM(cfg)
     m = m.to(torch.bfloat16).eval()
+    loops = max(1, args.adapter_loops)
+    base = m
+    if loops > 1:
+        m = _Looped(base, loops)
     n_embed = a["vocab"] * a["hidden"]
-    weight_bytes = 2 * (sum(p.numel() for p in m.parameters()) - n_embed)   # the embedding is gathered, not read
+    # the embedding is gathered, not read; a looped model reads the layers once per loop
+    layer_params = sum(p.numel() for p in base.model.layers.parameters())
+    weight_bytes = 2 * (sum(p.numel() for p in base.parameters()) - n_embed + (loops - 1) * layer_params)
     gen = torch.Generator(device=dev).manual_seed(5)
     ids = torch.randint(0, a["vocab"], (b_, T), generator=gen, device=dev)
     toks = torch.randint(0, a["vocab"], (b_, warm + steps), generator=gen, device=dev)
-    log(f"[bench] adapter: {a['layers']} layers, {a['heads']} heads, B={b_}, prefill {T} (chunk {ch}), "
-        f"{steps} decode steps; weights {weight_bytes / 1e9:.2f} GB read per step")
-    restore = adapter.install(m)
+    log(f"[bench] adapter: {a['layers']} layers x {loops} loops, {a['heads']} heads, B={b_}, prefill {T} "
+        f"(chunk {ch}), {steps} decode steps; weights {weight_bytes / 1e9:.2f} GB read per step")
+    restore = adapter.install(base)
 
     def run(kind):
         packed = kind != "hf_dense"
@@ -813,8 +853,8 @@ def main_adapter(args):
         arm = "PACKED_KV_FUSED" if graph else kind
         # the graph run is the full packed path (prefill over the packed context
         # on the MFMA prefill kernel); the eager fused run keeps the native prefill
-        cache = (adapter.PackedKVCache(cfg, b_, T + warm + steps + 64, arm=arm, max_prefill=ch, strict=False,
-                                       prefill="packed" if graph else "native", device=dev)
+        cache = (adapter.PackedKVCache(cfg, b_, T + warm + steps + 64, loops=loops, arm=arm, max_prefill=ch,
+                                       strict=False, prefill="packed" if graph or loops > 1 else "native", device=dev)
                  if packed else DynamicCache(config=cfg))
         with torch.no_grad():
             t0 = time.perf_counter()
@@ -852,7 +892,7 @@ def main_adapter(args):
             cache.check_status()
             st = cache.store
             L, C = st.length[0], st.compressed[0]
-            kv_bytes = a["layers"] * b_ * a["heads"] * 2 * (C * 58 + (L - C) * 256)
+            kv_bytes = st.slots * b_ * a["heads"] * 2 * (C * 58 + (L - C) * 256)
         # the graph (and its memory pool) and the step closure hold the cache:
         # drop all of them before handing the memory back
         dg = None
@@ -865,6 +905,8 @@ def main_adapter(args):
         return ms, host_ms, kv_bytes, pre_s
 
     arms = args.adapter_arms.split(",")
+    if loops > 1:   # the dense comparators index caches by layer, not by (loop, layer)
+        arms = [k for k in arms if k in ("graph", "PACKED_KV_FUSED")]
     require_arms = {"hf_dense", "graph", "PACKED_KV_FUSED", "NATIVE"}
     if not arms or not set(arms) <= require_arms or "graph" not in arms:
         raise SystemExit(f"--adapter-arms: a comma list of {sorted(require_arms)} that includes graph")
@@ -881,12 +923,14 @@ def main_adapter(args):
     nbytes = weight_bytes + kv_bytes
     achieved = nbytes / (graph_ms * 1e-3) / 1e9
     result = {
-        "metric": "HF-connected decode ms/step (Ouro-1.4B-shaped Llama, 24 layers, B=32, ctx 8192, INT3 packed K/V)",
+        "metric": (f"HF-connected decode ms/step (Ouro-1.4B-shaped Llama, 24 layers x {loops} loops, B=32, "
+                   "ctx 8192, INT3 packed K/V)"),
         "value": round(graph_ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(graph_ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (random-init weights, torch seed 5; tokens from GPU generator seed 5)",
         "config": {"workload": "transformers connection: whole-model decode step through the packed cache",
-                   "layers": a["layers"], "hidden": a["hidden"], "heads_q": a["heads"], "heads_kv": a["heads"],
+                   "layers": a["layers"], "loops": loops, "slots": a["layers"] * loops, "hidden": a["hidden"],
+                   "heads_q": a["heads"], "heads_kv": a["heads"],
                    "head_dim": D, "batch": b_, "prefill": T, "chunk": ch, "bits": 3,
                    "arm": "PACKED_KV_FUSED, step replayed as a HIP graph; packed prefill route"},
         "comparators": {"fused_eager_ms": _r(fused_ms), "fused_eager_host_issue_ms": _r(fused_host),
@@ -896,7 +940,8 @@ def main_adapter(args):
                                       "hf_dynamic_cache": _r(dense_pre, 2)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole decode step (weights + packed K/V of 24 layers)", "algorithmic_bytes": nbytes},
+                     "kernel": f"whole decode step (weights + packed K/V of {a['layers'] * loops} slots)",
+                     "algorithmic_bytes": nbytes},
     }
     print(json.dumps(result), flush=True)
 

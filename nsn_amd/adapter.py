@@ -386,8 +386,10 @@ def install(model, module=None):
 
 
 class DecodeGraph:
-    """One decode step of ``model`` through ``cache`` (fused arm, strict=False,
-    one loop) captured as a HIP graph and replayed per step.
+    """One decode step of ``model`` through ``cache`` (fused arm, strict=False)
+    captured as a HIP graph and replayed per step.  A looped model (cache
+    ``loops`` > 1) passes ``current_ut`` to its attention itself; every slot
+    shares the device counters.
 
     Every launch argument of the step is fixed: the token and position ids
     sit in static buffers, the tail append and the attention read the
@@ -404,8 +406,8 @@ class DecodeGraph:
     """
 
     def __init__(self, model, cache, use_graph=True):
-        require(cache.arm == "PACKED_KV_FUSED" and not cache.strict and cache.loops == 1 and cache.capture is None,
-                "Decode graph: fused arm, strict=False, one loop, no capture hook")
+        require(cache.arm == "PACKED_KV_FUSED" and not cache.strict and cache.capture is None,
+                "Decode graph: fused arm, strict=False, no capture hook")
         self.model, self.cache, self.use_graph = model, cache, use_graph
         dev = cache.store.device
         self.ids = torch.zeros((cache.batch, 1), dtype=torch.long, device=dev)

@@ -307,3 +307,73 @@ def test_packed_prefill_is_as_accurate_as_the_native_route(family):
         a, b = c_ref.store.side(0, name), c_got.store.side(0, name)
         assert torch.equal(a.codes[:, :, :8], b.codes[:, :, :8])
         assert torch.equal(a.norm[:, :, :8].view(torch.int16), b.norm[:, :, :8].view(torch.int16))
+
+
+def looped(base, loops):
+    """The decoder layers of a transformers Llama applied `loops` times with
+    shared weights (an Ouro-like looped model); loop ut's attention gets
+    current_ut = ut and so reads cache slot ut * layers + i."""
+    import types
+
+    class Looped(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.base = base
+
+        def forward(self, input_ids, position_ids=None, past_key_values=None, use_cache=True, logits_to_keep=0):
+            mdl = self.base.model
+            h = mdl.embed_tokens(input_ids)
+            if position_ids is None:
+                past = past_key_values.get_seq_length()
+                position_ids = torch.arange(past, past + input_ids.shape[1], device=h.device)[None]
+            pe = mdl.rotary_emb(h, position_ids=position_ids)
+            for ut in range(loops):
+                for layer in mdl.layers:
+                    h = layer(h, attention_mask=None, position_ids=position_ids, past_key_values=past_key_values,
+                              use_cache=use_cache, position_embeddings=pe, current_ut=ut)
+            h = mdl.norm(h)
+            return types.SimpleNamespace(logits=self.base.lm_head(h[:, -logits_to_keep:]))
+
+    return Looped().eval()
+
+
+def test_looped_model_slots_vs_oracle_and_graph():
+    """2 layers x 2 loops = 4 slots.  The fused arm at every slot and decode
+    step against the oracle over that slot's packed bytes (the loops write
+    different K/V, so a wrong slot mapping fails), then the same decode as a
+    HIP graph equals its eager device-position steps bit for bit."""
+    base, cfg, ids = model()
+    m = looped(base, 2)
+    scale = base.model.layers[0].self_attn.scaling
+    restore = adapter.install(base)
+    try:
+        cache = adapter.PackedKVCache(cfg, B, 1024, loops=2, arm="PACKED_KV_FUSED", max_prefill=P)
+        seen = []
+
+        def capture(slot, total, q, out):
+            k, v = slot_kv_oracle(cache, slot)
+            ref, _ = O.decode_attention64(q.float().cpu().numpy(), k, v, scale=scale)
+            err = np.abs(out.float().cpu().numpy() - ref)
+            assert np.all(err <= 2e-3 + 1e-2 * np.abs(ref)), (slot, total, float(err.max()))
+            seen.append(slot)
+
+        cache.capture = capture
+        adapter.greedy(m, cache, ids, 10)
+        assert sorted(set(seen)) == [0, 1, 2, 3] and len(seen) == 40
+        # loop 1 re-applies the layers to different hidden states: its K differ from loop 0's
+        assert not torch.equal(cache.store.side(0, "K").tail, cache.store.side(2, "K").tail)
+
+        tokens = torch.randint(0, 256, (B, 70), generator=torch.Generator().manual_seed(6)).to(DEV)
+        outs = {}
+        for use_graph in (False, True):
+            c = adapter.PackedKVCache(cfg, B, 1024, loops=2, arm="PACKED_KV_FUSED", max_prefill=P, strict=False)
+            with torch.no_grad():
+                m(input_ids=ids, past_key_values=c, use_cache=True)
+            c.post_prefill()
+            dg = adapter.DecodeGraph(m, c, use_graph=use_graph)
+            outs[use_graph] = torch.stack([dg.step(tokens[:, i:i + 1])[:, -1].float().clone() for i in range(70)])
+            c.check_status()
+            assert c.store.length == [P + 70] * 4 and c.store.compressed == [128] * 4
+        assert torch.equal(outs[True], outs[False])
+    finally:
+        restore()
