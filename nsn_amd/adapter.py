@@ -54,6 +54,10 @@ from .kernels import BLOCK, DIM, PackedKV
 from .stream_cache import StreamingKVCache
 
 ARMS = ("NATIVE", "PACKED_GROUPED", "PACKED_KV_FUSED", "PACKED_KV_EXACT")
+# attention classes whose rotary step is transformers' standard
+# apply_rotary_pos_emb over the whole head (rotate_half form, no q/k norm):
+# their decode step can run it fused with the tail append (nsn_rope_append)
+FUSED_ROPE_CLASSES = ("LlamaAttention", "MistralAttention", "Qwen2Attention")
 
 try:   # transformers is optional: only the adapter needs it
     from transformers.cache_utils import Cache, CacheLayerMixin
@@ -107,7 +111,7 @@ class PackedKVCache(Cache):
     nsn_connection = True
 
     def __init__(self, config, batch, max_tokens, *, loops=1, bits=3, arm="PACKED_KV_FUSED", max_prefill=512,
-                 strict=True, prefill="native", device=None):
+                 strict=True, prefill="native", fused_rope=True, device=None):
         require(arm in ARMS, "Unknown connection arm")
         require(prefill in ("native", "packed") and (prefill == "native" or arm != "NATIVE"), "Prefill route")
         heads_q = config.num_attention_heads
@@ -119,6 +123,7 @@ class PackedKVCache(Cache):
         self.heads_q, self.heads = heads_q, heads
         self.batch, self.max_tokens, self.arm, self.strict = batch, max_tokens, arm, strict
         self.prefill = prefill
+        self.fused_rope = fused_rope
         self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
                                       dtype=torch.float16, max_append=max(max_prefill, 1),
                                       device=device or torch.device("cuda:0"))
@@ -183,6 +188,41 @@ class PackedKVCache(Cache):
                                         status=None if self.strict else self.status)
         self.store.append(slot, k16, v16)
         return out.to(q.dtype)
+
+    def rope_append(self, slot, q, key, value, cos, sin, kwargs=None):
+        """The decode step's rotary embedding and tail append in one launch
+        (nsn_rope_append): q [B, 1, Hq*128], key / value [B, 1, Hkv*128] (the
+        projection outputs, model dtype), cos / sin [B or 1, 1, 128].  Returns
+        the rotated q [B, Hq, 128]; the rotated key and the value go to the
+        tail as fp16 -- at the device tail end in device-position mode, else
+        at the host tail length (then counted)."""
+        B, st = self.batch, self.store
+        dt = q.dtype
+        require(dt in (torch.bfloat16, torch.float16) and all(t.dtype == dt for t in (key, value, cos, sin)),
+                "Rotary dtypes")
+        require(tuple(q.shape) == (B, 1, self.heads_q * DIM) and tuple(key.shape) == (B, 1, self.heads * DIM)
+                and key.shape == value.shape and all(t.is_contiguous() for t in (q, key, value, cos, sin)),
+                "Decode projections")
+        require(cos.shape == sin.shape and cos.shape[-1] == DIM and cos.numel() in (DIM, B * DIM), "Rotary rows")
+        cs_stride = 0 if cos.numel() == DIM else DIM
+        kt, vt = st.side(slot, "K").tail, st.side(slot, "V").tail
+        q_out = torch.empty((B, self.heads_q, DIM), dtype=dt, device=q.device)
+        if self.graph_mode:
+            tail_end, offset = self.counters.data_ptr() + 4 * B, 0
+        else:
+            self._check_position(slot, 1, kwargs or {})
+            offset = st.tail_len(slot)
+            require(offset + 1 <= st.tail_cap and st.length[slot] + 1 <= self.cap_len,
+                    "Tail overflow: compress before appending more tokens")
+            tail_end = None
+        rc = _lib.lib().nsn_rope_append(q.data_ptr(), key.data_ptr(), value.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                        cs_stride, B, self.heads_q, self.heads, q_out.data_ptr(), kt.data_ptr(),
+                                        vt.data_ptr(), st.tail_cap, tail_end, offset, _dev.dtype_code(dt),
+                                        self.status.data_ptr(), _dev.stream())
+        _lib.check(rc, "nsn_rope_append")
+        if not self.graph_mode:
+            st.length[slot] += 1
+        return q_out
 
     def append_for_attention(self, slot, key, value, kwargs=None):
         """Append the step's K/V without the dense restore (loop_kv_ac08_attention.py:20-24).
@@ -333,6 +373,21 @@ def install(model, module=None):
                                  **kwargs)
             input_shape = hidden_states.shape[:-1]
             hidden_shape = (*input_shape, -1, self.head_dim)
+            slot = cache.slot(self.layer_idx, current_ut)
+            if (hidden_states.shape[1] == 1 and cache.arm != "NATIVE" and cache.fused_rope
+                    and type(self).__name__ in FUSED_ROPE_CLASSES):
+                # decode step, fused: rotary + append in one launch, then the packed attention
+                cos, sin = position_embeddings
+                q3 = cache.rope_append(slot, self.q_proj(hidden_states), self.k_proj(hidden_states),
+                                       self.v_proj(hidden_states), cos, sin, kwargs)
+                total = check_decode(self, q3.unsqueeze(2), cache, slot, kwargs.get("position_ids"), attention_mask)
+                out = cache.attend(slot, q3, self.scaling).to(q3.dtype).unsqueeze(1)   # [B, 1, Hq, 128]
+                if not cache.graph_mode:
+                    cache.connection_calls[slot] += 1
+                if cache.capture is not None:
+                    require(not cache.graph_mode, "No capture hook under device positions")
+                    cache.capture(slot, total, q3, out[:, 0])
+                return self.o_proj(out.reshape(*input_shape, -1)), None
             q = self.q_proj(hidden_states).view(hidden_shape)
             k = self.k_proj(hidden_states).view(hidden_shape)
             if hasattr(self, "q_norm"):
@@ -341,7 +396,6 @@ def install(model, module=None):
             v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
             cos, sin = position_embeddings
             q, k = _mod.apply_rotary_pos_emb(q, k, cos, sin)
-            slot = cache.slot(self.layer_idx, current_ut)
             if hidden_states.shape[1] != 1 and cache.prefill == "packed":
                 # prefill over the packed context on the MFMA prefill kernel,
                 # which applies the causal mask itself (no padding)

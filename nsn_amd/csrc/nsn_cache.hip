@@ -45,6 +45,92 @@ __global__ __launch_bounds__(256) void tail_append_to_kernel(const uint4 *k_new,
     v_tail[dst] = v_new[src];
 }
 
+struct RopeParams {
+    const uint16_t *q, *k, *v, *cos, *sin;
+    int64_t cs_stride;   // elements between the cos/sin rows of two sequences (0: one row for all)
+    int64_t batch, heads_q, heads_kv;
+    uint16_t *q_out, *k_tail, *v_tail;
+    int64_t tail_cap;
+    const int32_t *tail_end;
+    int64_t offset;
+    int32_t *status;
+};
+
+// One decode token per sequence: rotary embedding of q and k as transformers'
+// apply_rotary_pos_emb computes it in the model dtype DT (x*cos and
+// rotate_half(x)*sin each rounded to DT, then their sum rounded to DT), the
+// rotated q written out, and the rotated k and the plain v converted to fp16
+// and appended to the tails.  16 threads per row (q rows, then k rows, then v
+// rows); thread j owns the channel pairs (c, c + 64) for c = 4j .. 4j + 3.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
+    using E = Elem<DT>;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t nq = p.batch * p.heads_q, nk = p.batch * p.heads_kv;
+    if (i >= (nq + 2 * nk) * 16) return;
+    const int64_t row = i >> 4;
+    const int c0 = 4 * static_cast<int>(i & 15);
+    const int kind = row < nq ? 0 : (row < nq + nk ? 1 : 2);
+    int64_t off = p.offset;
+    if (p.tail_end) {
+        const int64_t end = *p.tail_end;
+        if (end < 1 || end > p.tail_cap) {   // the rotated q is still written; the tails are not
+            if (i == 0) raise_status(p.status, NSN_ST_TAIL_RANGE);
+            if (kind != 0) return;
+        }
+        off = end - 1;
+    }
+    const int64_t r = kind == 0 ? row : (kind == 1 ? row - nq : row - nq - nk);   // (b, h) row of its tensor
+    const int64_t b = kind == 0 ? r / p.heads_q : r / p.heads_kv;
+    const uint16_t *src = (kind == 0 ? p.q : (kind == 1 ? p.k : p.v)) + r * kDim;
+    const uint2 a = *reinterpret_cast<const uint2 *>(src + c0);
+    const uint2 z = *reinterpret_cast<const uint2 *>(src + 64 + c0);
+    const uint16_t x1[4] = {static_cast<uint16_t>(a.x), static_cast<uint16_t>(a.x >> 16), static_cast<uint16_t>(a.y),
+                            static_cast<uint16_t>(a.y >> 16)};
+    const uint16_t x2[4] = {static_cast<uint16_t>(z.x), static_cast<uint16_t>(z.x >> 16), static_cast<uint16_t>(z.y),
+                            static_cast<uint16_t>(z.y >> 16)};
+    float o1[4], o2[4];
+    if (kind < 2) {
+        auto rd = [](float x) { return E::load(E::store(x)); };
+        const uint16_t *cs = p.cos + b * p.cs_stride, *sn = p.sin + b * p.cs_stride;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float u = E::load(x1[j]), w = E::load(x2[j]);
+            const float c1 = E::load(cs[c0 + j]), c2 = E::load(cs[64 + c0 + j]);
+            const float s1 = E::load(sn[c0 + j]), s2 = E::load(sn[64 + c0 + j]);
+            o1[j] = rd(rd(u * c1) + rd(-w * s1));
+            o2[j] = rd(rd(w * c2) + rd(u * s2));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            o1[j] = E::load(x1[j]);
+            o2[j] = E::load(x2[j]);
+        }
+    }
+    uint16_t *dst;
+    uint16_t h1[4], h2[4];
+    if (kind == 0) {
+        dst = p.q_out + r * kDim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h1[j] = E::store(o1[j]);
+            h2[j] = E::store(o2[j]);
+        }
+    } else {
+        dst = (kind == 1 ? p.k_tail : p.v_tail) + (r * p.tail_cap + off) * kDim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h1[j] = f32_to_f16_bits(o1[j]);
+            h2[j] = f32_to_f16_bits(o2[j]);
+        }
+    }
+    *reinterpret_cast<uint2 *>(dst + c0) = make_uint2(h1[0] | (static_cast<uint32_t>(h1[1]) << 16),
+                                                      h1[2] | (static_cast<uint32_t>(h1[3]) << 16));
+    *reinterpret_cast<uint2 *>(dst + 64 + c0) = make_uint2(h2[0] | (static_cast<uint32_t>(h2[1]) << 16),
+                                                           h2[2] | (static_cast<uint32_t>(h2[3]) << 16));
+}
+
 }  // namespace
 }  // namespace nsn
 
@@ -87,5 +173,33 @@ extern "C" int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t 
                        reinterpret_cast<hipStream_t>(stream), static_cast<const uint4 *>(k_new),
                        static_cast<const uint4 *>(v_new), rows, n, new_row_stride, static_cast<uint4 *>(k_tail),
                        static_cast<uint4 *>(v_tail), tail_cap, tail_end, chunks, status);
+    return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
+}
+
+extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, const void *cos, const void *sin,
+                               int64_t cs_stride, int64_t batch, int64_t heads_q, int64_t heads_kv, void *q_out,
+                               void *k_tail,
+                               void *v_tail, int64_t tail_cap, const int32_t *tail_end, int64_t offset, int dtype,
+                               int32_t *status, nsn_stream_t stream) {
+    if (batch < 0 || heads_q < 0 || heads_kv < 0 || tail_cap < 1 || (cs_stride != 0 && cs_stride < kDim))
+        return NSN_EINVAL;
+    if (dtype != NSN_DTYPE_F16 && dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
+    if (!tail_end && (offset < 0 || offset >= tail_cap)) return NSN_EINVAL;
+    if (batch == 0 || heads_q + heads_kv == 0) return NSN_OK;
+    if (!q || !k || !v || !cos || !sin || !q_out || !k_tail || !v_tail || !status) return NSN_EINVAL;
+    for (const void *ptr : {q, k, v, static_cast<const void *>(q_out), static_cast<const void *>(k_tail),
+                            static_cast<const void *>(v_tail)})
+        if (reinterpret_cast<uintptr_t>(ptr) & 7u) return NSN_EINVAL;
+    const int64_t threads = batch * (heads_q + 2 * heads_kv) * 16;
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffff) return NSN_EINVAL;
+    RopeParams p{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
+                 static_cast<const uint16_t *>(cos), static_cast<const uint16_t *>(sin), cs_stride, batch, heads_q,
+                 heads_kv,
+                 static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_tail), static_cast<uint16_t *>(v_tail),
+                 tail_cap, tail_end, offset, status};
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dtype == NSN_DTYPE_BF16) hipLaunchKernelGGL(rope_append_kernel<NSN_DTYPE_BF16>, dim3(blocks), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(rope_append_kernel<NSN_DTYPE_F16>, dim3(blocks), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }

@@ -377,3 +377,47 @@ def test_looped_model_slots_vs_oracle_and_graph():
         assert torch.equal(outs[True], outs[False])
     finally:
         restore()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shared_rows", [True, False])
+def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
+    """nsn_rope_append against transformers' own apply_rotary_pos_emb (Llama
+    rotary, the model dtype's rounding) and a plain fp16 cast of k and v:
+    the rotated q and the appended tail rows are bit-identical, at a host
+    offset and at a device tail end; other tail rows stay untouched."""
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding, apply_rotary_pos_emb
+    from nsn_amd import _dev, _lib
+    lib = _lib.lib()
+    b_, hq, hkv, cap = 3, 8, 2, 10
+    cfg = LlamaConfig(hidden_size=1024, num_attention_heads=hq, num_key_value_heads=hkv, head_dim=128,
+                      max_position_embeddings=8192)
+    rot = LlamaRotaryEmbedding(cfg).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    q = (torch.randn((b_, 1, hq * 128), generator=g, device=DEV) * 3).to(dtype)
+    k = (torch.randn((b_, 1, hkv * 128), generator=g, device=DEV) * 3).to(dtype)
+    v = torch.randn((b_, 1, hkv * 128), generator=g, device=DEV).to(dtype)
+    pos = torch.tensor([[517]], device=DEV) if shared_rows else torch.tensor([[17], [517], [4000]], device=DEV)
+    cos, sin = rot(q, pos)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    qr, kr = apply_rotary_pos_emb(q.view(b_, 1, hq, 128).transpose(1, 2), k.view(b_, 1, hkv, 128).transpose(1, 2),
+                                  cos, sin)
+    for device_end in (False, True):
+        q_out = torch.empty((b_, hq, 128), dtype=dtype, device=DEV)
+        kt = torch.zeros((b_ * hkv, cap, 128), dtype=torch.float16, device=DEV)
+        vt = torch.zeros_like(kt)
+        st = _dev.new_status(DEV)
+        end_t = torch.tensor([5], dtype=torch.int32, device=DEV)
+        rc = lib.nsn_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                 0 if shared_rows else 128, b_, hq, hkv, q_out.data_ptr(), kt.data_ptr(), vt.data_ptr(),
+                                 cap, end_t.data_ptr() if device_end else None, 4, _dev.dtype_code(dtype),
+                                 st.data_ptr(), _dev.stream())
+        assert rc == 0 and _dev.read_status(st) == 0
+        assert torch.equal(q_out.view(torch.int16), qr[:, :, 0].contiguous().view(torch.int16))
+        want_k = kr[:, :, 0].to(torch.float16).reshape(b_ * hkv, 128)
+        want_v = v.view(b_ * hkv, 128).to(torch.float16)
+        assert torch.equal(kt[:, 4].view(torch.int16), want_k.view(torch.int16))
+        assert torch.equal(vt[:, 4].view(torch.int16), want_v.view(torch.int16))
+        rest = torch.ones(cap, dtype=torch.bool)
+        rest[4] = False
+        assert not kt[:, rest].any() and not vt[:, rest].any()
