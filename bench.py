@@ -957,13 +957,13 @@ ADAPTER_DOC = ("rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -
 def adapter_summary(d):
     """profiles/adapter_decode_graph.md from the kernel trace of
     `bench.py --workload adapter --adapter-arms graph`: the kernels from the
-    first device-position tail append on (the decode phase: one eager warm-up
-    step, then warmup + steps graph replays), grouped by name, per step."""
+    first fused rotary + append on (the decode phase: one eager warm-up step,
+    then warmup + steps graph replays), grouped by name, per step."""
     rows = _rows((Path(d), "**/*kernel_trace.csv"))
     ks = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in rows)
-    first = next(i for i, k in enumerate(ks) if "tail_append_to_kernel" in k[2])
+    first = next(i for i, k in enumerate(ks) if "rope_append_kernel" in k[2])
     dec = ks[first:]
-    n_append = sum("tail_append_to_kernel" in k[2] for k in dec)
+    n_append = sum("rope_append_kernel" in k[2] for k in dec)
     layers = ADAPTER["layers"]
     if n_append % layers:
         raise SystemExit(f"{n_append} tail appends is not a multiple of {layers} layers")
