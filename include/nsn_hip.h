@@ -268,7 +268,9 @@ int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t rows, int64
 
 /*
  * One decode token per sequence, fused: the rotary position embedding of q
- * [batch, heads_q, 128] and k [batch, heads_kv, 128] (model dtype `dtype`,
+ * [batch, heads_q, 128] and k [batch, heads_kv, 128] (sequence b's heads at
+ * b * q_stride, resp. b * kv_stride elements -- slices of one fused QKV
+ * projection work; model dtype `dtype`,
  * fp16 or bf16; cos, sin rows of 128, sequence b's at b * cs_stride --
  * 0 for one row shared by all) exactly as transformers'
  * apply_rotary_pos_emb computes it in that dtype (x*cos and rotate_half(x)*sin
@@ -281,8 +283,8 @@ int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t rows, int64
  * (experiments/ac08/source/loop_kv_ac08_attention.py:59-66) -- about a dozen
  * elementwise kernels per layer.
  */
-int nsn_rope_append(const void *q, const void *k, const void *v, const void *cos, const void *sin,
-                    int64_t cs_stride, int64_t batch, int64_t heads_q, int64_t heads_kv, void *q_out, void *k_tail,
+int nsn_rope_append(const void *q, const void *k, const void *v, int64_t q_stride, int64_t kv_stride,
+                    const void *cos, const void *sin, int64_t cs_stride, int64_t batch, int64_t heads_q, int64_t heads_kv, void *q_out, void *k_tail,
                     void *v_tail, int64_t tail_cap, const int32_t *tail_end, int64_t offset, int dtype,
                     int32_t *status, nsn_stream_t stream);
 

@@ -192,7 +192,9 @@ class PackedKVCache(Cache):
     def rope_append(self, slot, q, key, value, cos, sin, kwargs=None):
         """The decode step's rotary embedding and tail append in one launch
         (nsn_rope_append): q [B, 1, Hq*128], key / value [B, 1, Hkv*128] (the
-        projection outputs, model dtype), cos / sin [B or 1, 1, 128].  Returns
+        projection outputs, model dtype; each row contiguous, rows of
+        sequences at any stride -- slices of one fused QKV output), cos / sin
+        [B or 1, 1, 128].  Returns
         the rotated q [B, Hq, 128]; the rotated key and the value go to the
         tail as fp16 -- at the device tail end in device-position mode, else
         at the host tail length (then counted)."""
@@ -201,7 +203,8 @@ class PackedKVCache(Cache):
         require(dt in (torch.bfloat16, torch.float16) and all(t.dtype == dt for t in (key, value, cos, sin)),
                 "Rotary dtypes")
         require(tuple(q.shape) == (B, 1, self.heads_q * DIM) and tuple(key.shape) == (B, 1, self.heads * DIM)
-                and key.shape == value.shape and all(t.is_contiguous() for t in (q, key, value, cos, sin)),
+                and key.shape == value.shape and all(t.stride(2) == 1 for t in (q, key, value))
+                and key.stride(0) == value.stride(0) and cos.is_contiguous() and sin.is_contiguous(),
                 "Decode projections")
         require(cos.shape == sin.shape and cos.shape[-1] == DIM and cos.numel() in (DIM, B * DIM), "Rotary rows")
         cs_stride = 0 if cos.numel() == DIM else DIM
@@ -215,8 +218,8 @@ class PackedKVCache(Cache):
             require(offset + 1 <= st.tail_cap and st.length[slot] + 1 <= self.cap_len,
                     "Tail overflow: compress before appending more tokens")
             tail_end = None
-        rc = _lib.lib().nsn_rope_append(q.data_ptr(), key.data_ptr(), value.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-                                        cs_stride, B, self.heads_q, self.heads, q_out.data_ptr(), kt.data_ptr(),
+        rc = _lib.lib().nsn_rope_append(q.data_ptr(), key.data_ptr(), value.data_ptr(), q.stride(0), key.stride(0),
+                                        cos.data_ptr(), sin.data_ptr(), cs_stride, B, self.heads_q, self.heads, q_out.data_ptr(), kt.data_ptr(),
                                         vt.data_ptr(), st.tail_cap, tail_end, offset, _dev.dtype_code(dt),
                                         self.status.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_rope_append")
@@ -378,8 +381,10 @@ def install(model, module=None):
                     and type(self).__name__ in FUSED_ROPE_CLASSES):
                 # decode step, fused: rotary + append in one launch, then the packed attention
                 cos, sin = position_embeddings
-                q3 = cache.rope_append(slot, self.q_proj(hidden_states), self.k_proj(hidden_states),
-                                       self.v_proj(hidden_states), cos, sin, kwargs)
+                w, bias, nq, nk = self._nsn_qkv
+                qkv = torch.nn.functional.linear(hidden_states, w, bias)       # one GEMM for q, k and v
+                q3 = cache.rope_append(slot, qkv[..., :nq], qkv[..., nq:nq + nk], qkv[..., nq + nk:], cos, sin,
+                                       kwargs)
                 total = check_decode(self, q3.unsqueeze(2), cache, slot, kwargs.get("position_ids"), attention_mask)
                 out = cache.attend(slot, q3, self.scaling).to(q3.dtype).unsqueeze(1)   # [B, 1, Hq, 128]
                 if not cache.graph_mode:
@@ -432,10 +437,22 @@ def install(model, module=None):
 
         changed.append((attn, original))
         attn.forward = types.MethodType(forward, attn)
+        if type(attn).__name__ in FUSED_ROPE_CLASSES:
+            # the decode step's q, k and v projections as one GEMM over
+            # concatenated weights (a copy made now: install after loading
+            # the weights; restore() drops it)
+            with torch.no_grad():
+                ws = [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]
+                bs = [attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias]
+                attn._nsn_qkv = (torch.cat(ws, 0).contiguous(),
+                                 None if bs[0] is None else torch.cat(bs, 0).contiguous(),
+                                 ws[0].shape[0], ws[1].shape[0])
 
     def restore():
         for a, orig in changed:
             a.forward = orig
+            if hasattr(a, "_nsn_qkv"):
+                del a._nsn_qkv
     return restore
 
 

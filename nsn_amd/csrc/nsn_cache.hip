@@ -48,6 +48,7 @@ __global__ __launch_bounds__(256) void tail_append_to_kernel(const uint4 *k_new,
 struct RopeParams {
     const uint16_t *q, *k, *v, *cos, *sin;
     int64_t cs_stride;   // elements between the cos/sin rows of two sequences (0: one row for all)
+    int64_t q_stride, kv_stride;   // elements between two sequences' rows of q, and of k and v
     int64_t batch, heads_q, heads_kv;
     uint16_t *q_out, *k_tail, *v_tail;
     int64_t tail_cap;
@@ -81,8 +82,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
         off = end - 1;
     }
     const int64_t r = kind == 0 ? row : (kind == 1 ? row - nq : row - nq - nk);   // (b, h) row of its tensor
-    const int64_t b = kind == 0 ? r / p.heads_q : r / p.heads_kv;
-    const uint16_t *src = (kind == 0 ? p.q : (kind == 1 ? p.k : p.v)) + r * kDim;
+    const int64_t heads = kind == 0 ? p.heads_q : p.heads_kv;
+    const int64_t b = r / heads;
+    const uint16_t *src = (kind == 0 ? p.q : (kind == 1 ? p.k : p.v)) + b * (kind == 0 ? p.q_stride : p.kv_stride) +
+                          (r - b * heads) * kDim;
     const uint2 a = *reinterpret_cast<const uint2 *>(src + c0);
     const uint2 z = *reinterpret_cast<const uint2 *>(src + 64 + c0);
     const uint16_t x1[4] = {static_cast<uint16_t>(a.x), static_cast<uint16_t>(a.x >> 16), static_cast<uint16_t>(a.y),
@@ -176,12 +179,14 @@ extern "C" int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t 
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }
 
-extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, const void *cos, const void *sin,
-                               int64_t cs_stride, int64_t batch, int64_t heads_q, int64_t heads_kv, void *q_out,
-                               void *k_tail,
+extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, int64_t q_stride, int64_t kv_stride,
+                               const void *cos, const void *sin, int64_t cs_stride, int64_t batch, int64_t heads_q,
+                               int64_t heads_kv, void *q_out, void *k_tail,
                                void *v_tail, int64_t tail_cap, const int32_t *tail_end, int64_t offset, int dtype,
                                int32_t *status, nsn_stream_t stream) {
     if (batch < 0 || heads_q < 0 || heads_kv < 0 || tail_cap < 1 || (cs_stride != 0 && cs_stride < kDim))
+        return NSN_EINVAL;
+    if (q_stride < heads_q * kDim || kv_stride < heads_kv * kDim || (q_stride & 3) || (kv_stride & 3))
         return NSN_EINVAL;
     if (dtype != NSN_DTYPE_F16 && dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
     if (!tail_end && (offset < 0 || offset >= tail_cap)) return NSN_EINVAL;
@@ -194,8 +199,8 @@ extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, cons
     const int64_t blocks = (threads + 255) / 256;
     if (blocks > 0x7fffffff) return NSN_EINVAL;
     RopeParams p{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-                 static_cast<const uint16_t *>(cos), static_cast<const uint16_t *>(sin), cs_stride, batch, heads_q,
-                 heads_kv,
+                 static_cast<const uint16_t *>(cos), static_cast<const uint16_t *>(sin), cs_stride, q_stride, kv_stride,
+                 batch, heads_q, heads_kv,
                  static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_tail), static_cast<uint16_t *>(v_tail),
                  tail_cap, tail_end, offset, status};
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);

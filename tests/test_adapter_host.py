@@ -33,7 +33,15 @@ def test_install_is_passthrough_without_packed_cache_and_restore_undoes_it(famil
         restore = adapter.install(m)
         assert all(l.self_attn.forward != o for l, o in zip(m.model.layers, originals))
         got = m(input_ids=ids).logits                      # DynamicCache: the original forward
+        fused = [hasattr(l.self_attn, "_nsn_qkv") for l in m.model.layers]
+        assert fused == [family == "llama"] * 2            # one QKV weight per Llama-family attention
+        if family == "llama":
+            a = m.model.layers[0].self_attn
+            w, bias, nq, nk = a._nsn_qkv
+            assert bias is None and (nq, nk) == (256, 128)
+            assert torch.equal(w, torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))
         restore()
+        assert not any(hasattr(l.self_attn, "_nsn_qkv") for l in m.model.layers)
         assert [l.self_attn.forward for l in m.model.layers] == originals
         again = m(input_ids=ids).logits
     assert torch.equal(ref, got) and torch.equal(ref, again)

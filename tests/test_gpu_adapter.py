@@ -408,7 +408,8 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
         vt = torch.zeros_like(kt)
         st = _dev.new_status(DEV)
         end_t = torch.tensor([5], dtype=torch.int32, device=DEV)
-        rc = lib.nsn_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        rc = lib.nsn_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), hq * 128, hkv * 128, cos.data_ptr(),
+                                 sin.data_ptr(),
                                  0 if shared_rows else 128, b_, hq, hkv, q_out.data_ptr(), kt.data_ptr(), vt.data_ptr(),
                                  cap, end_t.data_ptr() if device_end else None, 4, _dev.dtype_code(dtype),
                                  st.data_ptr(), _dev.stream())
