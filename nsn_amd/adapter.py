@@ -111,7 +111,7 @@ class PackedKVCache(Cache):
     nsn_connection = True
 
     def __init__(self, config, batch, max_tokens, *, loops=1, bits=3, arm="PACKED_KV_FUSED", max_prefill=512,
-                 strict=True, prefill="native", fused_rope=True, device=None):
+                 strict=True, prefill="native", fused_rope=True, auto_policy=False, device=None):
         require(arm in ARMS, "Unknown connection arm")
         require(prefill in ("native", "packed") and (prefill == "native" or arm != "NATIVE"), "Prefill route")
         heads_q = config.num_attention_heads
@@ -124,6 +124,12 @@ class PackedKVCache(Cache):
         self.batch, self.max_tokens, self.arm, self.strict = batch, max_tokens, arm, strict
         self.prefill = prefill
         self.fused_rope = fused_rope
+        # auto_policy: each slot runs the compression policy its previous
+        # append left pending (prefill or decode target) right before its
+        # next append -- the state post_prefill / post_decode would have
+        # left, for callers that never call them (transformers' generate)
+        self.auto_policy = auto_policy
+        self._pending = [None] * (self.n_layers * loops)
         self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
                                       dtype=torch.float16, max_append=max(max_prefill, 1),
                                       device=device or torch.device("cuda:0"))
@@ -149,9 +155,23 @@ class PackedKVCache(Cache):
         return s
 
     # ------------------------------------------------------------------ appends
+    def _policy(self, slot, n):
+        """auto_policy: run the slot's pending policy, then note the one this
+        append of n tokens leaves."""
+        if not self.auto_policy:
+            return
+        from .stream_cache import decode_target, prefill_target
+        st, kind = self.store, self._pending[slot]
+        if kind == "prefill":
+            st.compress_to(slot, max(st.compressed[slot], prefill_target(st.length[slot])))
+        elif kind == "decode":
+            st.compress_to(slot, decode_target(st.length[slot], st.compressed[slot]))
+        self._pending[slot] = "prefill" if n > 1 else "decode"
+
     def _append(self, slot, key, value):
         require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
                 and key.shape[3] == DIM, "Packed KV coordinates")
+        self._policy(slot, key.shape[2])
         self.store.append(slot, key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous())
 
     def _check_position(self, slot, n, kwargs):
@@ -181,6 +201,7 @@ class PackedKVCache(Cache):
                 and key.shape[3] == DIM, "Packed KV coordinates")
         q16 = q.to(torch.float16).contiguous()
         k16, v16 = key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous()
+        self._policy(slot, key.shape[2])
         has_ctx = self.store.length[slot] > 0
         out = kernels.prefill_attention(q16, self.store.side(slot, "K") if has_ctx else None,
                                         self.store.side(slot, "V") if has_ctx else None, self.store.lengths(slot),
@@ -214,6 +235,7 @@ class PackedKVCache(Cache):
             tail_end, offset = self.counters.data_ptr() + 4 * B, 0
         else:
             self._check_position(slot, 1, kwargs or {})
+            self._policy(slot, 1)
             offset = st.tail_len(slot)
             require(offset + 1 <= st.tail_cap and st.length[slot] + 1 <= self.cap_len,
                     "Tail overflow: compress before appending more tokens")
@@ -477,8 +499,9 @@ class DecodeGraph:
     """
 
     def __init__(self, model, cache, use_graph=True):
-        require(cache.arm == "PACKED_KV_FUSED" and not cache.strict and cache.capture is None,
-                "Decode graph: fused arm, strict=False, no capture hook")
+        require(cache.arm == "PACKED_KV_FUSED" and not cache.strict and cache.capture is None
+                and not cache.auto_policy, "Decode graph: fused arm, strict=False, no capture hook, no auto_policy "
+                "(the graph runs post_decode itself; call post_prefill before the first step)")
         self.model, self.cache, self.use_graph = model, cache, use_graph
         dev = cache.store.device
         self.ids = torch.zeros((cache.batch, 1), dtype=torch.long, device=dev)

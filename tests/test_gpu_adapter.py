@@ -422,3 +422,24 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
         rest = torch.ones(cap, dtype=torch.bool)
         rest[4] = False
         assert not kt[:, rest].any() and not vt[:, rest].any()
+
+
+def test_generate_with_auto_policy_matches_the_manual_policy():
+    """transformers' generate() never calls post_prefill / post_decode; with
+    auto_policy each slot applies the pending policy right before its next
+    append, which leaves the same cache state at every attention: the
+    greedy tokens equal the manual loop's, across a compression."""
+    m, cfg, ids = model()
+    m.generation_config.eos_token_id = None
+    m.generation_config.pad_token_id = 0
+    restore = adapter.install(m)
+    try:
+        manual = adapter.PackedKVCache(cfg, B, 1024, max_prefill=P)
+        want, _ = adapter.greedy(m, manual, ids, 90)
+        auto = adapter.PackedKVCache(cfg, B, 1024, max_prefill=P, auto_policy=True)
+        with torch.no_grad():
+            out = m.generate(ids, past_key_values=auto, max_new_tokens=90, do_sample=False)
+    finally:
+        restore()
+    assert torch.equal(out[:, P:], want)
+    assert auto.store.compressed == [128, 128] == manual.store.compressed
