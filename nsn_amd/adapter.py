@@ -35,6 +35,14 @@ attention, training mode and beam reordering are refused.  Slots are
 ``current_ut * num_hidden_layers + layer_idx`` (looped models pass
 ``current_ut``; others use loop 0).
 
+For Llama-family attention (``FUSED_ROPE_CLASSES``) the packed decode step
+runs its q/k/v projections as one GEMM over weights concatenated at
+``install`` and its rotary embedding + fp16 casts + tail append as one
+launch (``nsn_rope_append``, bit-identical to ``apply_rotary_pos_emb``).
+``DecodeGraph`` captures a whole decode step as one HIP graph.
+``auto_policy=True`` runs the compression policy per slot for callers that
+never call ``post_prefill`` / ``post_decode`` (transformers' ``generate``).
+
 Nothing here synchronises with the device when ``strict=False``: the
 position / mask checks (host syncs in the reference) are then skipped and
 nonfinite flags accumulate in the cache's status word, read by
