@@ -47,6 +47,37 @@ def test_library_rejects_bad_arguments_without_gpu_work():
     assert lib.nsn_pack_codes(None, 0, 3, None, None, None) == _lib.NSN_OK
 
 
+def test_device_position_appends_reject_bad_arguments_without_gpu_work():
+    """nsn_tail_append_to and nsn_rope_append validate on the host before any
+    launch (fake, never dereferenced addresses stand in for device buffers)."""
+    lib = _lib.lib()
+    E, OK, F16 = _lib.NSN_EINVAL, _lib.NSN_OK, _lib.DTYPE_F16
+    A = 1 << 20   # 16-byte aligned stand-in address
+
+    def tail_to(rows=2, n=1, stride=1, cap=8, end=A, dtype=F16, k=A):
+        return lib.nsn_tail_append_to(k, A, rows, n, stride, A, A, cap, end, dtype, A, None)
+    assert tail_to(rows=-1) == E
+    assert tail_to(n=3, stride=2) == E                 # row stride shorter than the tokens
+    assert tail_to(n=9, stride=9, cap=8) == E          # more tokens than the tail holds
+    assert tail_to(dtype=9) == E
+    assert tail_to(end=None) == E                      # no device position
+    assert tail_to(k=A + 8) == E                       # misaligned source
+    assert tail_to(rows=0) == OK                       # empty: no work
+
+    def rope(q_stride=8 * 128, kv_stride=2 * 128, cs=128, b=2, cap=8, end=A, offset=0, dtype=F16, q=A):
+        return lib.nsn_rope_append(q, A, A, q_stride, kv_stride, A, A, cs, b, 8, 2, A, A, A, cap, end, offset,
+                                   dtype, A, None)
+    assert rope(cs=64) == E                            # cos/sin rows overlap
+    assert rope(q_stride=8 * 128 - 4) == E             # q rows overlap
+    assert rope(kv_stride=2 * 128 + 2) == E            # 8-byte row alignment
+    assert rope(dtype=_lib.DTYPE_F32) == E
+    assert rope(end=None, offset=8) == E               # host offset past the tail
+    assert rope(cap=0) == E
+    assert rope(q=A + 4) == E
+    assert rope(q=None) == E
+    assert rope(b=0) == OK
+
+
 def test_planned_bytes_matches_reference_accounting():
     # loop_kv_pilot.py:407 and the paper's 3,724 B block (3072 + 640 + 12)
     assert primitives.planned_bytes((1, 1, 64, 128), 64, 4) == {"codes": 4096, "metadata": 640, "native": 0, "block_headers": 12}
