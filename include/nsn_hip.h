@@ -54,6 +54,7 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 #define NSN_OK 0
 #define NSN_EINVAL (-1)
 #define NSN_ELAUNCH (-2)
+#define NSN_ENOSPC (-3) /* nsn_decode_attention_static: workspace beyond the static scratch */
 
 /* Library version string. */
 const char *nsn_version(void);
@@ -211,6 +212,24 @@ int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, i
 /* Workspace floats needed by nsn_decode_attention for the given shape
  * (partials plus the per-(b, hq) partial counts that nsn_attention_merge reads). */
 int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_splits);
+
+/*
+ * nsn_decode_attention with no caller workspace and no allocation: the
+ * partials live in a file-scope device array of NSN_STATIC_SCRATCH_FLOATS
+ * floats (16 MiB) that each GPU the library runs on holds until the process
+ * ends.  args->partials is ignored.  A shape whose
+ * nsn_attention_workspace_floats() exceeds the maximum returns NSN_ENOSPC
+ * before anything is launched.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (concurrent streams, or another
+ * launch before this one's merge has finished) race; calls in stream order
+ * are safe.  Nothing in the array needs to start at zero: every partial and
+ * partial count the merge reads is written by the same call.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+#define NSN_STATIC_SCRATCH_FLOATS (4 * 1024 * 1024)
+int nsn_decode_attention_static(const nsn_attn_args *args, nsn_stream_t stream);
 
 /*
  * Chunked-prefill attention: n_q chunk queries per (sequence, q-head) attend

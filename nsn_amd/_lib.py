@@ -28,7 +28,8 @@ ST_NONFINITE_SCAN = 0x80
 ST_NONFINITE_ATTN_INPUT = 0x100
 ST_TAIL_RANGE = 0x200
 
-NSN_OK, NSN_EINVAL, NSN_ELAUNCH = 0, -1, -2
+NSN_OK, NSN_EINVAL, NSN_ELAUNCH, NSN_ENOSPC = 0, -1, -2, -3
+STATIC_SCRATCH_FLOATS = 4 * 1024 * 1024   # NSN_STATIC_SCRATCH_FLOATS
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -72,6 +73,7 @@ SIGNATURES = {
     "nsn_unpack_codes": (I32, [P, I64, I32, P, P]),
     "nsn_restore_blocks": (I32, [P, I32, P, P, P, I64, I64, I64, I32, P, I32, I64, P, I32, I64, I64, P, P]),
     "nsn_decode_attention": (I32, [ctypes.POINTER(AttnArgs), P]),
+    "nsn_decode_attention_static": (I32, [ctypes.POINTER(AttnArgs), P]),
     "nsn_attention_merge": (I32, [P, I64, I64, I32, P, P, I32, P, P]),
     "nsn_attention_workspace_floats": (I64, [I64, I64, I32]),
     "nsn_finite_scan": (I32, [I32, P, P, P, P, P, P]),
@@ -102,5 +104,6 @@ def lib():
 
 def check(rc, what):
     if rc != NSN_OK:
-        kind = {NSN_EINVAL: "invalid arguments", NSN_ELAUNCH: "kernel launch failed"}.get(rc, str(rc))
+        kind = {NSN_EINVAL: "invalid arguments", NSN_ELAUNCH: "kernel launch failed",
+                NSN_ENOSPC: f"workspace exceeds the static scratch ({STATIC_SCRATCH_FLOATS} floats)"}.get(rc, str(rc))
         raise RuntimeError(f"{what}: {kind}")

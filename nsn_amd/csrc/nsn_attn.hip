@@ -16,6 +16,8 @@
 // back from HBM go through identical arithmetic, the bridge route (restore V
 // to HBM, then attend) and the fused route give bitwise-equal outputs -- the
 // reference's route-equality property (AC/verify_loop_kv_vf01.py:41-50).
+#include <mutex>
+
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -502,3 +504,43 @@ int nsn_attention_merge(const float *partials, int64_t batch, int64_t heads_q, i
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode attention: the partials workspace is a file-scope
+// device array instead of caller memory.  Each device holds its own copy; its
+// address is looked up once per device (with that device current) and used
+// for every launch -- the array's name is a host-side stand-in and is never
+// passed to a kernel.
+static __device__ __align__(256) float scratch[NSN_STATIC_SCRATCH_FLOATS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch[kMaxDevices] = {};
+
+int scratch_ptr(float **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return NSN_ELAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return NSN_ELAUNCH;
+        g_scratch[dev] = static_cast<float *>(ptr);
+    }
+    *out = g_scratch[dev];
+    return NSN_OK;
+}
+}  // namespace
+
+extern "C" int nsn_decode_attention_static(const nsn_attn_args *a, nsn_stream_t stream) {
+    if (!a || a->batch <= 0 || a->heads_q <= 0 || a->n_splits <= 0) return NSN_EINVAL;
+    if (nsn_attention_workspace_floats(a->batch, a->heads_q, a->n_splits) > NSN_STATIC_SCRATCH_FLOATS)
+        return NSN_ENOSPC;
+    float *ws = nullptr;
+    const int rc = scratch_ptr(&ws);
+    if (rc != NSN_OK) return rc;
+    nsn_attn_args b = *a;
+    b.partials = ws;
+    return nsn_decode_attention(&b, stream);
+}
+

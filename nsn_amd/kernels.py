@@ -112,13 +112,17 @@ def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
 
 def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
                      kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
-                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True):
+                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True,
+                     static_workspace=False):
     """Batched single-query decode attention.
 
     q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
     ctx [B,Hq,128] fp32).  ``scores`` [B, Hq, cap] fp32 replaces K (the AF01
     FULL=False readout).  ``check`` syncs and raises NumericalFailure on any
-    nonfinite intermediate/output.
+    nonfinite intermediate/output.  ``static_workspace`` runs through
+    nsn_decode_attention_static: the partials live in the library's per-device
+    scratch array (at most ``_lib.STATIC_SCRATCH_FLOATS`` floats), so with
+    ``out``, ``ctx`` and ``status`` given the call allocates nothing.
     """
     _dev.require_gpu(q, seq_len)
     require(q.ndim == 3 and q.shape[2] == DIM and q.is_contiguous(), "Query shape/type")
@@ -158,7 +162,10 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
         kv_round_dtype = tdt
     dev = q.device
     need = workspace_floats(B, Hq, n_splits)
-    if workspace is None or workspace.numel() < need:
+    if static_workspace:
+        require(need <= _lib.STATIC_SCRATCH_FLOATS,
+                f"Decode workspace of {need} floats exceeds the static scratch ({_lib.STATIC_SCRATCH_FLOATS})")
+    elif workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.float32, device=dev)
     if out is None:
         out = torch.empty((B, Hq, DIM), dtype=out_dtype, device=dev)
@@ -184,14 +191,15 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     a.kv_round_dtype = _dev.dtype_code(kv_round_dtype)
     a.split_tokens = split_tokens
     a.n_splits = n_splits
-    a.partials = workspace.data_ptr()
+    a.partials = 0 if static_workspace else workspace.data_ptr()
     a.ctx = ctx.data_ptr()
     a.out = out.data_ptr()
     a.out_dtype = _dev.dtype_code(out_dtype)
     a.status = st.data_ptr()
     a.merge = 1 if merge else 0
-    rc = _lib.lib().nsn_decode_attention(a, _dev.stream())
-    _lib.check(rc, "nsn_decode_attention")
+    entry = "nsn_decode_attention_static" if static_workspace else "nsn_decode_attention"
+    rc = getattr(_lib.lib(), entry)(a, _dev.stream())
+    _lib.check(rc, entry)
     if check and status is None:
         s = _dev.read_status(st)
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
