@@ -354,15 +354,9 @@ def measured_encode_traffic():
 
 
 def make_workload(dev):
-    import torch
-    from nsn_amd import cache, synthetic
-    lengths = [int(x) for x in synthetic.ragged_lengths(2, B, LMIN, LMAX)]
-    gen = torch.Generator(device=dev).manual_seed(2)
-    log(f"[bench] generating C2 K/V on the GPU: B={B} Hkv={HKV} Lmax={LMAX} (lengths {min(lengths)}..{max(lengths)})")
-    k = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
-    v = synthetic.kv_tokens_torch(gen, (B, HKV, LMAX, D), dev)
-    q = torch.randn((B, HQ, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    return lengths, k, v, q
+    from nsn_amd import synthetic
+    log(f"[bench] generating C2 K/V on the GPU: B={B} Hkv={HKV} Lmax={LMAX}")
+    return synthetic.c2_workload(dev)
 
 
 def c2_encoder(dev, k):
@@ -432,10 +426,8 @@ def main_c3(args):
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     b_, hq, hkv, L, bits = C3["B"], C3["HQ"], C3["HKV"], C3["L"], C3["bits"]
-    gen = torch.Generator(device=dev).manual_seed(3)
     log(f"[bench] generating C3 K/V on the GPU: B={b_} Hkv={hkv} L={L}, {bits}-bit")
-    kv = synthetic.heavy_tailed_torch(gen, (2, b_, hkv, L, D), dev)     # [K | V]
-    q = torch.randn((b_, hq, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    kv, q = synthetic.c3_workload(dev)     # [K | V]
 
     # ---- encode: all 64-token blocks of K and V, one launch
     rows, nblk = 2 * b_ * hkv, L // 64

@@ -90,3 +90,36 @@ def heavy_tailed_torch(gen, shape, device, df=3.0, dtype=None):
     nrm = torch.empty(shape[:-1] + (1,), device=device, dtype=torch.float32)
     nrm.log_normal_(0.0, 1.0, generator=gen)
     return (x * nrm).to(dtype)
+
+
+# ------------------------------------------------------ benchmark workloads
+
+# BASELINE.json configs[2] (C2), configs[3] (C3), configs[4] (C4)
+C2 = dict(B=16, HQ=32, HKV=8, LMIN=16384, LMAX=32768, bits=3, seed=2)
+C3 = dict(B=64, HQ=16, HKV=4, L=8192, bits=5, seed=3)
+C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256, seed=4)
+
+
+def c2_workload(device):
+    """C2 on the GPU: ragged lengths (numpy rng 2), K and V [B, Hkv, LMAX, 128]
+    fp16 from the outlier-token generator and bf16 queries [B, Hq, 128]
+    (torch.Generator seed 2).  Returns (lengths, k, v, q)."""
+    import torch
+    c = C2
+    lengths = [int(x) for x in ragged_lengths(c["seed"], c["B"], c["LMIN"], c["LMAX"])]
+    gen = torch.Generator(device=device).manual_seed(c["seed"])
+    k = kv_tokens_torch(gen, (c["B"], c["HKV"], c["LMAX"], DIM), device)
+    v = kv_tokens_torch(gen, (c["B"], c["HKV"], c["LMAX"], DIM), device)
+    q = torch.randn((c["B"], c["HQ"], DIM), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+    return lengths, k, v, q
+
+
+def c3_workload(device):
+    """C3 on the GPU: K and V heavy-tailed [2, B, Hkv, L, 128] fp16 (K first)
+    and bf16 queries [B, Hq, 128] (torch.Generator seed 3)."""
+    import torch
+    c = C3
+    gen = torch.Generator(device=device).manual_seed(c["seed"])
+    kv = heavy_tailed_torch(gen, (2, c["B"], c["HKV"], c["L"], DIM), device)
+    q = torch.randn((c["B"], c["HQ"], DIM), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+    return kv, q

@@ -30,6 +30,9 @@ Pinning (what fixes each function; the tests live in tests/test_oracle.py):
 * attention oracles: closed-form fixtures (uniform / dominant / cancel / zero
   softmax, one-hot queries), split invariance of the merge, and the GQA
   repeat invariant.
+* chunked-prefill oracle: row i equals the decode oracle over context +
+  chunk[:i + 1]; constant keys give prefix means (closed form); planted
+  off-by-one causal masks fail both.
 """
 from __future__ import annotations
 
@@ -273,18 +276,53 @@ def decode_attention64(q, k, v, scale=SCALE):
 
     q: [B, Hq, 128]; k, v: [B, Hkv, T, 128] (any float); Hq = G * Hkv, q-head h
     reads kv-head h // G.  Returns (ctx [B,Hq,128] float64, p [B,Hq,T]).
+    One matrix product per (sequence, kv-head) serves its G query heads.
     """
     q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
     B, Hq, D = q.shape
-    Hkv = k.shape[1]
+    Hkv, T = k.shape[1], k.shape[2]
     G = Hq // Hkv
-    kk = np.repeat(k, G, axis=1)
-    vv = np.repeat(v, G, axis=1)
-    s = np.einsum("bhd,bhtd->bht", q, kk) * scale
-    p = softmax64(s)
-    return np.einsum("bht,bhtd->bhd", p, vv), p
+    ctx = np.empty((B, Hq, D))
+    p = np.empty((B, Hq, T))
+    for b in range(B):
+        for kv in range(Hkv):
+            kk = np.asarray(k[b, kv], np.float64)
+            vv = np.asarray(v[b, kv], np.float64)
+            hs = slice(kv * G, (kv + 1) * G)
+            pw = softmax64((q[b, hs] @ kk.T) * scale)            # [G, T]
+            p[b, hs] = pw
+            ctx[b, hs] = pw @ vv
+    return ctx, p
+
+
+def prefill_attention64(q, kctx, vctx, kch, vch, scale=SCALE, causal_shift=0):
+    """fp64 chunked-prefill attention of one sequence.
+
+    q [Hq, n, 128]; kctx / vctx [Hkv, L, 128] the context (packed blocks
+    restored, then the tail); kch / vch [Hkv, n, 128] the chunk's own K/V.
+    Chunk query i attends all L context tokens and chunk tokens 0 .. i
+    (0 .. i + causal_shift: a nonzero shift exists only to plant an off-by-one
+    mask in the oracle's own tests).  q-head h reads kv-head h // G.  Returns
+    [Hq, n, 128] float64.  The reference attends a chunk over its
+    materialised cache plus the chunk (loop_kv_pk01_cache.py:87-106) with the
+    model's causal attention; row i is the single-query attention of q[:, i]
+    over context + chunk[:i + 1] (decode_attention64), which
+    tests/test_oracle.py checks row by row.
+    """
+    q = np.asarray(q, np.float64)
+    Hq, n, D = q.shape
+    Hkv, L = kctx.shape[0], kctx.shape[1]
+    G = Hq // Hkv
+    hidden = np.arange(n)[None, :] > np.arange(n)[:, None] + causal_shift   # [query i, chunk token j]
+    out = np.empty((Hq, n, D))
+    for kv in range(Hkv):
+        k = np.concatenate([np.asarray(kctx[kv], np.float64), np.asarray(kch[kv], np.float64)])
+        v = np.concatenate([np.asarray(vctx[kv], np.float64), np.asarray(vch[kv], np.float64)])
+        for h in range(kv * G, (kv + 1) * G):
+            s = (q[h] @ k.T) * scale                                         # [n, L + n]
+            s[:, L:][hidden] = -np.inf
+            out[h] = softmax64(s) @ v
+    return out
 
 
 def readout64(scores, v, groups=1):

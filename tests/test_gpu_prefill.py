@@ -2,7 +2,8 @@
 
 Expected values: the context K/V restored by the oracle (C restatement of
 nsn_encode + nsn_decode, fp32 reconstructions), the tail and the chunk K/V as
-stored, then float64 causal softmax attention per (sequence, q-head).
+stored, then the oracle's float64 chunked-prefill attention
+(oracle.prefill_attention64, pinned row by row against the decode oracle).
 Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise, on
 top of the output's own rounding (bf16/fp16).  K/V and queries are N(0,1)
 activations, as in the chunked-prefill configuration: the kernel's MFMA
@@ -43,25 +44,6 @@ def restore_ctx(x16, length, bits, dtype):
     return np.concatenate(parts, axis=1) if parts else np.zeros((H, 0, 128), np.float32)
 
 
-def oracle_prefill(q, kctx, vctx, kch, vch):
-    """q [Hq, n, 128]; kctx/vctx [Hkv, L, 128]; kch/vch [Hkv, n, 128] -> [Hq, n, 128] float64."""
-    Hq, n, _ = q.shape
-    G = Hq // kch.shape[0]
-    out = np.zeros((Hq, n, 128))
-    for h in range(Hq):
-        kv = h // G
-        k = np.concatenate([kctx[kv], kch[kv]]).astype(np.float64)
-        v = np.concatenate([vctx[kv], vch[kv]]).astype(np.float64)
-        L = kctx.shape[1]
-        s = (q[h].astype(np.float64) @ k.T) * SCALE          # [n, L + n]
-        causal = np.arange(n)[:, None] < np.arange(n)[None, :]
-        s[:, L:][causal] = -np.inf
-        s -= s.max(axis=1, keepdims=True)
-        p = np.exp(s)
-        out[h] = (p @ v) / p.sum(axis=1, keepdims=True)
-    return out
-
-
 def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
     rng = np.random.default_rng(seed)
     T = max(max(ctx_lengths), 1)
@@ -82,7 +64,7 @@ def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
         L = ctx_lengths[b]
         kc = restore_ctx(kx[b], L, bits, dtype)
         vc = restore_ctx(vx[b], L, bits, dtype)
-        ref = oracle_prefill(q[b].float().numpy(), kc, vc, kch[b].float().numpy(), vch[b].float().numpy())
+        ref = O.prefill_attention64(q[b].float().numpy(), kc, vc, kch[b].float().numpy(), vch[b].float().numpy())
         ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11      # output rounding
         err = np.abs(got[b] - ref)
         bound = ATOL + (RTOL + ulp) * np.abs(ref)
@@ -91,8 +73,21 @@ def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_prefill_packed_context_tail_and_chunk(dtype):
-    # sequence 0: 4 blocks + 44 tail tokens; sequence 1: 1 block + 13 tail; chunk of 150 (two query tiles)
+    # sequence 0: 4 blocks + 44 tail tokens; sequence 1: 1 block + 13 tail; one query tile of 150
     run_case(21, 2, 4, 2, [300, 77], 150, 3, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_second_query_tile_ragged(dtype):
+    """A workgroup covers 256 chunk queries: 520 queries take three tiles, the
+    last with 8 rows, so the query offset, the end clamp and the causal mask
+    of queries >= 256 against chunk blocks are all compared with the oracle."""
+    run_case(25, 2, 4, 2, [300, 77], 520, 3, dtype)
+
+
+def test_prefill_c4_chunk_of_512():
+    # the C4 chunk size (two full query tiles) over a packed context + tail, GQA 2:1
+    run_case(26, 2, 4, 2, [1000, 130], 512, 3, torch.float16)
 
 
 def test_prefill_no_context_is_causal_attention():

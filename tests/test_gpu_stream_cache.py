@@ -16,7 +16,7 @@ import torch
 
 from nsn_amd.stream_cache import StreamingKVCache
 from oracle import oracle as O
-from tests.test_gpu_prefill import normal_tokens, oracle_prefill, restore_ctx
+from tests.test_gpu_prefill import normal_tokens, restore_ctx
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -76,7 +76,7 @@ def test_stream_cache_prefill_then_decode():
             C = cache.compressed[slot]
             kctx = np.concatenate([restore_ctx(k[b], C, 3, torch.float16)[:, :C], k[b][:, C:c0].astype(np.float32)], 1)
             vctx = np.concatenate([restore_ctx(v[b], C, 3, torch.float16)[:, :C], v[b][:, C:c0].astype(np.float32)], 1)
-            ref = oracle_prefill(q[b].astype(np.float32), kctx, vctx, k[b][:, c0:c0 + n].astype(np.float32),
+            ref = O.prefill_attention64(q[b].astype(np.float32), kctx, vctx, k[b][:, c0:c0 + n].astype(np.float32),
                                  v[b][:, c0:c0 + n].astype(np.float32))
             ok, err = within(out[b], ref, 2.0 ** -11)
             assert ok, (c0, b, err)

@@ -311,3 +311,56 @@ def test_gqa_head_map_and_split_invariance():
     a = np.exp(m - m.max())
     merged = (u * a[:, None]).sum(0) / (z * a).sum()
     assert np.allclose(merged, O.readout64(s[None, None], vv[None, None])[0, 0], atol=1e-13)
+
+
+# ------------------------------------------------------------- chunked prefill
+
+def _prefill_case(seed, Hq=4, Hkv=2, L=37, n=9):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((Hq, n, 128)) * 2
+    kc, vc = rng.standard_normal((2, Hkv, L, 128))
+    kn, vn = rng.standard_normal((2, Hkv, n, 128))
+    return q, kc, vc, kn, vn
+
+
+def _rows_match_decode(out, q, kc, vc, kn, vn):
+    """Row i of the prefill == decode attention of q[:, i] over context + chunk[:i+1]."""
+    n = q.shape[1]
+    for i in range(n):
+        k = np.concatenate([kc, kn[:, :i + 1]], axis=1)[None]
+        v = np.concatenate([vc, vn[:, :i + 1]], axis=1)[None]
+        ctx, _ = O.decode_attention64(q[None, :, i], k, v)
+        if not np.allclose(out[:, i], ctx[0], rtol=0, atol=1e-12):
+            return False
+    return True
+
+
+@pytest.mark.parametrize("L", [0, 37])
+def test_prefill_oracle_rows_are_decode_attention(L):
+    q, kc, vc, kn, vn = _prefill_case(7, L=L)
+    out = O.prefill_attention64(q, kc, vc, kn, vn)
+    assert _rows_match_decode(out, q, kc, vc, kn, vn)
+    # planted mistakes: a causal mask off by one either way fails the row check
+    for shift in (-1, 1):
+        with np.errstate(invalid="ignore"):     # (shift -1 with no context leaves row 0 nothing to attend)
+            bad = O.prefill_attention64(q, kc, vc, kn, vn, causal_shift=shift)
+        assert not _rows_match_decode(bad, q, kc, vc, kn, vn)
+
+
+def test_prefill_oracle_constant_keys_give_prefix_means():
+    """Equal keys -> uniform weights over every visible token: row i is the
+    mean of the L context values and chunk values 0..i (closed form)."""
+    rng = np.random.default_rng(8)
+    Hq, Hkv, L, n = 2, 1, 5, 7
+    q = rng.standard_normal((Hq, n, 128))
+    key = rng.standard_normal(128)
+    kc = np.broadcast_to(key, (Hkv, L, 128)).copy()
+    kn = np.broadcast_to(key, (Hkv, n, 128)).copy()
+    vc = rng.standard_normal((Hkv, L, 128))
+    vn = rng.standard_normal((Hkv, n, 128))
+    out = O.prefill_attention64(q, kc, vc, kn, vn)
+    allv = np.concatenate([vc[0], vn[0]])
+    want = np.stack([allv[:L + i + 1].mean(0) for i in range(n)])
+    assert np.allclose(out[0], want, atol=1e-12) and np.allclose(out[1], want, atol=1e-12)
+    bad = O.prefill_attention64(q, kc, vc, kn, vn, causal_shift=1)
+    assert not np.allclose(bad[0], want, atol=1e-6)
