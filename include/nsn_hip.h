@@ -49,6 +49,7 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 #define NSN_ST_TAIL_RANGE 0x200 /* tail append: device end position outside [n, tail_cap] */
 #define NSN_ST_NONFINITE_ATTN_INPUT 0x100 /* attention: nonfinite raw input read by the kernel
                                              (q, tail tokens; block metadata in the REFERENCE kernel) */
+#define NSN_ST_WORKSPACE 0x400  /* attention: the partial slots (n_splits) are too few for the FAST kernel's partition */
 
 /* Return codes. */
 #define NSN_OK 0
@@ -58,6 +59,11 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 
 /* Library version string. */
 const char *nsn_version(void);
+
+/* sizeof of the argument structs this library was built with, for bindings
+ * to check their own layouts against at load time: which = 0 nsn_kv_side,
+ * 1 nsn_attn_args, 2 nsn_prefill_args, 3 nsn_kscore_args; -1 otherwise. */
+int64_t nsn_abi_sizeof(int which);
 
 /*
  * Encode 64x128 blocks: token norm, per-channel min/max over the block,

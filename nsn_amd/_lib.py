@@ -27,6 +27,7 @@ ST_NONFINITE_OUTPUT = 0x40
 ST_NONFINITE_SCAN = 0x80
 ST_NONFINITE_ATTN_INPUT = 0x100
 ST_TAIL_RANGE = 0x200
+ST_WORKSPACE = 0x400
 
 NSN_OK, NSN_EINVAL, NSN_ELAUNCH, NSN_ENOSPC = 0, -1, -2, -3
 STATIC_SCRATCH_FLOATS = 4 * 1024 * 1024   # NSN_STATIC_SCRATCH_FLOATS
@@ -67,6 +68,7 @@ KS_U8, KS_PACKED, KS_FP16 = 0, 1, 2
 # symbol -> (restype, argtypes); must cover every function include/nsn_hip.h declares
 SIGNATURES = {
     "nsn_version": (ctypes.c_char_p, []),
+    "nsn_abi_sizeof": (I64, [I32]),
     "nsn_encode_blocks": (I32, [P, I32, I64, I64, I64, I64, I32, I32, I32, P, P, P, P, P, P, I64, I64, I64, P, P, P]),
     "nsn_block_factors": (I32, [P, P, P, P, I64, I64, I64, I32, P, P]),
     "nsn_pack_codes": (I32, [P, I64, I32, P, P, P]),
@@ -98,6 +100,12 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        # the argument structs are passed by pointer: a library built from other
+        # headers than these mirrors would read past or misread them on the GPU
+        for which, st in enumerate((KVSide, AttnArgs, PrefillArgs, KScoreArgs)):
+            if L.nsn_abi_sizeof(which) != ctypes.sizeof(st):
+                raise RuntimeError(f"{LIB_PATH}: {st.__name__} is {L.nsn_abi_sizeof(which)} bytes in the library, "
+                                   f"{ctypes.sizeof(st)} in the bindings -- rebuild (python -m nsn_amd.build)")
         _lib = L
     return _lib
 

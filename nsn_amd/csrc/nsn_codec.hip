@@ -788,7 +788,17 @@ void restore_dispatch_out(int out_dt, int tail_dt, dim3 grid, hipStream_t s, con
 
 extern "C" {
 
-const char *nsn_version(void) { return "nsn_hip 0.1 gfx950"; }
+const char *nsn_version(void) { return "nsn_hip 0.2 gfx950"; }
+
+int64_t nsn_abi_sizeof(int which) {
+    switch (which) {
+        case 0: return static_cast<int64_t>(sizeof(nsn_kv_side));
+        case 1: return static_cast<int64_t>(sizeof(nsn_attn_args));
+        case 2: return static_cast<int64_t>(sizeof(nsn_prefill_args));
+        case 3: return static_cast<int64_t>(sizeof(nsn_kscore_args));
+        default: return -1;
+    }
+}
 
 int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blocks, int64_t x_outer_stride,
                       int64_t x_token_offset, int bits, int norm_order, int zero_flat_scale, uint8_t *codes,

@@ -901,7 +901,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
             segment<BITS, QDT, SCORES, GRP>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
                                             at(nk_l), at(nv_l), static_cast<int>(k), static_cast<int>(n));
         } else {
-            raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // workspace too small for this layout
+            raise_status(p.status, NSN_ST_WORKSPACE);   // workspace too small for this layout
         }
         return;
     }
@@ -942,7 +942,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
                                             (i1 * kBlockTok < T) ? i1 * kBlockTok : T, at(nk_l), at(nv_l), slot,
                                             count);
         } else {
-            raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // workspace too small for this layout
+            raise_status(p.status, NSN_ST_WORKSPACE);   // workspace too small for this layout
         }
         g += i1 - i0;
         i0 = 0;

@@ -202,6 +202,8 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     _lib.check(rc, entry)
     if check and status is None:
         s = _dev.read_status(st)
+        if s & _lib.ST_WORKSPACE:
+            raise IntegrityError("Decode workspace too small: n_splits below the fast kernel's partial slots")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):

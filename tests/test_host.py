@@ -163,3 +163,19 @@ def test_stream_cache_policy_matches_reference_formulas():
         L += 1
         C = decode_target(L, C)
         assert C % 64 == 0 and 64 <= L - C < 128
+
+
+def test_abi_struct_sizes_match_the_bindings():
+    """The library reports the sizes of the argument structs it was built with;
+    the ctypes mirrors must match them (a stale library whose nsn_attn_args
+    differs from the bindings would read past the struct on the GPU)."""
+    import ctypes
+    from nsn_amd import _lib
+    lib = _lib.lib()
+    for which, st in enumerate((_lib.KVSide, _lib.AttnArgs, _lib.PrefillArgs, _lib.KScoreArgs)):
+        assert lib.nsn_abi_sizeof(which) == ctypes.sizeof(st), st.__name__
+    assert lib.nsn_abi_sizeof(4) == -1
+
+    class Grown(ctypes.Structure):   # a layout with one more field than the library's
+        _fields_ = _lib.AttnArgs._fields_ + [("extra", ctypes.c_void_p)]
+    assert lib.nsn_abi_sizeof(1) != ctypes.sizeof(Grown)

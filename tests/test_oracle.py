@@ -364,3 +364,64 @@ def test_prefill_oracle_constant_keys_give_prefix_means():
     assert np.allclose(out[0], want, atol=1e-12) and np.allclose(out[1], want, atol=1e-12)
     bad = O.prefill_attention64(q, kc, vc, kn, vn, causal_shift=1)
     assert not np.allclose(bad[0], want, atol=1e-6)
+
+
+# --------------------------------------------- PyTorch-CPU restatement (bench baseline)
+
+def test_torch_cpu_restatement_matches_goldens(golden):
+    """oracle/torch_cpu.py (timed as bench.py's cpu_baseline) is pinned to the
+    same goldens: unpack3 of the golden bitstream equals the C oracle's codes,
+    nsn_int3_qdq and nsn_decode reproduce the golden outputs bit for bit."""
+    from oracle import torch_cpu as T
+    G = golden("c0.npz")
+    k, v = gi.config0_inputs()
+    for name, x in (("k", k), ("v", v)):
+        q, n16, m16, s16, err = O.nsn_encode(x.astype(np.float32), 3)
+        codes = T.unpack3(torch.from_numpy(G[name + "_codes"]), (32, 64, 128))
+        assert np.array_equal(codes.numpy(), q.reshape(32, 64, 128))
+        y = T.nsn_int3_qdq(torch.from_numpy(x))                      # fp16 in, fp16 out
+        assert np.array_equal(y.view(torch.int16).numpy().view(np.uint16), G[name + "_qdq"])
+        yd = T.nsn_decode(codes, torch.from_numpy(G[name + "_norm"].view(np.float16)).reshape(32, 64, 1),
+                          torch.from_numpy(G[name + "_min"].view(np.float16)).reshape(32, 1, 128),
+                          torch.from_numpy(G[name + "_scale"].view(np.float16)).reshape(32, 1, 128), torch.float16)
+        assert np.array_equal(yd.view(torch.int16).numpy().view(np.uint16), G[name + "_qdq"])
+    C = golden("codec.npz")
+    for bits, tensors in gi.pilot_fixture_tensors().items():
+        if bits != 3:
+            continue
+        for i, t in enumerate(tensors):
+            key = f"b3|t{i}|"
+            q = T.unpack3(torch.from_numpy(C[key + "codes"]), C[key + "decoded"].shape)
+            y = T.nsn_decode(q, torch.from_numpy(C[key + "norm"].view(np.float16)),
+                             torch.from_numpy(C[key + "min"].view(np.float16)),
+                             torch.from_numpy(C[key + "scale"].view(np.float16)))
+            assert np.array_equal(y.numpy().view(np.uint32), C[key + "decoded"]), key
+
+
+def test_torch_cpu_unpack3_kat_and_bridge_vs_fp64():
+    from oracle import torch_cpu as T
+    # the reference's KAT (loop_kv_pk01_cache.py:175-179): codes (arange*5+3)%8 round-trip
+    codes = ((np.arange(1000) * 5 + 3) % 8).astype(np.uint8)
+    packed = O.pack_codes(codes, 3)
+    assert np.array_equal(T.unpack3(torch.from_numpy(packed), (1000,)).numpy(), codes)
+    # the bridge readout equals the fp64 oracle over the same restored K/V (GQA 4:1, blocks + tail)
+    rng = np.random.default_rng(5)
+    H, nb, tail = 2, 3, 37
+    side = []
+    for _ in range(2):
+        x = rng.standard_normal((H, nb, 64, 128)).astype(np.float32)
+        q_, n16, m16, s16, err = O.nsn_encode(x, 3)
+        assert err == 0
+        blocks = (torch.from_numpy(O.pack_codes(q_.reshape(H * nb, -1), 3).reshape(H, nb, 3072)),
+                  torch.from_numpy(n16.view(np.float16)), torch.from_numpy(m16.view(np.float16)),
+                  torch.from_numpy(s16.view(np.float16)))
+        t = torch.from_numpy(rng.standard_normal((H, tail, 128)).astype(np.float16))
+        full = np.concatenate([O.nsn_decode_f32(q_, n16, m16, s16).reshape(H, nb * 64, 128), t.float().numpy()], 1)
+        side.append((blocks, t, full))
+    q = torch.from_numpy(rng.standard_normal((8, 128)).astype(np.float32))
+    got = T.bridge_readout(q, side[0][0], side[0][1], side[1][0], side[1][1]).numpy()
+    ref, _ = O.decode_attention64(q.numpy()[None], side[0][2][None], side[1][2][None])
+    assert np.allclose(got, ref[0], rtol=1e-4, atol=1e-5)
+    # planted mistake: the head map h % Hkv instead of h // G is far off
+    bad = T.bridge_readout(q[[0, 4, 1, 5, 2, 6, 3, 7]], side[0][0], side[0][1], side[1][0], side[1][1]).numpy()
+    assert not np.allclose(bad[[0, 2, 4, 6, 1, 3, 5, 7]], ref[0], rtol=1e-4, atol=1e-5)
