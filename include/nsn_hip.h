@@ -50,6 +50,9 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
 #define NSN_ST_NONFINITE_ATTN_INPUT 0x100 /* attention: nonfinite raw input read by the kernel
                                              (q, tail tokens; block metadata in the REFERENCE kernel) */
 #define NSN_ST_WORKSPACE 0x400  /* attention: the partial slots (n_splits) are too few for the FAST kernel's partition */
+#define NSN_ST_CAPACITY 0x800   /* attention: a sequence's blocks or tail lie past the cache's capacity
+                                   (blocks > block_cap or seq_len - 64*blocks > tail_cap); the FAST
+                                   kernel reads nothing of that sequence */
 
 /* Return codes. */
 #define NSN_OK 0

@@ -73,6 +73,28 @@ except ImportError:   # pragma: no cover - the image ships transformers
     Cache, CacheLayerMixin = object, object
 
 
+def sliding_window(config, layer_idx):
+    """The attention window of layer ``layer_idx`` under ``config`` (None: full
+    attention).  transformers keeps it in the config, not the module:
+    ``layer_types`` entries ``"sliding_attention"``, or ``sliding_window``
+    unless ``use_sliding_window`` is set false (Qwen2's default)."""
+    window = getattr(config, "sliding_window", None)
+    types_ = getattr(config, "layer_types", None)
+    if types_ is not None and layer_idx is not None and 0 <= layer_idx < len(types_):
+        return window if "sliding" in str(types_[layer_idx]) else None
+    if getattr(config, "use_sliding_window", True) is False:
+        return None
+    return window
+
+
+def _refuse_window(config, layer_idx, capacity):
+    """The packed decode attends every cached token: a window shorter than what
+    the cache can hold would change the result, so it is refused."""
+    window = sliding_window(config, layer_idx)
+    require(window is None or window >= capacity,
+            f"Packed decode refuses sliding-window attention (window {window} < cache capacity {capacity})")
+
+
 class _PackedLayer(CacheLayerMixin):
     """One slot of the packed cache seen through transformers' layer API."""
 
@@ -138,6 +160,10 @@ class PackedKVCache(Cache):
         # left, for callers that never call them (transformers' generate)
         self.auto_policy = auto_policy
         self._pending = [None] * (self.n_layers * loops)
+        # refused here, before any append changes the cache
+        for i in range(self.n_layers):
+            _refuse_window(config, i, max_tokens)
+        self.config = config
         self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
                                       dtype=torch.float16, max_append=max(max_prefill, 1),
                                       device=device or torch.device("cuda:0"))
@@ -307,6 +333,8 @@ class PackedKVCache(Cache):
         s = _dev.read_status(self.status)
         if s & _lib.ST_TAIL_RANGE:
             raise IntegrityError("Tail append position out of range")
+        if s & _lib.ST_CAPACITY:
+            raise IntegrityError("Sequence length past the cache's block / tail capacity")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s:
@@ -355,6 +383,9 @@ def check_decode(module, q, cache, slot, position, mask):
     total = cache.store.length[slot]
     require(not module.training and getattr(module, "sliding_window", None) is None,
             "Packed decode requires eval and no sliding window")
+    config = getattr(module, "config", None)
+    if config is not None:
+        _refuse_window(config, getattr(module, "layer_idx", None), getattr(cache, "max_tokens", 0))
     dtypes = (torch.bfloat16, torch.float16) + ((torch.float32,) if cache.arm == "NATIVE" else ())
     require(q.ndim == 4 and tuple(q.shape) == (cache.batch, cache.heads_q, 1, DIM) and q.dtype in dtypes,
             "Decode query shape/dtype")
@@ -387,6 +418,28 @@ def _modeling(attn):
     return sys.modules[type(attn).__module__]
 
 
+def _qkv_sources(attn):
+    ps = [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.q_proj.bias, attn.k_proj.bias,
+          attn.v_proj.bias]
+    return tuple(None if t is None else (t.data_ptr(), t._version, t.dtype, t.device) for t in ps)
+
+
+def _fused_qkv(attn):
+    """The decode step's q, k and v projections as one GEMM: the three weights
+    (and biases) concatenated, rebuilt whenever a source weight was replaced,
+    moved, cast or written in place since the last build (restore() drops it)."""
+    key = _qkv_sources(attn)
+    cached = getattr(attn, "_nsn_qkv", None)
+    if cached is None or getattr(attn, "_nsn_qkv_key", None) != key:
+        with torch.no_grad():
+            ws = [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]
+            bs = [attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias]
+            cached = (torch.cat(ws, 0).contiguous(), None if bs[0] is None else torch.cat(bs, 0).contiguous(),
+                      ws[0].shape[0], ws[1].shape[0])
+        attn._nsn_qkv, attn._nsn_qkv_key = cached, key
+    return cached
+
+
 def install(model, module=None):
     """Patch the attention of every decoder layer (instances only) and return
     ``restore()``, which puts every original bound method back
@@ -411,7 +464,7 @@ def install(model, module=None):
                     and type(self).__name__ in FUSED_ROPE_CLASSES):
                 # decode step, fused: rotary + append in one launch, then the packed attention
                 cos, sin = position_embeddings
-                w, bias, nq, nk = self._nsn_qkv
+                w, bias, nq, nk = _fused_qkv(self)
                 qkv = torch.nn.functional.linear(hidden_states, w, bias)       # one GEMM for q, k and v
                 q3 = cache.rope_append(slot, qkv[..., :nq], qkv[..., nq:nq + nk], qkv[..., nq + nk:], cos, sin,
                                        kwargs)
@@ -468,21 +521,14 @@ def install(model, module=None):
         changed.append((attn, original))
         attn.forward = types.MethodType(forward, attn)
         if type(attn).__name__ in FUSED_ROPE_CLASSES:
-            # the decode step's q, k and v projections as one GEMM over
-            # concatenated weights (a copy made now: install after loading
-            # the weights; restore() drops it)
-            with torch.no_grad():
-                ws = [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]
-                bs = [attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias]
-                attn._nsn_qkv = (torch.cat(ws, 0).contiguous(),
-                                 None if bs[0] is None else torch.cat(bs, 0).contiguous(),
-                                 ws[0].shape[0], ws[1].shape[0])
+            _fused_qkv(attn)
 
     def restore():
         for a, orig in changed:
             a.forward = orig
-            if hasattr(a, "_nsn_qkv"):
-                del a._nsn_qkv
+            for name in ("_nsn_qkv", "_nsn_qkv_key"):
+                if hasattr(a, name):
+                    delattr(a, name)
     return restore
 
 
@@ -519,6 +565,7 @@ class DecodeGraph:
         self.replays = 0
         cache._workspace(cache.cap_len)
         self._reload = True
+        self._failed = None   # set when the policy after a step raised: no further steps
 
     def _load_counters(self):
         st, B = self.cache.store, self.cache.batch
@@ -541,6 +588,8 @@ class DecodeGraph:
         [B, 1, vocab]; under replay this is the graph's static output buffer,
         overwritten by the next step."""
         st = self.cache.store
+        if self._failed is not None:
+            raise IntegrityError(f"Decode graph stopped: {self._failed}")
         self.ids.copy_(tokens)
         if self._reload:
             self._load_counters()
@@ -570,7 +619,15 @@ class DecodeGraph:
             st.length[s] += 1
             self.cache.connection_calls[s] += 1
         before = st.compressed[0]
-        self.cache.post_decode()
+        try:
+            self.cache.post_decode()
+        except Exception as e:
+            # the device counters have already advanced past what the host
+            # tracks: refuse further replays rather than read past the cache
+            self._failed = str(e)
+            raise
+        if st.length[0] + 1 > self.cache.cap_len or st.length[0] - st.compressed[0] + 1 > st.tail_cap:
+            self._failed = "Cache capacity exceeded"   # the next step would append past it
         if st.compressed[0] != before:
             self._reload = True
         return logits

@@ -822,22 +822,46 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     int64_t c0 = 0;
     int32_t t_l = 0, nk_l = 0, nv_l = 0, nb_l = 0;
     int64_t incl = 0;   // blocks of sequences c0 .. c0 + l, all kv-heads
+    // Sequence bb's length, or 0 when its blocks or tail lie past the cache's
+    // capacity (the launch-time host checks cover checked calls; a graph
+    // replay with device lengths has only this one): nothing of such a
+    // sequence is read, and the status word says why.
+    bool over = false;
+    auto usable = [&](int64_t bb, int32_t &nk, int32_t &nv) -> int32_t {
+        const int32_t t = p.seq_len[bb];
+        nk = (!SCORES && p.k.blocks) ? p.k.blocks[bb] : 0;
+        nv = p.v.blocks ? p.v.blocks[bb] : 0;
+        auto fits = [&](const FastSide &sd, int32_t nb, bool present) {
+            if (!present) return true;
+            if (nb < 0 || nb > sd.block_cap) return false;
+            const int64_t rest = static_cast<int64_t>(t) - static_cast<int64_t>(nb) * kBlockTok;
+            return rest <= 0 || (sd.tail != nullptr && rest <= sd.tail_cap);
+        };
+        const bool ok = (SCORES ? t <= p.scores_cap : fits(p.k, nk, true)) && fits(p.v, nv, true);
+        if (!ok) {
+            over = true;
+            nk = nv = 0;
+            return 0;
+        }
+        return t > 0 ? t : 0;
+    };
     auto load_chunk = [&]() {
         const int64_t bb = c0 + l;
-        const bool in = bb < p.batch;
-        const int32_t t = in ? p.seq_len[bb] : 0;
-        t_l = t > 0 ? t : 0;
-        nk_l = (in && !SCORES && p.k.blocks) ? p.k.blocks[bb] : 0;
-        nv_l = (in && p.v.blocks) ? p.v.blocks[bb] : 0;
+        int32_t nk = 0, nv = 0;
+        t_l = (bb < p.batch) ? usable(bb, nk, nv) : 0;
+        nk_l = nk;
+        nv_l = nv;
         nb_l = static_cast<int32_t>((static_cast<int64_t>(t_l) + kBlockTok - 1) / kBlockTok);
         incl = H * wave_incl_scan(nb_l);
     };
     load_chunk();
     int64_t N = lane_get(incl, 63);
     for (int64_t c = 64; c < p.batch; c += 64) {   // sequences past the first 64
-        const int32_t t = (c + l < p.batch) ? p.seq_len[c + l] : 0;
-        N += lane_get(H * wave_incl_scan((static_cast<int64_t>(t > 0 ? t : 0) + kBlockTok - 1) / kBlockTok), 63);
+        int32_t nk = 0, nv = 0;
+        const int32_t t = (c + l < p.batch) ? usable(c + l, nk, nv) : 0;
+        N += lane_get(H * wave_incl_scan((static_cast<int64_t>(t) + kBlockTok - 1) / kBlockTok), 63);
     }
+    if (blockIdx.x == 0 && __ballot(over)) raise_status(p.status, l == 0 ? NSN_ST_CAPACITY : 0);
     if (N == 0) return;
     const int64_t W = gridDim.x;
     int lane = 0;   // (uniform) the lane holding the current sequence

@@ -324,8 +324,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     const int64_t qend = (q0 + kQTile < p.n_q) ? q0 + kQTile : p.n_q;   // chunk tokens this workgroup sees
     const int64_t nt_blk = (ntail + kBlockTok - 1) / kBlockTok;
     const int64_t nblk = nb + nt_blk + (qend + kBlockTok - 1) / kBlockTok;
-    if (nbk != nbv || ntail < 0 || ntail > p.k.tail_cap || ntail > p.v.tail_cap) {
-        if (tid == 0) raise_status(p.status, NSN_ST_NONFINITE_ATTN);   // inconsistent cache (host checks first)
+    if (nbk != nbv || nb < 0 || (nb > 0 && (nb > p.k.block_cap || nb > p.v.block_cap)) || ntail < 0 ||
+        ntail > p.k.tail_cap || ntail > p.v.tail_cap) {
+        if (tid == 0) raise_status(p.status, NSN_ST_CAPACITY);   // inconsistent cache (host checks first)
         return;
     }
 

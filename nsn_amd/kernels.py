@@ -202,6 +202,8 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     _lib.check(rc, entry)
     if check and status is None:
         s = _dev.read_status(st)
+        if s & _lib.ST_CAPACITY:
+            raise IntegrityError("Sequence length past the cache's block / tail capacity")
         if s & _lib.ST_WORKSPACE:
             raise IntegrityError("Decode workspace too small: n_splits below the fast kernel's partial slots")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
@@ -277,8 +279,10 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     _lib.check(rc, "nsn_prefill_attention")
     if check and status is None:
         s = _dev.read_status(st)
+        if s & _lib.ST_CAPACITY:
+            raise IntegrityError("Inconsistent cache: K/V block counts differ or the tail exceeds its capacity")
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_OUTPUT):
-            raise NumericalFailure("Nonfinite prefill output or inconsistent cache")
+            raise NumericalFailure("Nonfinite prefill output")
     return out
 
 

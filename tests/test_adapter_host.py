@@ -120,3 +120,47 @@ def test_check_decode_takes_fp32_queries_on_the_native_arm_only():
     assert adapter.check_decode(_module(), q, _stub_cache(arm="NATIVE"), 0, None, None) == 10
     with pytest.raises(IntegrityError):
         adapter.check_decode(_module(), q, _stub_cache(), 0, None, None)
+
+
+def test_sliding_window_configs_are_refused_before_any_append():
+    """The window lives in the config (Mistral keeps no attribute on the
+    module): a window shorter than the cache capacity is refused at cache
+    construction and in check_decode; Qwen2's unused window is not."""
+    from transformers import MistralConfig, Qwen2Config
+    kw = dict(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+              num_key_value_heads=1, head_dim=128, max_position_embeddings=8192)
+    mistral = MistralConfig(sliding_window=4096, **kw)
+    assert adapter.sliding_window(mistral, 0) == 4096
+    with pytest.raises(IntegrityError, match="sliding-window"):
+        adapter.PackedKVCache(mistral, 1, 8192, device=torch.device("cpu"))
+    # a window at least the capacity never cuts the attention
+    adapter._refuse_window(mistral, 0, 4096)
+    qwen2 = Qwen2Config(**kw)
+    assert adapter.sliding_window(qwen2, 0) is None
+    layered = SimpleNamespace(sliding_window=512, layer_types=["full_attention", "sliding_attention"])
+    assert adapter.sliding_window(layered, 0) is None and adapter.sliding_window(layered, 1) == 512
+    mod = SimpleNamespace(training=False, sliding_window=None, config=mistral, layer_idx=0)
+    with pytest.raises(IntegrityError, match="sliding-window"):
+        adapter.check_decode(mod, torch.zeros(1, 2, 1, 128, dtype=torch.bfloat16),
+                             SimpleNamespace(store=SimpleNamespace(length=[10]), batch=1, heads_q=2, strict=False,
+                                             arm="PACKED_KV_FUSED", max_tokens=8192), 0, None, None)
+
+
+def test_fused_qkv_is_rebuilt_when_the_weights_change():
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    torch.manual_seed(0)
+    m = Qwen2ForCausalLM(Qwen2Config(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=1,
+                                     num_attention_heads=2, num_key_value_heads=1, head_dim=128)).eval()
+    restore = adapter.install(m)
+    a = m.model.layers[0].self_attn
+    w, bias, nq, nk = adapter._fused_qkv(a)
+    assert bias is not None and torch.equal(bias, torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]))
+    assert adapter._fused_qkv(a)[0] is w                          # unchanged weights: the same copy
+    with torch.no_grad():
+        a.k_proj.weight.add_(1.0)                                 # an in-place update
+    w2 = adapter._fused_qkv(a)[0]
+    assert w2 is not w and torch.equal(w2[nq:nq + nk], a.k_proj.weight)
+    m.to(torch.float64)                                           # a cast replaces the parameters
+    assert adapter._fused_qkv(a)[0].dtype == torch.float64
+    restore()
+    assert not hasattr(a, "_nsn_qkv") and not hasattr(a, "_nsn_qkv_key")

@@ -29,13 +29,22 @@ B, P, STEPS = 2, 150, 60
 
 def model(family="llama"):
     """Random-init 2-layer GQA decoder (8 q-heads / 2 kv-heads, d=128, bf16).
-    qwen3 adds per-head RMS norms on q and k before the rotary embedding."""
+    qwen3 adds per-head RMS norms on q and k before the rotary embedding;
+    qwen2 has q, k and v biases (concatenated into the fused QKV GEMM)."""
     torch.manual_seed(0)
     kw = dict(vocab_size=256, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
               num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=1024)
     if family == "qwen3":
         cfg = Qwen3Config(**kw)
         m = Qwen3ForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+    elif family == "qwen2":
+        from transformers import Qwen2Config, Qwen2ForCausalLM
+        cfg = Qwen2Config(**kw)
+        m = Qwen2ForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+        with torch.no_grad():   # non-zero biases, so that a dropped or misplaced bias shows
+            for layer in m.model.layers:
+                for proj in (layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj):
+                    proj.bias.normal_(0.0, 0.5)
     else:
         cfg = LlamaConfig(**kw)
         m = LlamaForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
@@ -66,7 +75,7 @@ def slot_kv_oracle(cache, slot):
     return out
 
 
-@pytest.mark.parametrize("family", ["llama", "qwen3"])
+@pytest.mark.parametrize("family", ["llama", "qwen3", "qwen2"])
 def test_fused_arm_every_layer_and_step_vs_oracle(family):
     m, cfg, ids = model(family)
     cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P)
@@ -111,7 +120,8 @@ def forced_logits(m, cache, ids, tokens):
 
 
 @pytest.mark.parametrize("family,arm", [("llama", "PACKED_KV_FUSED"), ("llama", "PACKED_GROUPED"),
-                                        ("llama", "PACKED_KV_EXACT"), ("qwen3", "PACKED_KV_FUSED")])
+                                        ("llama", "PACKED_KV_EXACT"), ("qwen3", "PACKED_KV_FUSED"),
+                                        ("qwen2", "PACKED_KV_FUSED")])
 def test_arms_agree_with_native(family, arm):
     m, cfg, ids = model(family)
     tokens = torch.randint(0, 256, (B, 40), generator=torch.Generator().manual_seed(2)).to(DEV)
@@ -380,8 +390,8 @@ def test_looped_model_slots_vs_oracle_and_graph():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shared_rows", [True, False])
-def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
+@pytest.mark.parametrize("shared_rows,fused", [(True, False), (False, False), (False, True)])
+def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows, fused):
     """nsn_rope_append against transformers' own apply_rotary_pos_emb (Llama
     rotary, the model dtype's rounding) and a plain fp16 cast of k and v:
     the rotated q and the appended tail rows are bit-identical, at a host
@@ -394,21 +404,25 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
                       max_position_embeddings=8192)
     rot = LlamaRotaryEmbedding(cfg).to(DEV)
     g = torch.Generator(device=DEV).manual_seed(8)
-    q = (torch.randn((b_, 1, hq * 128), generator=g, device=DEV) * 3).to(dtype)
-    k = (torch.randn((b_, 1, hkv * 128), generator=g, device=DEV) * 3).to(dtype)
-    v = torch.randn((b_, 1, hkv * 128), generator=g, device=DEV).to(dtype)
+    if fused:   # slices of one fused QKV projection row, as the adapter passes them
+        qkv = (torch.randn((b_, 1, (hq + 2 * hkv) * 128), generator=g, device=DEV) * 3).to(dtype)
+        q, k, v = qkv[..., :hq * 128], qkv[..., hq * 128:(hq + hkv) * 128], qkv[..., (hq + hkv) * 128:]
+    else:
+        q = (torch.randn((b_, 1, hq * 128), generator=g, device=DEV) * 3).to(dtype)
+        k = (torch.randn((b_, 1, hkv * 128), generator=g, device=DEV) * 3).to(dtype)
+        v = torch.randn((b_, 1, hkv * 128), generator=g, device=DEV).to(dtype)
     pos = torch.tensor([[517]], device=DEV) if shared_rows else torch.tensor([[17], [517], [4000]], device=DEV)
     cos, sin = rot(q, pos)
     cos, sin = cos.contiguous(), sin.contiguous()
-    qr, kr = apply_rotary_pos_emb(q.view(b_, 1, hq, 128).transpose(1, 2), k.view(b_, 1, hkv, 128).transpose(1, 2),
-                                  cos, sin)
+    qr, kr = apply_rotary_pos_emb(q.reshape(b_, 1, hq, 128).transpose(1, 2),
+                                  k.reshape(b_, 1, hkv, 128).transpose(1, 2), cos, sin)
     for device_end in (False, True):
         q_out = torch.empty((b_, hq, 128), dtype=dtype, device=DEV)
         kt = torch.zeros((b_ * hkv, cap, 128), dtype=torch.float16, device=DEV)
         vt = torch.zeros_like(kt)
         st = _dev.new_status(DEV)
         end_t = torch.tensor([5], dtype=torch.int32, device=DEV)
-        rc = lib.nsn_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), hq * 128, hkv * 128, cos.data_ptr(),
+        rc = lib.nsn_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), cos.data_ptr(),
                                  sin.data_ptr(),
                                  0 if shared_rows else 128, b_, hq, hkv, q_out.data_ptr(), kt.data_ptr(), vt.data_ptr(),
                                  cap, end_t.data_ptr() if device_end else None, 4, _dev.dtype_code(dtype),
@@ -416,7 +430,7 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows):
         assert rc == 0 and _dev.read_status(st) == 0
         assert torch.equal(q_out.view(torch.int16), qr[:, :, 0].contiguous().view(torch.int16))
         want_k = kr[:, :, 0].to(torch.float16).reshape(b_ * hkv, 128)
-        want_v = v.view(b_ * hkv, 128).to(torch.float16)
+        want_v = v.reshape(b_ * hkv, 128).to(torch.float16)
         assert torch.equal(kt[:, 4].view(torch.int16), want_k.view(torch.int16))
         assert torch.equal(vt[:, 4].view(torch.int16), want_v.view(torch.int16))
         rest = torch.ones(cap, dtype=torch.bool)

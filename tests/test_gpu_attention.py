@@ -326,3 +326,30 @@ def test_fast_kernel_flags_nonfinite_raw_input():
     vv.tail[0, 1, 3, 7] = float("inf")          # token 64*3 + 3 of sequence 0 (tail)
     with pytest.raises(NumericalFailure, match="raw attention input"):
         kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel="fast")
+
+
+def test_capacity_guard_with_device_lengths():
+    """check=False (a graph replay's mode): a length past the cache's blocks +
+    tail capacity is refused on the device -- nothing of that sequence is
+    read and NSN_ST_CAPACITY is raised -- instead of reading past the tail.
+    The prefill kernel refuses a block count past block_cap the same way."""
+    from nsn_amd import _dev, _lib
+    k, v, qb, kk, vv, seq = make_case(7, 2, 8, 2, [700, 300])
+    assert kk.tail.shape[2] == 64 and int(kk.blocks[1]) == 4          # capacity of sequence 1: 4*64 + 64 tokens
+    bad = torch.tensor([700, 300 + 640], dtype=torch.int32, device=DEV)
+    print("capacity case: decode, seq_len [700, 940] against capacity 320", flush=True)
+    st = _dev.new_status(DEV)
+    kernels.decode_attention(qb.to(DEV), kk, vv, bad, max_seq_len=940, kernel="fast", check=False, status=st)
+    assert _dev.read_status(st) & _lib.ST_CAPACITY
+    with pytest.raises(Exception, match="capacity|Tail exceeds"):
+        kernels.decode_attention(qb.to(DEV), kk, vv, bad, max_seq_len=940, kernel="fast")
+    print("capacity case: prefill, blocks past block_cap", flush=True)
+    kk.blocks[1] = kk.codes.shape[2] + 1
+    vv.blocks[1] = kk.codes.shape[2] + 1
+    ctx_len = torch.tensor([700, 64 * (kk.codes.shape[2] + 1)], dtype=torch.int32, device=DEV)
+    q = torch.zeros((2, 8, 16, 128), dtype=torch.float16, device=DEV)
+    ch = torch.zeros((2, 2, 16, 128), dtype=torch.float16, device=DEV)
+    kk.tail, vv.tail = kk.tail.to(torch.float16), vv.tail.to(torch.float16)
+    st = _dev.new_status(DEV)
+    kernels.prefill_attention(q, kk, vv, ctx_len, ch, ch, check=False, status=st)
+    assert _dev.read_status(st) & _lib.ST_CAPACITY
