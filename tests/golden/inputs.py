@@ -139,3 +139,63 @@ def array_hash(a):
     """experiments/ac08/source/loop_kv_af01_contract.py:20."""
     import hashlib
     return hashlib.sha256(str((a.shape, str(a.dtype))).encode() + a.tobytes()).hexdigest()
+
+
+# The reference's 24 rejection kinds, in its plan order
+# (experiments/ac08/source/loop_kv_vf01_inputs.json "negative_fixtures").
+NEGATIVE_KINDS = (
+    "q_nan", "q_inf", "k_tail_nan", "v_tail_inf", "k_norm_nan", "k_min_nan", "k_scale_inf", "v_norm_nan",
+    "v_min_nan", "v_scale_nan", "v_norm_inf", "v_zero_norm_nan_direction", "q_dtype", "q_shape", "k_codes_dtype",
+    "v_codes_dtype", "v_codes_short", "v_meta_shape", "v_tail_noncontiguous", "kv_length_mismatch",
+    "k_header_position", "v_header_position", "empty_sequence", "score_overflow")
+
+# kind -> (field, value, flat position) for the one-value nonfinite defects
+_NONFINITE = {
+    "q_nan": ("q", np.nan, 0), "q_inf": ("q", np.inf, 0), "k_tail_nan": ("k_tail", np.nan, 0),
+    "v_tail_inf": ("v_tail", np.inf, -1), "k_norm_nan": ("k_meta0", np.nan, 0), "k_min_nan": ("k_meta1", np.nan, 0),
+    "k_scale_inf": ("k_meta2", np.inf, 0), "v_norm_nan": ("v_meta0", np.nan, -1),
+    "v_min_nan": ("v_meta1", np.nan, 0), "v_scale_nan": ("v_meta2", np.nan, 0), "v_norm_inf": ("v_meta0", np.inf, 0),
+}
+
+
+def vf01_negative(kind):
+    """One defect planted in the 64 + 1 token mixed-codes fixture
+    (experiments/ac08/source/loop_kv_vf01_contract.py:98-120).
+
+    Returns (arrays, mutation): ``mutation`` names a defect made after the
+    transfer to the device (a noncontiguous V tail), else None.
+    """
+    a = vf01_fixture(64, 65, "mixed_codes")
+    mutation = None
+    if kind in _NONFINITE:
+        field, value, pos = _NONFINITE[kind]
+        x = a[field]
+        x.reshape(-1)[pos] = _bf16_bits(np.array([value], np.float32))[0] if x.dtype == np.uint16 else value
+    elif kind == "v_zero_norm_nan_direction":       # every norm zero, one direction component NaN
+        a["v_meta0"].fill(0)
+        a["v_meta1"].reshape(-1)[0] = np.nan
+    elif kind == "q_dtype":                          # fp32 values instead of bf16 bit patterns
+        a["q"] = (a["q"].astype(np.uint32) << 16).view(np.float32)
+    elif kind == "q_shape":
+        a["q"] = a["q"][..., :127].copy()
+    elif kind in ("k_codes_dtype", "v_codes_dtype"):
+        a[kind[0] + "_codes"] = a[kind[0] + "_codes"].astype(np.int16)
+    elif kind == "v_codes_short":
+        a["v_codes"] = a["v_codes"][..., :-1].copy()
+    elif kind == "v_meta_shape":
+        a["v_meta1"] = a["v_meta1"][..., :127].copy()
+    elif kind == "v_tail_noncontiguous":
+        mutation = kind
+    elif kind == "kv_length_mismatch":
+        a["v_tail"] = np.concatenate([a["v_tail"], a["v_tail"]], axis=2)
+    elif kind in ("k_header_position", "v_header_position"):
+        a[kind[0] + "_headers"].reshape(-1)[0] = 1
+    elif kind == "empty_sequence":
+        a = {"q": a["q"], "k_tail": a["k_tail"][:, :, :0].copy(), "v_tail": a["v_tail"][:, :, :0].copy()}
+    elif kind == "score_overflow":                   # q . k = 128 * 2**240 overflows fp32
+        a = vf01_fixture(0, 17, "tail_only")
+        for name in ("q", "k_tail"):
+            a[name] = np.full(a[name].shape, 0x7B80, np.uint16)      # bf16 2**120
+    else:
+        raise ValueError("unknown negative fixture " + kind)
+    return a, mutation
