@@ -140,10 +140,14 @@ int nsn_restore_blocks(const uint8_t *codes, int codes_are_unpacked, const uint1
  * experiments/ac08/source/loop_kv_vf01_kernel.py:28-34).
  *   codes/norms/mins/scales: [n_outer, in_outer_blocks, ...] as nsn_restore_blocks;
  *   factors: [n_outer, in_outer_blocks, 64] fp32.
+ *   status (nullable): NSN_ST_NONFINITE_ATTN_INPUT is raised when a block's
+ *   norms, mins or scales hold a NaN/Inf (the finite check of the raw
+ *   metadata, loop_kv_vf01_checks.py:55-63, for callers that read factors).
  */
 int nsn_block_factors(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins,
                       const uint16_t *scales, int64_t n_outer, int64_t n_blocks,
-                      int64_t in_outer_blocks, int bits, float *factors, nsn_stream_t stream);
+                      int64_t in_outer_blocks, int bits, float *factors, int32_t *status,
+                      nsn_stream_t stream);
 
 /* K/V sources of the decode attention. */
 enum {

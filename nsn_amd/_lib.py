@@ -71,7 +71,7 @@ SIGNATURES = {
     "nsn_version": (ctypes.c_char_p, []),
     "nsn_abi_sizeof": (I64, [I32]),
     "nsn_encode_blocks": (I32, [P, I32, I64, I64, I64, I64, I32, I32, I32, P, P, P, P, P, P, I64, I64, I64, P, P, P]),
-    "nsn_block_factors": (I32, [P, P, P, P, I64, I64, I64, I32, P, P]),
+    "nsn_block_factors": (I32, [P, P, P, P, I64, I64, I64, I32, P, P, P]),
     "nsn_pack_codes": (I32, [P, I64, I32, P, P, P]),
     "nsn_unpack_codes": (I32, [P, I64, I32, P, P]),
     "nsn_restore_blocks": (I32, [P, I32, P, P, P, I64, I64, I64, I32, P, I32, I64, P, I32, I64, I64, P, P]),

@@ -683,18 +683,22 @@ __global__ __launch_bounds__(256) void restore_kernel(RestoreParams p) {
 template <int BITS>
 __global__ __launch_bounds__(256) void factor_kernel(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins,
                                                      const uint16_t *scales, int64_t n_blocks, int64_t in_outer_blocks,
-                                                     float *factors) {
+                                                     float *factors, int32_t *status) {
     __shared__ float m_s[kDim], s_s[kDim], n_s[kBlockTok];
     __shared__ uint32_t codes_s[kBlockTok * kDim / 4];
     const int tid = threadIdx.x;
     const int64_t o = blockIdx.x / n_blocks, i = blockIdx.x - o * n_blocks;
     const int64_t ib = o * in_outer_blocks + i;
+    bool bad = false;   // nonfinite metadata: the block's raw inputs fail the finite check
     if (tid < kDim) {
         m_s[tid] = f16_bits_to_f32(mins[ib * kDim + tid]);
         s_s[tid] = f16_bits_to_f32(scales[ib * kDim + tid]);
+        bad = !finite(m_s[tid]) || !finite(s_s[tid]);
     } else if (tid < kDim + kBlockTok) {
         n_s[tid - kDim] = f16_bits_to_f32(norms[ib * kBlockTok + tid - kDim]);
+        bad = !finite(n_s[tid - kDim]);
     }
+    if (bad && status) raise_status(status, NSN_ST_NONFINITE_ATTN_INPUT);
     {
         const uint32_t *src = reinterpret_cast<const uint32_t *>(codes + ib * packed_block_bytes(BITS)) + tid * BITS;
         uint32_t w[BITS];
@@ -894,16 +898,22 @@ int nsn_restore_blocks(const uint8_t *codes, int codes_are_unpacked, const uint1
 
 int nsn_block_factors(const uint8_t *codes, const uint16_t *norms, const uint16_t *mins, const uint16_t *scales,
                       int64_t n_outer, int64_t n_blocks, int64_t in_outer_blocks, int bits, float *factors,
-                      nsn_stream_t stream) {
+                      int32_t *status, nsn_stream_t stream) {
     if (n_outer < 0 || n_blocks < 0 || !bits_ok(bits) || in_outer_blocks < n_blocks) return NSN_EINVAL;
     if (n_outer == 0 || n_blocks == 0) return NSN_OK;
     if (!codes || !norms || !mins || !scales || !factors || !aligned(codes, 16)) return NSN_EINVAL;
     if (n_outer * n_blocks > 0x7fffffff) return NSN_EINVAL;
     const dim3 grid(static_cast<unsigned>(n_outer * n_blocks));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (bits == 3) hipLaunchKernelGGL(factor_kernel<3>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
-    else if (bits == 4) hipLaunchKernelGGL(factor_kernel<4>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
-    else hipLaunchKernelGGL(factor_kernel<5>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks, factors);
+    if (bits == 3)
+        hipLaunchKernelGGL(factor_kernel<3>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks,
+                           factors, status);
+    else if (bits == 4)
+        hipLaunchKernelGGL(factor_kernel<4>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks,
+                           factors, status);
+    else
+        hipLaunchKernelGGL(factor_kernel<5>, grid, dim3(256), 0, s, codes, norms, mins, scales, n_blocks, in_outer_blocks,
+                           factors, status);
     return launch_status();
 }
 

@@ -23,9 +23,11 @@
 // (nsn_block_factors).  They are constant once a block is encoded, so they are
 // read, not recomputed.  Reconstruction equals nsn_decode's up to rounding
 // (loop_kv_pilot.py:216-225); results match the fp64 oracle within the stated
-// tolerance, not bit for bit.  Tokens past the packed prefix (the fp16 tail,
-// or a fully dense fp16 K/V for the fp16 baseline) take the same MFMA path
-// with the fp16 values themselves as operands.
+// tolerance, not bit for bit.  Tokens past the packed prefix (the tail, or a
+// fully dense K/V for the fp16 baseline) take the same MFMA path with the
+// stored values themselves as operands: fp16 tails on the fp16 product, bf16
+// tails on v_mfma_f32_16x16x32_bf16 with the query and the softmax weights as
+// bf16 hi + lo rows (~16 bits), so bf16 values outside the fp16 range compute.
 //
 // Reference routes replaced: experiments/ac08/source/loop_kv_vf01_kernel.py:56-139
 // (fused readout), experiments/nb06/source/loop_kv_nb06_kernel.py:54-154 (GQA),
@@ -42,6 +44,7 @@ using unpack::Layout;
 using unpack::kunpack;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -55,6 +58,16 @@ constexpr float kPScale = 16384.f;   // softmax weights enter the PV product as 
 
 __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+// The same product on bf16 operands (dense bf16 tail tokens).
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                   0);
+}
+template <bool BF>
+__device__ __forceinline__ f32x4 mfma_t(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    if constexpr (BF) return mfma_bf16(a, b, c);
+    else return mfma(a, b, c);
 }
 // v_perm_b32: byte i of the result = byte sel[i] of {hi:lo} (0..3 = lo, 4..7 = hi, 0x0c = 0).
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -75,6 +88,22 @@ __device__ __forceinline__ float f16hi(uint32_t p) { return static_cast<float>(_
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
     hi = pkrtz(a, b);
     lo = pkrtz(a - lo_f32(hi), b - hi_f32(hi));
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_rn(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+// fp32 pair -> bf16 hi (toward zero) + bf16 lo = rn(x - hi): ~16 significant bits.
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const uint32_t ua = __builtin_bit_cast(uint32_t, a) & 0xFFFF0000u, ub = __builtin_bit_cast(uint32_t, b) & 0xFFFF0000u;
+    hi = (ua >> 16) | ub;
+    lo = bf16_rn(a - __builtin_bit_cast(float, ua)) | (bf16_rn(b - __builtin_bit_cast(float, ub)) << 16);
+}
+// An fp16 hi + lo pair of element pairs -> the bf16 hi + lo pair of the same values.
+__device__ __forceinline__ void f16_to_bf16_pair(uint32_t h, uint32_t l, uint32_t &bh, uint32_t &bl) {
+    split2_bf16(f16lo(h) + f16lo(l), f16hi(h) + f16hi(l), bh, bl);
 }
 
 // The 16-bit half of dword `S[a/2]` holding element a, paired with element b
@@ -136,7 +165,7 @@ struct FastSide {
     const float *factors;
     const int32_t *blocks;
     int64_t block_cap;
-    const uint16_t *tail;   // fp16
+    const uint16_t *tail;   // fp16, or bf16 in the TBF kernel variants
     int64_t tail_cap;
 };
 
@@ -234,6 +263,15 @@ __device__ __forceinline__ int64_t lane_get(int64_t x, int lane) {
 __device__ __forceinline__ uint32_t f16x8_nonfinite(const uint4 &w) {
     const uint32_t m = 0x7C007C00u, one = 0x04000400u, top = 0x80008000u;
     return (((w.x & m) + one) | ((w.y & m) + one) | ((w.z & m) + one) | ((w.w & m) + one)) & top;
+}
+__device__ __forceinline__ uint32_t bf16x8_nonfinite(const uint4 &w) {
+    const uint32_t m = 0x7F807F80u, one = 0x00800080u, top = 0x80008000u;
+    return (((w.x & m) + one) | ((w.y & m) + one) | ((w.z & m) + one) | ((w.w & m) + one)) & top;
+}
+template <bool BF>
+__device__ __forceinline__ uint32_t x8_nonfinite(const uint4 &w) {
+    if constexpr (BF) return bf16x8_nonfinite(w);
+    else return f16x8_nonfinite(w);
 }
 
 // LDS hand-off inside the single wave of a workgroup: the wave's LDS accesses
@@ -350,7 +388,7 @@ __device__ __forceinline__ void dma_block(const FastParams &p, int64_t ibk, int6
 // One stream segment: tokens [t_begin, t_end) of (sequence b, kv-head kvh),
 // written as partial slot `slot` of each of the kv-head's G query heads.
 // nbk_b / nbv_b: the sequence's packed K / V block counts (0 without blocks).
-template <int BITS, int QDT, bool SCORES, int GRP>
+template <int BITS, int QDT, bool SCORES, int GRP, bool TBF>
 __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP> &sh, int b, int kvh,
                                         int64_t t_begin, int64_t t_end, int64_t nbk_b, int64_t nbv_b, int slot,
                                         int count) {
@@ -468,7 +506,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     // top of the next block.  No prefetched data lives in
     // registers, so the compiler never has to wait for it mid-block, and no
     // DMA is left in flight when the pipelined loop ends.  Blocks past t_fast
-    // (fp16 tail, dense K or V) fetch their own data first.
+    // (tail, dense K or V) fetch their own data first.
 
     auto block = [&](auto fast, auto stage_c, const int64_t t0, const int64_t t_next) {
         constexpr bool FAST = decltype(fast)::value;
@@ -562,12 +600,28 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                     for (int j = 0; j < NJ; ++j)
                         s[j][nt] = ((C[nt][2 * j] + C[nt][2 * j + 1]) + qm[j]) * (fk[nt] * c1s[j]);
             } else {
-                // dense fp16 keys (tokens t0 - 64*nbk + tt of the tail buffer): the A rows are the
-                // query itself (q * 2^sigma, hi + lo), channels in the same element order
+                // dense keys (tokens t0 - 64*nbk + tt of the tail buffer): the A rows are the
+                // query itself (q * 2^sigma, hi + lo; bf16 hi + lo for bf16 keys), channels in
+                // the same element order
+                if constexpr (TBF) {
 #pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    put_frag(j, u32x4{quh[j][0], quh[j][1], quh[j][2], quh[j][3]},
-                             u32x4{qul[j][0], qul[j][1], qul[j][2], qul[j][3]});
+                    for (int j = 0; j < NJ; ++j) {
+                        u32x4 hi, lo;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            uint32_t bh, bl;
+                            f16_to_bf16_pair(quh[j][i], qul[j][i], bh, bl);
+                            hi[i] = bh;
+                            lo[i] = bl;
+                        }
+                        put_frag(j, hi, lo);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        put_frag(j, u32x4{quh[j][0], quh[j][1], quh[j][2], quh[j][3]},
+                                 u32x4{qul[j][0], qul[j][1], qul[j][2], qul[j][3]});
+                }
                 lds_sync();
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk) af[kk] = get_frag(kk);
@@ -582,12 +636,12 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 #pragma unroll
                     for (int kk = 0; kk < 4; ++kk) {
                         const uint4 v = ld16(src + 8 * kk);
-                        bad_in |= f16x8_nonfinite(v) != 0;
+                        bad_in |= x8_nonfinite<TBF>(v) != 0;
                         const uint32_t X[4] = {v.x, v.y, v.z, v.w};
                         u32x4 Bd;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) Bd[i] = half_pair(X, LY::chE[2 * i], LY::chE[2 * i + 1]);
-                        C[nt] = mfma(af[kk], Bd, C[nt]);
+                        C[nt] = mfma_t<TBF>(af[kk], Bd, C[nt]);
                     }
                 }
 #pragma unroll
@@ -653,7 +707,8 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 uint32_t hi, lo;
-                split2(pp[2 * k], pp[2 * k + 1], hi, lo);
+                if (TBF && !vpacked) split2_bf16(pp[2 * k], pp[2 * k + 1], hi, lo);   // dense bf16 V
+                else split2(pp[2 * k], pp[2 * k + 1], hi, lo);
                 phi[32 * k + row] = static_cast<uint16_t>(hi);
                 phi[32 * k + 16 + row] = static_cast<uint16_t>(hi >> 16);
                 plo[32 * k + row] = static_cast<uint16_t>(lo);
@@ -706,7 +761,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                 const uint4 pv = *reinterpret_cast<const uint4 *>(pb_rd + pb_step * (8 * grp + 4 * kk2));
                 const u32x4 pa = {pv.x, pv.y, pv.z, pv.w};
                 uint32_t D[8][4];
-                // dense fp16 V: tokens 16*grp + 8*kk2 + e, channels 8*row .. 8*row+7.
+                // dense V: tokens 16*grp + 8*kk2 + e, channels 8*row .. 8*row+7.
                 // Tokens past `valid` read the last valid token (in bounds); their
                 // weights are zero.
                 const uint16_t *vrow = p.v.tail + (seqrow * p.v.tail_cap + t0 - nbv * kBlockTok) * kDim + 8 * row;
@@ -715,7 +770,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                     const int ta = 16 * grp + 8 * kk2 + 2 * k, tb = ta + 1;
                     const uint4 xa4 = ld16(vrow + (ta < valid ? ta : valid - 1) * kDim);
                     const uint4 xb4 = ld16(vrow + (tb < valid ? tb : valid - 1) * kDim);
-                    bad_in |= (f16x8_nonfinite(xa4) | f16x8_nonfinite(xb4)) != 0;
+                    bad_in |= (x8_nonfinite<TBF>(xa4) | x8_nonfinite<TBF>(xb4)) != 0;
                     const uint32_t xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
                     const uint32_t xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
 #pragma unroll
@@ -723,7 +778,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
                         D[m][k] = perm(xb[m >> 1], xa[m >> 1], (m & 1) ? 0x07060302u : 0x05040100u);
                 }
 #pragma unroll
-                for (int m = 0; m < 8; ++m) O[m] = mfma(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
+                for (int m = 0; m < 8; ++m) O[m] = mfma_t<TBF>(pa, u32x4{D[m][0], D[m][1], D[m][2], D[m][3]}, O[m]);
             }
         }
         // ------------------------------------------------------------ epilogue
@@ -801,7 +856,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
 // 64-token blocks of all streams are laid end to end and cut into equal
 // ranges ("stream-K"); a range that crosses a stream boundary yields one
 // partial per stream, wave w's for stream s in slot w - first_wave(s).
-template <int BITS, int QDT, bool SCORES, int GRP>
+template <int BITS, int QDT, bool SCORES, int GRP, bool TBF>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fast_kernel(FastParams p) {
     using S = LdsShape<BITS, GRP>;
     __shared__ u32x4 s_afrag[S::ROWS * 16 + 1];
@@ -922,7 +977,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int64_t i0 = blk(cw(k) * U / ctot), i1 = blk(cw(k + 1) * U / ctot);
         const int64_t T = at(t_l);
         if (n <= p.n_splits) {
-            segment<BITS, QDT, SCORES, GRP>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
+            segment<BITS, QDT, SCORES, GRP, TBF>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
                                             at(nk_l), at(nv_l), static_cast<int>(k), static_cast<int>(n));
         } else {
             raise_status(p.status, NSN_ST_WORKSPACE);   // workspace too small for this layout
@@ -962,7 +1017,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int slot = static_cast<int>(blockIdx.x - start_s / P);
         const int count = static_cast<int>((start_s + nb - 1) / P - start_s / P + 1);
         if (slot < p.n_splits && count <= p.n_splits) {
-            segment<BITS, QDT, SCORES, GRP>(p, sh, static_cast<int>(c0 + lane), kvh, i0 * kBlockTok,
+            segment<BITS, QDT, SCORES, GRP, TBF>(p, sh, static_cast<int>(c0 + lane), kvh, i0 * kBlockTok,
                                             (i1 * kBlockTok < T) ? i1 * kBlockTok : T, at(nk_l), at(nv_l), slot,
                                             count);
         } else {
@@ -1002,10 +1057,17 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
         if (s.mins && (reinterpret_cast<uintptr_t>(s.mins) & 15u)) return false;
         if (s.scales && (reinterpret_cast<uintptr_t>(s.scales) & 15u)) return false;
         if (s.factors && (reinterpret_cast<uintptr_t>(s.factors) & 15u)) return false;
-        if (s.tail && (s.tail_dtype != NSN_DTYPE_F16 || (reinterpret_cast<uintptr_t>(s.tail) & 15u))) return false;
+        if (s.tail && ((s.tail_dtype != NSN_DTYPE_F16 && s.tail_dtype != NSN_DTYPE_BF16) ||
+                       (reinterpret_cast<uintptr_t>(s.tail) & 15u)))
+            return false;
         return true;
     };
     if (!side_ok(a->v) || (!scores && !side_ok(a->k))) return NSN_EINVAL;
+    // one tail dtype per launch (a kernel variant each): both sides' tails, when present, agree
+    const bool vtail_bf = a->v.tail && a->v.tail_dtype == NSN_DTYPE_BF16;
+    const bool ktail_bf = !scores && a->k.tail && a->k.tail_dtype == NSN_DTYPE_BF16;
+    if (!scores && a->k.tail && a->v.tail && ktail_bf != vtail_bf) return NSN_EINVAL;
+    const bool tbf = vtail_bf || ktail_bf;
     if (a->q && (reinterpret_cast<uintptr_t>(a->q) & 1u)) return NSN_EINVAL;
     if (a->n_splits < 2 || a->max_seq_len <= 0) return NSN_EINVAL;
     FastParams p{};
@@ -1044,7 +1106,13 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     p.weighted = per_cu == 8;
     const dim3 grid(static_cast<unsigned>(per_cu * (cus[dev] > 0 ? cus[dev] : 256)));
     const bool bf = a->q_dtype == NSN_DTYPE_BF16;
-#define NSN_FAST_LAUNCH1(B_, Q_, S_, G_) hipLaunchKernelGGL((attn_fast_kernel<B_, Q_, S_, G_>), grid, dim3(64), 0, st, p)
+#define NSN_FAST_LAUNCH2(B_, Q_, S_, G_, T_) \
+    hipLaunchKernelGGL((attn_fast_kernel<B_, Q_, S_, G_, T_>), grid, dim3(64), 0, st, p)
+#define NSN_FAST_LAUNCH1(B_, Q_, S_, G_)                              \
+    do {                                                              \
+        if (tbf) NSN_FAST_LAUNCH2(B_, Q_, S_, G_, true);              \
+        else NSN_FAST_LAUNCH2(B_, Q_, S_, G_, false);                 \
+    } while (0)
 #define NSN_FAST_LAUNCH(B_, Q_, S_)                                   \
     do {                                                              \
         if (G <= 4) NSN_FAST_LAUNCH1(B_, Q_, S_, 4);                  \
@@ -1059,6 +1127,7 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     }
 #undef NSN_FAST_LAUNCH
 #undef NSN_FAST_LAUNCH1
+#undef NSN_FAST_LAUNCH2
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }
 

@@ -134,7 +134,6 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     if kernel == "fast":
         for side in ((v,) if scores is not None else (k, v)):
             require(side.codes is None or side.factor is not None, "Fast kernel needs decode factors")
-            require(side.tail is None or side.tail.dtype == torch.float16, "Fast kernel reads fp16 tails")
         require(v.bits in (3, 5), "Fast kernel supports 3- and 5-bit codes")
     if scores is None:
         require(k is not None, "K cache required")
@@ -310,19 +309,23 @@ def _validate_lengths(seq_len, k, v, scores, max_seq_len):
 
 # --------------------------------------------------- reference (b == 1) surface
 
-def block_factors(codes, norm, mn, sc, bits):
-    """Decode factors n/|m+s*q| of packed blocks codes [rows, n, nbytes] -> fp32 [rows, n, 64]."""
+def block_factors(codes, norm, mn, sc, bits, status=None):
+    """Decode factors n/|m+s*q| of packed blocks codes [rows, n, nbytes] -> fp32 [rows, n, 64].
+    ``status`` (int32 device word) receives NSN_ST_NONFINITE_ATTN_INPUT for nonfinite metadata."""
     rows, n, _ = codes.shape
     out = torch.empty((rows, n, BLOCK), dtype=torch.float32, device=codes.device)
     norm, mn, sc = (t.contiguous() for t in (norm, mn, sc))
     rc = _lib.lib().nsn_block_factors(codes.contiguous().data_ptr(), norm.data_ptr(), mn.data_ptr(), sc.data_ptr(),
-                                      rows, n, n, bits, out.data_ptr(), _dev.stream())
+                                      rows, n, n, bits, out.data_ptr(),
+                                      None if status is None else status.data_ptr(), _dev.stream())
     _lib.check(rc, "nsn_block_factors")
     return out
 
 
-def _group_side(g, tail, bits=None, factors=False):
-    """Reference group dict (+ tail [1,H,L,128]) -> PackedKV for batch 1."""
+def _group_side(g, tail, bits=None, factors=False, status=None):
+    """Reference group dict (+ tail [1,H,L,128]) -> PackedKV for batch 1.  With
+    ``factors`` the decode factors are computed (and the metadata checked into
+    ``status``)."""
     dev = tail.device
     if g is None:
         return PackedKV(None, None, None, None, None, None, tail.contiguous(), bits or 3)
@@ -331,7 +334,7 @@ def _group_side(g, tail, bits=None, factors=False):
     b = (nbytes * 8) // (BLOCK * DIM)
     f = None
     if factors:
-        f = block_factors(codes.reshape(b_ * h, n, nbytes), *g["metas"], b).reshape(b_, h, n, BLOCK)
+        f = block_factors(codes.reshape(b_ * h, n, nbytes), *g["metas"], b, status=status).reshape(b_, h, n, BLOCK)
     return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2], f,
                     torch.full((1,), n, dtype=torch.int32, device=dev), tail.contiguous(), b)
 
@@ -423,7 +426,7 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
     Hq = q.shape[1]
     T = _length(g, kt)
     fast = kernel == "fast"
-    ks, vs = _group_side(g, kt, factors=fast), _group_side(vg, vt, factors=fast)
+    ks, vs = _fast_sides(((g, kt), (vg, vt)), fast, status, q.device)
     seq = torch.full((1,), T, dtype=torch.int32, device=q.device)
     out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
                                 kv_round_dtype=kt.dtype, status=status)
@@ -434,6 +437,19 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
         G = Hq // kt.shape[1]
         score = (torch.einsum("hd,htd->ht", q.reshape(Hq, DIM).float(), kk[0].repeat_interleave(G, 0)) * SCALE)[None]
     return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM), score, vtr
+
+
+def _fast_sides(groups, fast, status, device):
+    """PackedKV sides of (group, tail) pairs; for the fast kernel with their
+    decode factors, whose computation also checks the raw block metadata:
+    nonfinite metadata raises NumericalFailure, or with ``status`` given sets
+    NSN_ST_NONFINITE_ATTN_INPUT there."""
+    st = (status if status is not None else _dev.new_status(device)) if fast else None
+    sides = [_group_side(g, t, factors=fast, status=st) for g, t in groups]
+    if fast and status is None and any(g is not None for g, _ in groups) \
+            and _dev.read_status(st) & _lib.ST_NONFINITE_ATTN_INPUT:
+        raise NumericalFailure("Nonfinite raw attention input (block metadata)")
+    return sides
 
 
 def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
@@ -448,9 +464,9 @@ def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
     vs = PackedKV(None, None, None, None, None, None, v.contiguous(), 3)
     seq = torch.full((1,), T, dtype=torch.int32, device=v.device)
     if full:
-        out, ctx = decode_attention(q.reshape(1, Hq, DIM), _group_side(g, tail, factors=kernel == "fast"), vs, seq,
-                                    max_seq_len=T,
-                                    kernel=kernel, kv_round_dtype=v.dtype)
+        ks, = _fast_sides(((g, tail),), kernel == "fast", None, v.device)
+        out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
+                                    kv_round_dtype=v.dtype)
     else:
         require(score is not None and tuple(score.shape) == (1, Hq, T), "Score shape/type")
         out, ctx = decode_attention(q.reshape(1, Hq, DIM), None, vs, seq, max_seq_len=T, scores=score.contiguous(),
@@ -463,12 +479,14 @@ def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
 FUSED_VALIDATION = True
 
 
-def pipeline(arm, data, trace=False):
+def pipeline(arm, data, trace=False, kernel="reference"):
     """Checked route selection (loop_kv_vf01_kernel.py:141-158, loop_kv_nb06_kernel.py:175-191).
 
     Arms: 'V_FUSED' / 'GQA_FUSED' (fused), 'TILE_MATERIALIZE' (bridge: V
     restored to HBM then attention), 'RF01_MATERIALIZE' (V from restore_group
-    + cat).  Stages recorded in LAST_STAGE as the reference does.
+    + cat).  Stages recorded in LAST_STAGE as the reference does.  ``kernel``
+    picks the attention kernel: 'reference' (exact order, restored values
+    rounded to the tail dtype) or 'fast' (MFMA, within the stated tolerance).
     """
     global LAST_STAGE
     g, kt, q, vg, vt = data
@@ -480,7 +498,7 @@ def pipeline(arm, data, trace=False):
         # still fails at the 'input_finite' stage
         LAST_STAGE = "attention"
         st = _dev.new_status(q.device)
-        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace, status=st)
+        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace, status=st, kernel=kernel)
         s = _dev.read_status(st)
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             LAST_STAGE = "input_finite"
@@ -496,7 +514,7 @@ def pipeline(arm, data, trace=False):
     finite(g, kt, q, vg, vt)
     if arm in ("V_FUSED", "GQA_FUSED"):
         LAST_STAGE = "attention"
-        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace)
+        out, ctx, score, v = launch(g, kt, q, vg, vt, trace=trace, kernel=kernel)
     elif arm in ("TILE_MATERIALIZE", "RF01_MATERIALIZE"):
         LAST_STAGE = "restore"
         if arm == "TILE_MATERIALIZE":
@@ -508,7 +526,7 @@ def pipeline(arm, data, trace=False):
         if not bool(torch.isfinite(v).all()):
             raise NumericalFailure("Nonfinite V")
         LAST_STAGE = "attention"
-        out, ctx = af_launch(g, kt, q, v, full=True)
+        out, ctx = af_launch(g, kt, q, v, full=True, kernel=kernel)
         score = None
     else:
         raise IntegrityError("Unknown VF01 arm")

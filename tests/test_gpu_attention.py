@@ -26,9 +26,10 @@ def within(got, ref, atol=ATOL, rtol=RTOL):
     return ok, float(err.max())
 
 
-def oracle_restore(x16, length, bits, round_dtype):
+def oracle_restore(x16, length, bits, round_dtype, tail_dtype="float16"):
     """Oracle view of one sequence: x16 [H, T, 128] fp16 -> fp32 [H, length, 128]
-    as the kernel sees it (packed prefix restored + rounded, tail as stored)."""
+    as the kernel sees it (packed prefix restored + rounded, tail as stored in
+    ``tail_dtype``)."""
     H = x16.shape[0]
     C = (length // 64) * 64
     parts = []
@@ -43,11 +44,14 @@ def oracle_restore(x16, length, bits, round_dtype):
             bitsr = O.cast_bits(y, round_dtype)
             parts.append(O.from_bf16_bits(bitsr) if round_dtype == "bfloat16" else O.from_f16_bits(bitsr))
     if length > C:
-        parts.append(x16[:, C:length].astype(np.float32))
+        t = x16[:, C:length].astype(np.float32)
+        if tail_dtype == "bfloat16":
+            t = O.from_bf16_bits(O.cast_bits(t, "bfloat16"))
+        parts.append(t)
     return np.concatenate(parts, axis=1)
 
 
-def make_case(seed, B, Hq, Hkv, lengths, bits=3, gen="kv"):
+def make_case(seed, B, Hq, Hkv, lengths, bits=3, gen="kv", tail_dtype=None):
     rng = np.random.default_rng(seed)
     T = max(lengths)
     if gen == "kv":
@@ -60,18 +64,18 @@ def make_case(seed, B, Hq, Hkv, lengths, bits=3, gen="kv"):
         v = synthetic.heavy_tailed_tokens(rng, (B, Hkv), T)
     q = rng.standard_normal((B, Hq, 128)).astype(np.float32)
     qb = torch.from_numpy(q).to(torch.bfloat16)
-    kk, seq = cache.pack_sequences(torch.from_numpy(k).to(DEV), lengths, bits=bits)
-    vv, _ = cache.pack_sequences(torch.from_numpy(v).to(DEV), lengths, bits=bits)
+    kk, seq = cache.pack_sequences(torch.from_numpy(k).to(DEV), lengths, bits=bits, tail_dtype=tail_dtype)
+    vv, _ = cache.pack_sequences(torch.from_numpy(v).to(DEV), lengths, bits=bits, tail_dtype=tail_dtype)
     return k, v, qb, kk, vv, seq
 
 
-def oracle_ctx(k, v, qb, lengths, bits, round_dtype="float16"):
+def oracle_ctx(k, v, qb, lengths, bits, round_dtype="float16", tail_dtype="float16"):
     B, Hq = qb.shape[:2]
     out = np.zeros((B, Hq, 128))
     q = qb.float().numpy()
     for b, L in enumerate(lengths):
-        kr = oracle_restore(k[b], L, bits, round_dtype)
-        vr = oracle_restore(v[b], L, bits, round_dtype)
+        kr = oracle_restore(k[b], L, bits, round_dtype, tail_dtype)
+        vr = oracle_restore(v[b], L, bits, round_dtype, tail_dtype)
         c, _ = O.decode_attention64(q[b:b + 1], kr[None], vr[None])
         out[b] = c[0]
     return out
@@ -162,8 +166,9 @@ def _fixture_data(f):
     return a, (g, bf(a["k_tail"]), bf(a["q"]), vg, bf(a["v_tail"]))
 
 
-def _fixture_oracle(a, f):
-    """fp64 attention over the oracle-restored (bf16-rounded) K/V of a VF01 fixture."""
+def _fixture_oracle(a, f, round_dtype="bfloat16"):
+    """fp64 attention over the oracle-restored K/V of a VF01 fixture (packed
+    tokens rounded to bf16, or kept in fp32 with round_dtype='float32')."""
     c, T = f["compressed"], f["length"]
     out = []
     for side in ("k", "v"):
@@ -174,7 +179,10 @@ def _fixture_oracle(a, f):
             n16 = a[side + "_meta0"].view(np.uint16).reshape(2, n, 64, 1)
             m16 = a[side + "_meta1"].view(np.uint16).reshape(2, n, 1, 128)
             s16 = a[side + "_meta2"].view(np.uint16).reshape(2, n, 1, 128)
-            y = O.from_bf16_bits(O.nsn_decode(q, n16, m16, s16, "bfloat16")).reshape(2, c, 128)
+            if round_dtype == "float32":
+                y = O.nsn_decode_f32(q, n16, m16, s16).reshape(2, c, 128)
+            else:
+                y = O.from_bf16_bits(O.nsn_decode(q, n16, m16, s16, "bfloat16")).reshape(2, c, 128)
             tail = np.concatenate([y, tail], axis=1)
         out.append(tail)
     q = O.from_bf16_bits(a["q"]).reshape(1, 2, 128)
@@ -353,3 +361,58 @@ def test_capacity_guard_with_device_lengths():
     st = _dev.new_status(DEV)
     kernels.prefill_attention(q, kk, vv, ctx_len, ch, ch, check=False, status=st)
     assert _dev.read_status(st) & _lib.ST_CAPACITY
+
+
+@pytest.mark.parametrize("Hq,Hkv,bits", [(8, 2, 3), (32, 4, 3), (8, 2, 5), (16, 8, 5)])
+def test_fast_bf16_tails_vs_oracle(Hq, Hkv, bits):
+    """bf16 tails (the reference's dtype, loop_kv_qk01_kernel.py:66-69) on the
+    fast kernel's bf16 MFMA path; packed tokens keep fp32 reconstructions."""
+    lengths = [1000, 333, 320, 70]
+    k, v, qb, kk, vv, seq = make_case(21, 4, Hq, Hkv, lengths, bits=bits, tail_dtype=torch.bfloat16)
+    assert kk.tail.dtype == torch.bfloat16
+    _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, kernel="fast")
+    ref = oracle_ctx(k, v, qb, lengths, bits, "float32", "bfloat16")
+    ok, err = within(ctx.cpu().numpy(), ref)
+    assert ok, err
+
+
+def test_fast_bf16_dense_beyond_fp16_range():
+    """A dense bf16 K/V (no packed blocks) holding values past fp16's range
+    (|x| up to 3e6) computes on the bf16 path instead of overflowing."""
+    rng = np.random.default_rng(22)
+    B, Hq, Hkv, T = 2, 8, 2, 300
+    k = rng.standard_normal((B, Hkv, T, 128)).astype(np.float32) * 0.05
+    v = rng.standard_normal((B, Hkv, T, 128)).astype(np.float32)
+    k[:, :, 17] *= 1e3          # large keys: scores of order 1e2
+    v[:, :, 5::7] *= 3e6        # values beyond 65504
+    kb = O.from_bf16_bits(O.cast_bits(k, "bfloat16"))
+    vb = O.from_bf16_bits(O.cast_bits(v, "bfloat16"))
+    qb = torch.from_numpy(rng.standard_normal((B, Hq, 128)).astype(np.float32)).to(torch.bfloat16)
+    kd = kernels.PackedKV(None, None, None, None, None, None, torch.from_numpy(kb).to(torch.bfloat16).to(DEV), 3)
+    vd = kernels.PackedKV(None, None, None, None, None, None, torch.from_numpy(vb).to(torch.bfloat16).to(DEV), 3)
+    seq = torch.tensor([T, 251], dtype=torch.int32, device=DEV)
+    _, ctx = kernels.decode_attention(qb.to(DEV), kd, vd, seq, kernel="fast")
+    ref = np.zeros((B, Hq, 128))
+    for b, L in enumerate([T, 251]):
+        c, _ = O.decode_attention64(qb.float().numpy()[b:b + 1], kb[b:b + 1, :, :L], vb[b:b + 1, :, :L])
+        ref[b] = c[0]
+    scale = np.abs(ref).max(axis=-1, keepdims=True)     # (errors relative to each row's magnitude)
+    ok, err = within(ctx.cpu().numpy() / scale, ref / scale)
+    assert ok, err
+
+
+@pytest.mark.parametrize("arm", ["V_FUSED", "TILE_MATERIALIZE", "RF01_MATERIALIZE"])
+def test_vf01_normal_fixtures_on_the_fast_kernel(arm):
+    """The 16 VF01 fixtures (bf16 tails and queries, the reference's dtypes)
+    through every arm on the fast kernel, against the fp64 oracle over fp32
+    reconstructions (fused arm) or the bf16-rounded restore (bridge arms)."""
+    import json
+    from pathlib import Path
+    rec = json.loads((Path(__file__).parent / "golden" / "vf01_input_hashes.json").read_text())
+    for f in rec["fixtures"]:
+        a, data = _fixture_data(f)
+        _, ctx, _, _ = kernels.pipeline(arm, data, trace=True, kernel="fast")
+        assert kernels.LAST_STAGE == "returned"
+        ref = _fixture_oracle(a, f, "float32" if arm == "V_FUSED" else "bfloat16")
+        ok, err = within(ctx.cpu().numpy().reshape(2, 128), ref)
+        assert ok, (f["id"], err)

@@ -62,7 +62,7 @@ def strided_tail(vt):
     return view
 
 
-def run(kind, arm):
+def run(kind, arm, kernel="reference"):
     a, mutation = gi.vf01_negative(kind)
     host_before = host_hashes(a)
     data = before = None
@@ -73,7 +73,7 @@ def run(kind, arm):
             g, kt, q, vg, vt = data
             data = (g, kt, q, vg, strided_tail(vt))
         before = device_hashes(data)
-        kernels.pipeline(arm, data)
+        kernels.pipeline(arm, data, kernel=kernel)
         result = dict(rejected=False, stage=kernels.LAST_STAGE, error_type=None)
     except (ContractError, IntegrityError, NumericalFailure) as exc:
         result = dict(rejected=True, stage=kernels.LAST_STAGE, error_type=type(exc).__name__)
@@ -82,11 +82,14 @@ def run(kind, arm):
     return result
 
 
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
 @pytest.mark.parametrize("arm", ARMS)
 @pytest.mark.parametrize("kind", gi.NEGATIVE_KINDS)
-def test_negative_fixture_rejected_at_reference_stage(kind, arm):
+def test_negative_fixture_rejected_at_reference_stage(kind, arm, kernel):
+    """kernel: the attention kernel behind every arm (the fast one checks the
+    raw block metadata while computing its decode factors)."""
     want = REJ[kind]
-    r = run(kind, arm)
+    r = run(kind, arm, kernel)
     assert r["rejected"], (kind, arm, r)
     assert r["stage"] == want["expected_stage"], (kind, arm, r)
     assert r["error_type"] == ERROR[want["expected_stage"]], (kind, arm, r)
@@ -104,15 +107,16 @@ def test_negative_fixtures_with_the_separate_finite_scan(monkeypatch):
         assert r["rejected"] and r["stage"] == REJ[kind]["expected_stage"] and r["input_unchanged"], (kind, r)
 
 
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
 @pytest.mark.parametrize("arm", ARMS)
-def test_normal_fixtures_leave_inputs_unchanged(arm):
+def test_normal_fixtures_leave_inputs_unchanged(arm, kernel):
     for f in NORMAL:
         a = gi.vf01_fixture(f["compressed"], f["length"], f["pattern"])
         assert host_hashes(a) == f["input_hashes"]
         data = contract.inputs(a, DEV)
         before = device_hashes(data)
         assert before == f["input_hashes"], f["id"]
-        out = kernels.pipeline(arm, data)
+        out = kernels.pipeline(arm, data, kernel=kernel)
         torch.cuda.synchronize()
         assert bool(torch.isfinite(out).all()) and kernels.LAST_STAGE == "returned", f["id"]
         assert device_hashes(data) == before and host_hashes(a) == f["input_hashes"], f["id"]
