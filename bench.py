@@ -664,11 +664,12 @@ C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
 
 def main_c4(args):
     """C4: a streaming packed cache of Ouro-like
-    slots (MHA, 16 kv heads, d=128, batch 32, N(0,1) fp16 activations, GPU
-    generator seed 4).  Per slot: an 8192-token chunked prefill (16 chunks of
-    512: prefill attention over packed context + tail + the chunk, append,
-    compress), then decode steps that append one token, attend over packed +
-    tail with the fast kernel and compress a block every 64 tokens.  The 96
+    slots (MHA, 16 kv heads, d=128, batch 32, N(0,1) bf16 activations, GPU
+    generator seed 4, fp16 tails).  Per slot: an 8192-token chunked prefill
+    (16 chunks of 512: bf16-MFMA prefill attention over packed context + tail
+    + the chunk, append to the fp16 tail, compress), then decode steps that
+    append one token, attend over packed + tail with the fast kernel and
+    compress a block every 64 tokens.  The 96
     slots of the configuration do identical work; `--slots` of them are run
     and the figures are per slot."""
     import torch
@@ -683,7 +684,7 @@ def main_c4(args):
     nchunks = T // ch
     log(f"[bench] C4: {S} slots x B={b_} x {h} kv-heads, {T}-token chunked prefill (chunk {ch}), decode")
     # activations: one set of chunk K/V/Q shared by the slots (identical work per slot)
-    acts = [tuple(torch.randn((b_, h, ch, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+    acts = [tuple(torch.randn((b_, h, ch, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
                   for _ in range(3)) for _ in range(nchunks)]
     cache = StreamingKVCache(S, b_, h, T + C4["steps"] + 64, bits=3, dtype=torch.float16, max_append=ch, device=dev)
 
@@ -708,7 +709,7 @@ def main_c4(args):
     flops = 2.0 * b_ * h * T * T * D          # causal QK^T + PV (2 * B * H * T^2 * d)
     mfma = flops / (pre_ms * 1e-3) / 1e12
     log(f"[bench] C4 prefill: {pre_ms:.2f} ms per slot (16 chunks incl. append + in-place encode), "
-        f"{mfma:.0f} TFLOP/s = {mfma / 2500:.1%} of 2.5 PFLOP/s dense fp16")
+        f"{mfma:.0f} TFLOP/s = {mfma / 2500:.1%} of 2.5 PFLOP/s dense bf16")
     # the prefill kernel alone, on the last chunk of one slot (context 7680 tokens)
     qc, kc, vc = acts[-1]
     saved = (cache.length[0], cache.compressed[0])
@@ -764,7 +765,8 @@ def main_c4(args):
         "metric": "C4 streaming cache: chunked-prefill ms/slot (MFMA %) + decode µs/slot/step",
         "value": round(dec_us, 2), "unit": "µs/slot/step", "n_gpus": 1, "steps": n_dec, "warmup": 2,
         "ms_per_step": round(dec_us * S / 1e3, 5), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f16", "data": "synthetic N(0,1) (GPU torch.Generator seed 4)",
+        "vs_baseline": None, "dtype": "bf16 prefill / f16x2 decode",
+        "data": "synthetic N(0,1) (GPU torch.Generator seed 4)",
         "config": {"workload": "C4: Ouro-like streaming cache, MHA 16 kv heads, d=128, batch 32, 8192-token "
                                "chunked prefill (chunk 512) + decode over packed INT3 + fp16 tail",
                    "slots_run": S, "batch": b_, "heads": h, "head_dim": D, "prefill_tokens": T, "chunk": ch,

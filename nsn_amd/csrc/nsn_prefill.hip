@@ -3,6 +3,9 @@
 // One chunk of n_q queries per (sequence, q-head) attends the sequence's
 // context -- packed 64-token blocks, then an fp16/bf16 tail -- and the chunk's
 // own dense K/V, causally (chunk query i sees chunk tokens 0..i).  The
+// products run in the chunk's dtype: v_mfma_f32_16x16x32_f16 for fp16 data,
+// v_mfma_f32_16x16x32_bf16 for bf16 data (no value is squeezed into the
+// fp16 range); a tail of the other dtype is converted as it is staged.  The
 // reference path materialises the whole K/V (restore of every packed block
 // plus the tail, loop_kv_pk01_cache.py:87-106) and runs dense attention on it;
 // here the packed blocks are dequantised tile by tile into LDS and never reach
@@ -15,17 +18,16 @@
 //      staged into LDS by DMA two blocks ahead;
 //   2. the 512 threads dequantise it once for the workgroup (threads 0-255
 //      K', 256-511 V'^T) into K' [64 tok][128 ch] and V'^T [128 ch][64 tok]
-//      (fp16; for fp16 data the per-token factor is folded in, for bf16
-//      data the directions m + s*z are stored and the factor is applied
-//      below), double-buffered so that the fill of the next block overlaps
+//      (the reconstructed values f_t * (m + s*z), rounded to the compute
+//      dtype), double-buffered so that the fill of the next block overlaps
 //      the products of this one;
-//   3. each wave computes S^T = K' Q^T and O^T += V'^T P^T on
-//      v_mfma_f32_16x16x32_f16 (bf16 data: the per-token factors applied to
-//      the scores (K) and to the softmax weights (V)) -- the transposed products keep P
-//      in registers: the C layout of S^T is already the B layout of P^T for
-//      a token order in which lane group g of a 32-token step holds tokens
-//      4g..4g+3 of both 16-token tiles.
-// Softmax runs in the log2 domain (Q pre-scaled by scale*log2(e)).
+//   3. each wave computes S^T = K' Q^T and O^T += V'^T P^T on MFMA -- the
+//      transposed products keep P in registers: the C layout of S^T is
+//      already the B layout of P^T for a token order in which lane group g
+//      of a 32-token step holds tokens 4g..4g+3 of both 16-token tiles.
+// Softmax runs in the log2 domain: fp16 queries are pre-scaled by
+// scale*log2(e); bf16 queries enter the product exactly and the scores are
+// scaled after it.
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -33,6 +35,8 @@ namespace prefill {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -43,16 +47,29 @@ constexpr int kKP = 136;      // K' row pitch (halves): 272 B rows
 constexpr int kVP = 72;       // V'^T row pitch (halves): 144 B rows
 constexpr float kLog2e = 1.4426950408889634f;
 
+// D = A B + C on the compute dtype CT (NSN_DTYPE_F16 or NSN_DTYPE_BF16).
+template <int CT>
 __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    if constexpr (CT == NSN_DTYPE_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                       0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0,
+                                                      0);
 }
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
-// fp32 pair -> packed fp16 (round to nearest even)
-__device__ __forceinline__ uint32_t pk16(float a, float b) {
-    const half2v h = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
-    return __builtin_bit_cast(uint32_t, h);
+// fp32 pair -> packed pair of the compute dtype (round to nearest even)
+template <int CT>
+__device__ __forceinline__ uint32_t pk(float a, float b) {
+    if constexpr (CT == NSN_DTYPE_BF16) {
+        const bf16x2 h = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+        return __builtin_bit_cast(uint32_t, h);
+    } else {
+        const half2v h = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+        return __builtin_bit_cast(uint32_t, h);
+    }
 }
 __device__ __forceinline__ float h16(uint32_t w, int hi) {
     return static_cast<float>(__builtin_bit_cast(half2v, w)[hi]);
@@ -108,7 +125,7 @@ struct Side {
     const float *factors;
     const int32_t *blocks;
     int64_t block_cap;
-    const uint16_t *tail;   // DT
+    const uint16_t *tail;   // TDT
     int64_t tail_cap;
 };
 
@@ -174,19 +191,16 @@ __device__ __forceinline__ int vpos(int t) {
     return (t & 32) | ((t & 12) << 1) | ((t & 16) >> 2) | (t & 3);
 }
 
-// The block buffer compute reads: K' [64 tok][kKP], V'^T [128 ch][kVP], and
-// (when the factors are not folded in) the K / V decode factors.
+// The block buffer compute reads: K' [64 tok][kKP], V'^T [128 ch][kVP].
 struct KV {
     uint16_t *kt, *vt;
-    float *fac;   // [K 64 | V 64]
 };
 
-// Fill one side of a KV buffer from a dense token source x (row pitch 128,
-// `valid` rows; rows past it are zero).  Thread: tokens 4*rg .. 4*rg+3,
-// channels 8*cg .. 8*cg+7; side 0 writes K' rows, side 1 V'^T columns.
-// (Dense tokens carry no decode factor: compute applies kv.fac to packed
-// blocks only.)
-template <int BITS, int DT, int side>
+// Fill one side of a KV buffer from a dense token source x of dtype DT (row
+// pitch 128, `valid` rows; rows past it are zero), rounded to CT.  Thread:
+// tokens 4*rg .. 4*rg+3, channels 8*cg .. 8*cg+7; side 0 writes K' rows,
+// side 1 V'^T columns.
+template <int BITS, int DT, int CT, int side>
 __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg, int cg, const KV &kv) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
@@ -206,12 +220,12 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg,
         }
         if constexpr (side == 0) {
             *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
-                uint4{pk16(f[O::chE[0]], f[O::chE[1]]), pk16(f[O::chE[2]], f[O::chE[3]]),
-                      pk16(f[O::chE[4]], f[O::chE[5]]), pk16(f[O::chE[6]], f[O::chE[7]])};
+                uint4{pk<CT>(f[O::chE[0]], f[O::chE[1]]), pk<CT>(f[O::chE[2]], f[O::chE[3]]),
+                      pk<CT>(f[O::chE[4]], f[O::chE[5]]), pk<CT>(f[O::chE[6]], f[O::chE[7]])};
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                if (i & 1) vcol[e][i >> 1] = pk16(vprev[e], f[e]);
+                if (i & 1) vcol[e][i >> 1] = pk<CT>(vprev[e], f[e]);
                 else vprev[e] = f[e];
             }
         }
@@ -225,10 +239,10 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg,
 
 // Fill one side of a KV buffer from a staged packed block: direction m + s*z
 // per element (one fma with the code as an exact fp16 subnormal, scaled back
-// by 2^(24-k)), times the token's decode factor when FOLD (fp16 data: the
-// product is the reconstructed value itself, within fp16 range by
-// construction); otherwise the factors go to kv.fac for the compute phase.
-template <int BITS, bool FOLD, int side>
+// by 2^(24-k)) times the token's decode factor -- the reconstructed value
+// itself (|x| <= its fp16 norm, so within fp16 range by construction),
+// rounded to CT.
+template <int BITS, int CT, int side>
 __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, const KV &kv) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
@@ -263,17 +277,14 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, c
             codes8<BITS>(codes + t * ROWB, cg, b);
             float d[8];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                d[p] = __builtin_fmaf(h16(b[p >> 1], p & 1), sE[p], mE[p]);
-                if (FOLD) d[p] *= ft;
-            }
+            for (int p = 0; p < 8; ++p) d[p] = __builtin_fmaf(h16(b[p >> 1], p & 1), sE[p], mE[p]) * ft;
             if constexpr (side == 0) {
                 *reinterpret_cast<uint4 *>(kv.kt + t * kKP + 8 * cg) =
-                    uint4{pk16(d[0], d[1]), pk16(d[2], d[3]), pk16(d[4], d[5]), pk16(d[6], d[7])};
+                    uint4{pk<CT>(d[0], d[1]), pk<CT>(d[2], d[3]), pk<CT>(d[4], d[5]), pk<CT>(d[6], d[7])};
             } else {
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
-                    if (h) vcol[p][slot] = pk16(vprev[p], d[p]);
+                    if (h) vcol[p][slot] = pk<CT>(vprev[p], d[p]);
                     else vprev[p] = d[p];
                 }
             }
@@ -287,18 +298,17 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, c
             *reinterpret_cast<uint32_t *>(dst + 2 * (pfirst ^ 1)) = vcol[p][1];
         }
     }
-    if (!FOLD && cg == 0) *reinterpret_cast<float4 *>(kv.fac + 64 * side + 4 * rg) = f4;
 }
 
-template <int BITS, int DT>
+// DT: dtype of the queries, the chunk K/V, the output and the products; TDT:
+// dtype of the context tail.
+template <int BITS, int DT, int TDT>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
-    // fp16 data: the decode factors are folded into K' / V'^T when they are filled
-    constexpr bool FOLD = DT == NSN_DTYPE_F16;
+    constexpr bool QPRE = DT == NSN_DTYPE_F16;   // fp16 queries carry scale*log2(e); bf16 ones stay exact
     __shared__ __align__(16) uint16_t kt[2][kBlockTok * kKP];
     __shared__ __align__(16) uint16_t vt[2][kDim * kVP];
-    __shared__ __align__(16) float fac[2][2 * kBlockTok];
     __shared__ __align__(16) uint8_t stg[2][S::BYTES];
 
     const int tid = threadIdx.x, l = tid & 63;
@@ -331,7 +341,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     }
 
     // ---- Q fragments (B operand of S^T = K' Q^T): query qw + 16*qt + row,
-    // channels 32*ks + 8*g + chE[e], times scale*log2(e), fp16
+    // channels 32*ks + 8*g + chE[e] (fp16: times scale*log2(e))
     u32x4 qf[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -344,14 +354,16 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                     p.q + ((static_cast<int64_t>(b) * p.heads_q + hq) * p.n_q + qi) * kDim + 32 * ks + 8 * g);
                 const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    x[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)))) * p.qscale;
+                for (int e = 0; e < 8; ++e) {
+                    x[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
+                    if (QPRE) x[e] *= p.qscale;
+                }
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] = 0.f;
             }
-            qf[qt][ks] = u32x4{pk16(x[O::chE[0]], x[O::chE[1]]), pk16(x[O::chE[2]], x[O::chE[3]]),
-                               pk16(x[O::chE[4]], x[O::chE[5]]), pk16(x[O::chE[6]], x[O::chE[7]])};
+            qf[qt][ks] = u32x4{pk<DT>(x[O::chE[0]], x[O::chE[1]]), pk<DT>(x[O::chE[2]], x[O::chE[3]]),
+                               pk<DT>(x[O::chE[4]], x[O::chE[5]]), pk<DT>(x[O::chE[6]], x[O::chE[7]])};
         }
     }
 
@@ -379,23 +391,23 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     };
     // Fill block j into KV buffer j & 1 (its raw stage j & 1 when packed).
     auto fill = [&](int64_t j) {
-        const KV kv{kt[j & 1], vt[j & 1], fac[j & 1]};
+        const KV kv{kt[j & 1], vt[j & 1]};
         if (j < nb) {
-            if (side) fill_packed<BITS, FOLD, 1>(stg[j & 1], rg, cg, kv);
-            else fill_packed<BITS, FOLD, 0>(stg[j & 1], rg, cg, kv);
+            if (side) fill_packed<BITS, DT, 1>(stg[j & 1], rg, cg, kv);
+            else fill_packed<BITS, DT, 0>(stg[j & 1], rg, cg, kv);
         } else {
             int valid;
             int64_t cpos;
             block_rows(j, valid, cpos);
-            const uint16_t *src;
             if (cpos < 0) {
                 const int64_t t0 = (j - nb) * kBlockTok;
-                src = side ? p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim : p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim;
+                if (side) fill_dense<BITS, TDT, DT, 1>(p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim, valid, rg, cg, kv);
+                else fill_dense<BITS, TDT, DT, 0>(p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim, valid, rg, cg, kv);
             } else {
-                src = (side ? p.vc : p.kc) + (seqrow * p.n_q + cpos) * kDim;
+                const uint16_t *src = (side ? p.vc : p.kc) + (seqrow * p.n_q + cpos) * kDim;
+                if (side) fill_dense<BITS, DT, DT, 1>(src, valid, rg, cg, kv);
+                else fill_dense<BITS, DT, DT, 0>(src, valid, rg, cg, kv);
             }
-            if (side) fill_dense<BITS, DT, 1>(src, valid, rg, cg, kv);
-            else fill_dense<BITS, DT, 0>(src, valid, rg, cg, kv);
         }
     };
 
@@ -435,19 +447,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             for (int ks = 0; ks < 4; ++ks) {
                 const u32x4 a = *reinterpret_cast<const u32x4 *>(ktj + (16 * tt + row) * kKP + 32 * ks + 8 * g);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) s[tt][qt] = mfma(a, qf[qt][ks], s[tt][qt]);
-            }
-        }
-        // per-token factors of this lane's tokens 16*tt + 4*g + i (not folded: bf16 data)
-        float fk[4][4], fv[4][4];
-        if (!FOLD) {
-            const float *fks = fac[j & 1];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const float4 a = *reinterpret_cast<const float4 *>(fks + 16 * tt + 4 * g);
-                const float4 c = *reinterpret_cast<const float4 *>(fks + 64 + 16 * tt + 4 * g);
-                fk[tt][0] = a.x; fk[tt][1] = a.y; fk[tt][2] = a.z; fk[tt][3] = a.w;
-                fv[tt][0] = c.x; fv[tt][1] = c.y; fv[tt][2] = c.z; fv[tt][3] = c.w;
+                for (int qt = 0; qt < 2; ++qt) s[tt][qt] = mfma<DT>(a, qf[qt][ks], s[tt][qt]);
             }
         }
         // ---- online softmax per query (lane's query qw + 16*qt + row).  The
@@ -457,11 +457,11 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            if (!FOLD && packed) {
+            if (!QPRE) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) s[tt][qt][i] *= fk[tt][i];
+                    for (int i = 0; i < 4; ++i) s[tt][qt][i] *= p.qscale;
             }
             if (masked) {
                 // allowed tokens of this block: tok < valid and (chunk blocks) tok <= query - cpos
@@ -496,14 +496,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 for (int i = 0; i < 4; ++i) {
                     const float e = __builtin_amdgcn_exp2f(s[tt][qt][i] - msafe);
                     ls += e;
-                    pw[tt][i] = (!FOLD && packed) ? e * fv[tt][i] : e;
+                    pw[tt][i] = e;
                 }
             l_run[qt] += ls;
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2)
-                pb[ks2][qt] = u32x4{pk16(pw[2 * ks2][0], pw[2 * ks2][1]), pk16(pw[2 * ks2][2], pw[2 * ks2][3]),
-                                    pk16(pw[2 * ks2 + 1][0], pw[2 * ks2 + 1][1]),
-                                    pk16(pw[2 * ks2 + 1][2], pw[2 * ks2 + 1][3])};
+                pb[ks2][qt] = u32x4{pk<DT>(pw[2 * ks2][0], pw[2 * ks2][1]), pk<DT>(pw[2 * ks2][2], pw[2 * ks2][3]),
+                                    pk<DT>(pw[2 * ks2 + 1][0], pw[2 * ks2 + 1][1]),
+                                    pk<DT>(pw[2 * ks2 + 1][2], pw[2 * ks2 + 1][3])};
         }
         // ---- O^T[channel][query] += V'^T P''^T (k order: tokens 4g..4g+3 of both 16-token tiles)
 #pragma unroll
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             for (int ks2 = 0; ks2 < 2; ++ks2) {
                 const u32x4 a = *reinterpret_cast<const u32x4 *>(vtj + (16 * ct + row) * kVP + 32 * ks2 + 8 * g);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma(a, pb[ks2][qt], acc[ct][qt]);
+                for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma<DT>(a, pb[ks2][qt], acc[ct][qt]);
             }
         }
     }
@@ -567,8 +567,13 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     };
     if (!side_ok(a->k) || !side_ok(a->v)) return NSN_EINVAL;
     if (!a->k.blocks != !a->v.blocks) return NSN_EINVAL;
-    if (a->k.tail && a->k.tail_dtype != a->dtype) return NSN_EINVAL;
-    if (a->v.tail && a->v.tail_dtype != a->dtype) return NSN_EINVAL;
+    auto tail_ok = [](const nsn_kv_side &s) {
+        return !s.tail || s.tail_dtype == NSN_DTYPE_F16 || s.tail_dtype == NSN_DTYPE_BF16;
+    };
+    if (!tail_ok(a->k) || !tail_ok(a->v)) return NSN_EINVAL;
+    if (a->k.tail && a->v.tail && a->k.tail_dtype != a->v.tail_dtype) return NSN_EINVAL;
+    const nsn_kv_side &ts = a->k.tail ? a->k : a->v;
+    const bool tbf = ts.tail ? ts.tail_dtype == NSN_DTYPE_BF16 : a->dtype == NSN_DTYPE_BF16;
     for (const void *ptr : {static_cast<const void *>(a->q), a->k_chunk, a->v_chunk, static_cast<const void *>(a->out)})
         if (reinterpret_cast<uintptr_t>(ptr) & 15u) return NSN_EINVAL;
     const int64_t qt = (a->n_q + kQTile - 1) / kQTile;
@@ -595,12 +600,18 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     const dim3 grid(static_cast<unsigned>(qt), static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool bf = a->dtype == NSN_DTYPE_BF16;
+#define NSN_PREFILL_LAUNCH(B_, D_)                                                                              \
+    do {                                                                                                        \
+        if (tbf) hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p); \
+        else hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);      \
+    } while (0)
     if (a->bits == 3) {
-        if (bf) hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p);
-        else hipLaunchKernelGGL((prefill_kernel<3, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);
+        if (bf) NSN_PREFILL_LAUNCH(3, NSN_DTYPE_BF16);
+        else NSN_PREFILL_LAUNCH(3, NSN_DTYPE_F16);
     } else {
-        if (bf) hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p);
-        else hipLaunchKernelGGL((prefill_kernel<5, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);
+        if (bf) NSN_PREFILL_LAUNCH(5, NSN_DTYPE_BF16);
+        else NSN_PREFILL_LAUNCH(5, NSN_DTYPE_F16);
     }
+#undef NSN_PREFILL_LAUNCH
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }

@@ -217,7 +217,8 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     """Chunked-prefill attention over a packed context (C4's prefill step).
 
     q [B, Hq, n, 128]; k_chunk, v_chunk [B, Hkv, n, 128] (the chunk's own K/V;
-    one dtype, fp16 or bf16, for q, chunk, tails and output).  Chunk query i
+    one dtype, fp16 or bf16, for q, chunk and output, and the dtype of the
+    MFMA products; the tails may hold either dtype).  Chunk query i
     attends the context -- ``blocks[b]`` packed blocks then ``ctx_len[b] -
     64*blocks[b]`` tail tokens of k/v (None: no context) -- and chunk tokens
     0..i.  Returns out [B, Hq, n, 128].  The reference materialises the
@@ -242,8 +243,9 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
         for side in (k, v):
             side.validate(B, Hkv)
             require(side.codes is None or side.factor is not None, "Prefill needs decode factors")
-            require(side.tail is None or side.tail.dtype == q.dtype, "Tail dtype must equal the query dtype")
+            require(side.tail is None or side.tail.dtype in (torch.float16, torch.bfloat16), "Tail dtype (fp16 or bf16)")
         require(k.bits == v.bits and k.bits in (3, 5), "Prefill supports 3- and 5-bit codes")
+        require(k.tail is None or v.tail is None or k.tail.dtype == v.tail.dtype, "K/V tail dtypes differ")
         require((k.codes is None) == (v.codes is None), "K/V packed layout differs")
         bits = k.bits
         if check:

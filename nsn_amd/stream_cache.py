@@ -58,9 +58,9 @@ class StreamingKVCache:
 
     max_tokens bounds the sequence length (block capacity = max_tokens // 64);
     max_append bounds the tokens appended between two compressions (a
-    prefill chunk, or 1 per decode step).  The tail dtype is the dtype of
-    the appended K/V; the fast decode kernel reads fp16 tails, so fp16 is the
-    default (bf16 activations convert exactly within fp16's normal range).
+    prefill chunk, or 1 per decode step).  ``dtype`` is the tail's dtype
+    (fp16 or bf16; both kernels read either); appended K/V of another dtype
+    are converted to it.
     """
 
     def __init__(self, slots, batch, heads, max_tokens, *, bits=3, dtype=torch.float16, max_append=512,
@@ -117,7 +117,7 @@ class StreamingKVCache:
 
     # ------------------------------------------------------------------ updates
     def append(self, slot, k, v):
-        """Append k, v [B, H, n, 128] (the cache dtype) to the slot's tail."""
+        """Append k, v [B, H, n, 128] to the slot's tail (converted to the tail dtype if needed)."""
         require(k.shape == v.shape and k.ndim == 4 and tuple(k.shape[:2]) == (self.batch, self.heads)
                 and k.shape[3] == DIM, "Append shape")
         n = k.shape[2]
@@ -126,8 +126,10 @@ class StreamingKVCache:
             raise IntegrityError("Tail overflow: compress before appending more tokens")
         if self.length[slot] + n > self.block_cap * BLOCK + self.tail_cap:
             raise IntegrityError("Cache capacity exceeded")
-        require(k.dtype == self.dtype and v.dtype == self.dtype and k.is_contiguous() and v.is_contiguous(),
-                "Append dtype/layout")
+        require(k.dtype in (torch.float16, torch.bfloat16, torch.float32) and v.dtype == k.dtype, "Append dtype")
+        if k.dtype != self.dtype:
+            k, v = k.to(self.dtype), v.to(self.dtype)
+        k, v = k.contiguous(), v.contiguous()
         kt, vt = self._sides[(slot, "K")].kv.tail, self._sides[(slot, "V")].kv.tail
         rc = _lib.lib().nsn_tail_append(k.data_ptr(), v.data_ptr(), self.batch * self.heads, n, n, kt.data_ptr(),
                                         vt.data_ptr(), self.tail_cap, t0, _dev.dtype_code(self.dtype), _dev.stream())

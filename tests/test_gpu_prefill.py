@@ -1,14 +1,15 @@
 """GPU parity of the chunked-prefill attention (nsn_prefill_attention) through the C-ABI.
 
 Expected values: the context K/V restored by the oracle (C restatement of
-nsn_encode + nsn_decode, fp32 reconstructions), the tail and the chunk K/V as
-stored, then the oracle's float64 chunked-prefill attention
+nsn_encode + nsn_decode: fp32 reconstructions for fp16 data, rounded to bf16
+for bf16 data as the reference's restore returns them), the tail and the
+chunk K/V as stored, then the oracle's float64 chunked-prefill attention
 (oracle.prefill_attention64, pinned row by row against the decode oracle).
 Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise, on
 top of the output's own rounding (bf16/fp16).  K/V and queries are N(0,1)
-activations, as in the chunked-prefill configuration: the kernel's MFMA
-operands are fp16 (11-bit significands), so its absolute error grows with
-the largest |v| a query attends to (about 2^-12 of it).
+activations, as in the chunked-prefill configuration.  The MFMA operands
+have the data's dtype (fp16: 11-bit, bf16: 8-bit significands), so the
+absolute error grows with the largest |v| a query attends to.
 """
 import numpy as np
 import pytest
@@ -28,9 +29,9 @@ def normal_tokens(rng, prefix, ntok):
     return rng.standard_normal(tuple(prefix) + (ntok, 128)).astype(np.float16)
 
 
-def restore_ctx(x16, length, bits, dtype):
+def restore_ctx(x16, length, bits, dtype, packed_dtype=None):
     """[H, T, 128] fp16 source -> fp32 [H, length, 128]: packed blocks restored
-    (fp32), tail tokens as stored in `dtype`."""
+    (fp32, rounded to ``packed_dtype`` when bf16), tail tokens as stored in `dtype`."""
     H = x16.shape[0]
     C = (length // 64) * 64
     parts = []
@@ -38,23 +39,30 @@ def restore_ctx(x16, length, bits, dtype):
         blocks = x16[:, :C].astype(np.float32).reshape(H, C // 64, 64, 128)
         q, n, m, s, err = O.nsn_encode(blocks, bits)
         assert err == 0
-        parts.append(O.nsn_decode_f32(q, n, m, s).reshape(H, C, 128))
+        y = O.nsn_decode_f32(q, n, m, s).reshape(H, C, 128)
+        if packed_dtype == torch.bfloat16:
+            y = O.from_bf16_bits(O.cast_bits(y, "bfloat16"))
+        parts.append(y)
     if length > C:
         parts.append(torch.from_numpy(x16[:, C:length]).to(dtype).float().numpy())
     return np.concatenate(parts, axis=1) if parts else np.zeros((H, 0, 128), np.float32)
 
 
-def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
+def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chunk_scale=None):
+    """chunk_scale: optional [n] multipliers of the chunk's V rows (values past fp16's range)."""
     rng = np.random.default_rng(seed)
+    tail_dtype = tail_dtype or dtype
     T = max(max(ctx_lengths), 1)
     kx = normal_tokens(rng, (B, Hkv), T)
     vx = normal_tokens(rng, (B, Hkv), T)
     kch = torch.from_numpy(normal_tokens(rng, (B, Hkv), n)).to(dtype)
     vch = torch.from_numpy(normal_tokens(rng, (B, Hkv), n)).to(dtype)
+    if chunk_scale is not None:
+        vch = (vch.float() * torch.from_numpy(chunk_scale.astype(np.float32))[None, None, :, None]).to(dtype)
     q = torch.from_numpy(rng.standard_normal((B, Hq, n, 128)).astype(np.float32)).to(dtype)
     if max(ctx_lengths) > 0:
-        kk, seq = cache.pack_sequences(torch.from_numpy(kx).to(DEV), ctx_lengths, bits=bits, tail_dtype=dtype)
-        vv, _ = cache.pack_sequences(torch.from_numpy(vx).to(DEV), ctx_lengths, bits=bits, tail_dtype=dtype)
+        kk, seq = cache.pack_sequences(torch.from_numpy(kx).to(DEV), ctx_lengths, bits=bits, tail_dtype=tail_dtype)
+        vv, _ = cache.pack_sequences(torch.from_numpy(vx).to(DEV), ctx_lengths, bits=bits, tail_dtype=tail_dtype)
     else:
         kk = vv = None
         seq = torch.zeros(B, dtype=torch.int32, device=DEV)
@@ -62,12 +70,20 @@ def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype):
     got = out.float().cpu().numpy()
     for b in range(B):
         L = ctx_lengths[b]
-        kc = restore_ctx(kx[b], L, bits, dtype)
-        vc = restore_ctx(vx[b], L, bits, dtype)
+        kc = restore_ctx(kx[b], L, bits, tail_dtype, dtype)
+        vc = restore_ctx(vx[b], L, bits, tail_dtype, dtype)
         ref = O.prefill_attention64(q[b].float().numpy(), kc, vc, kch[b].float().numpy(), vch[b].float().numpy())
         ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11      # output rounding
         err = np.abs(got[b] - ref)
         bound = ATOL + (RTOL + ulp) * np.abs(ref)
+        if dtype == torch.bfloat16:
+            # bf16 softmax weights carry a 2^-9 relative rounding each, so the
+            # output may move by 2^-9 of the attention-weighted |v| (computed
+            # exactly: the same attention over |V|); 2^-8 leaves room for the
+            # K and V rounding
+            wabs = O.prefill_attention64(q[b].float().numpy(), kc, np.abs(vc), kch[b].float().numpy(),
+                                         np.abs(vch[b].float().numpy()))
+            bound = bound + 2.0 ** -8 * wabs
         assert np.all(err <= bound), (b, float(err.max()), float((err / bound).max()))
 
 
@@ -101,3 +117,16 @@ def test_prefill_block_aligned_context_gqa8():
 
 def test_prefill_5bit():
     run_case(24, 2, 2, 2, [192, 100], 70, 5, torch.float16)
+
+
+def test_prefill_bf16_products_with_an_fp16_tail():
+    """C4's mix: bf16 queries and chunk on the bf16 MFMA over an fp16 tail."""
+    run_case(27, 2, 4, 2, [300, 77], 150, 3, torch.bfloat16, tail_dtype=torch.float16)
+
+
+def test_prefill_bf16_values_beyond_fp16_range():
+    """bf16 chunk values of order 1e6 compute on the bf16 products (fp16 would
+    overflow); the error stays within 2^-8 of the attention-weighted |v|."""
+    scale = np.ones(200)
+    scale[3::11] = 1e6
+    run_case(28, 1, 2, 2, [130], 200, 3, torch.bfloat16, chunk_scale=scale)
