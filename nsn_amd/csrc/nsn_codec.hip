@@ -28,9 +28,15 @@ namespace nsn {
 //     x * RN(1/n)); one fp64 multiply by RN64(1/n) for bf16 / fp32 input;
 //   - per-channel min / max: min3 / max3 over the thread's 4 rows, then the
 //     16 row-group partials through LDS;
-//   - codes: t = d - m, RN32(t / s) by one fp64 multiply, the half-even
-//     rounding to an integer by adding 1.5 * 2^23, and a shift-add of that
-//     word straight into the row's bitstream;
+//   - codes: t = d - m, RN32(t / s) as RN(t * yh + RN(t * yl)) with
+//     yh + yl = 1/s to about 2^-48 (one multiply, one fma; the half-even code
+//     is exact for every scale s >= 2^-64, tests/exact_code_check.c), the
+//     half-even rounding to an integer by adding 1.5 * 2^23, and a shift-add
+//     of that word straight into the row's bitstream; blocks with a smaller
+//     nonzero scale take a clamped copy of the loop on an fp64 multiply;
+//   - decode factors (optional): each lane sums (m + s*code)^2 over its 8
+//     channels per row, a 16-lane DPP tree finishes the row, and one lane per
+//     row divides the fp16 norm by the root; no second pass over the block;
 //   - no per-element finite test: a nonfinite input shows in its row norm.
 // =====================================================================
 
@@ -47,7 +53,7 @@ struct EncodeParams {
     uint8_t *codes_unpacked;
     int32_t *status;
     int zero_flat_scale;
-    int grid2d;   // 1: blockIdx.y = outer row, blockIdx.x = block; 0: one flat index
+    int64_t total;   // n_outer * n_blocks, one workgroup each
 };
 
 constexpr int kXPadT = kDim + 8;  // LDS row pitch of the encode input block (elements; 16-byte rows)
@@ -197,273 +203,355 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     using T = typename Elem<DT>::T;
     constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
     // The input block (in its own type) is only read by the norm pass; the
-    // 16 row-group min/max partials and then the u8 codes reuse its bytes.
+    // 16 row-group min/max partials reuse its bytes.
     // Keeping the block at 2 bytes per element (fp16/bf16 inputs) holds the
-    // LDS to ~22 KB per workgroup.
+    // LDS to ~22 KB per workgroup: 7 workgroups per CU.
     constexpr int kXBytes = kBlockTok * kXPadT * static_cast<int>(sizeof(T));
     static_assert(kXBytes >= 2 * 16 * kDim * 4, "LDS aliasing");
     __shared__ __align__(16) uint8_t xraw[kXBytes];
     T *const xs = reinterpret_cast<T *>(xraw);
     float (*const pmin)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw);           // [16][128], after the norms
     float (*const pmax)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 8192);    // [16][128]
-    uint32_t *const codes_s = reinterpret_cast<uint32_t *>(xraw);                  // u8 codes, after the partials
     __shared__ float nrm_s[kBlockTok], den_s[kBlockTok], rcp_s[kBlockTok];
-    __shared__ double rden_s[kBlockTok];
+    __shared__ double rden_s[DT == NSN_DTYPE_F16 ? 1 : kBlockTok];   // fp16 input divides by den and rcp
     __shared__ float m_s[kDim];
     __shared__ double rs_s[kDim];
+    __shared__ float yh_s[kDim], yl_s[kDim];
     __shared__ float mh_s[kDim], sh_s[kDim], nh_s[kBlockTok];
     __shared__ int bad_s, clamp_s;
 
     const int tid = threadIdx.x;
-    int64_t o, i;
-    if (p.grid2d) {
-        o = blockIdx.y;
-        i = blockIdx.x;
-    } else {
-        const uint32_t b = blockIdx.x, nb = static_cast<uint32_t>(p.n_blocks);
-        o = b / nb;
-        i = b - static_cast<uint32_t>(o) * nb;
-    }
-    const int64_t ob = o * p.out_outer_blocks + p.out_block_offset + i;
-    const T *x = static_cast<const T *>(p.x) + o * p.x_outer_stride + (p.x_token_offset + i * kBlockTok) * kDim;
-
+    const int cg = tid & 15, r0 = tid >> 4;
+    const uint32_t f = blockIdx.x;   // block f: outer row f / n_blocks, block f % n_blocks
+    const uint32_t o = f / static_cast<uint32_t>(p.n_blocks), i = f - o * static_cast<uint32_t>(p.n_blocks);
+    const int64_t ob = static_cast<int64_t>(o) * p.out_outer_blocks + p.out_block_offset + i;
+    constexpr int NW = (DT == NSN_DTYPE_F32) ? 8 : 4;   // dwords per 8 values
+    int status_acc = 0;
     if (tid == 0) {
         bad_s = 0;
         clamp_s = 0;
     }
-    const int cg = tid & 15, r0 = tid >> 4;
-
-    // ---- load: the thread's 4 rows x 8 channels as raw dwords, also staged in LDS
-    constexpr int NW = (DT == NSN_DTYPE_F32) ? 8 : 4;   // dwords per 8 values
-    uint32_t xw[4][NW];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = r0 + 16 * j;
-        const uint4 *src = reinterpret_cast<const uint4 *>(x + r * kDim + 8 * cg);
-        uint4 *dst = reinterpret_cast<uint4 *>(xs + r * kXPadT + 8 * cg);
-#pragma unroll
-        for (int h = 0; h < NW / 4; ++h) {
-            const uint4 a = src[h];
-            dst[h] = a;
-            xw[j][4 * h] = a.x; xw[j][4 * h + 1] = a.y; xw[j][4 * h + 2] = a.z; xw[j][4 * h + 3] = a.w;
-        }
-    }
-    __syncthreads();
-
-    // ---- token norms, in torch's order.  A nonfinite input makes its row's
-    // norm nonfinite; for fp16 the converse holds too (128 squares of finite
-    // fp16 values stay below 2^40), otherwise the row is scanned.
-    auto set_row = [&](int r, float n) {
-        nrm_s[r] = n;
-        const float den = clamp_eps(n);
-        const double rd = recip_rn(den);
-        den_s[r] = den;
-        rden_s[r] = rd;
-        rcp_s[r] = static_cast<float>(rd);   // RN32(RN64(1/den)) = RN32(1/den): 1/den is never that close to a tie
-        if (!finite(n)) {
-            bool row_bad = DT == NSN_DTYPE_F16;
-            if (!row_bad)
-                for (int c = 0; c < kDim; ++c) row_bad |= !finite(Elem<DT>::load(xs[r * kXPadT + c]));
-            if (row_bad) bad_s = 1;
-        }
-    };
-    if constexpr (ORDER == NSN_NORM_LANES8) {
-        const int r = tid >> 2, jp = (tid & 3) * 2;
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            float q0, q1;
-            if constexpr (DT == NSN_DTYPE_F32) {
-                const float2 q = *reinterpret_cast<const float2 *>(xs + r * kXPadT + 8 * k + jp);
-                q0 = q.x;
-                q1 = q.y;
-            } else {
-                const uint32_t q = *reinterpret_cast<const uint32_t *>(xs + r * kXPadT + 8 * k + jp);
-                q0 = Elem<DT>::load(static_cast<uint16_t>(q & 0xffffu));
-                q1 = Elem<DT>::load(static_cast<uint16_t>(q >> 16));
-            }
-            a0 = __builtin_fmaf(q0, q0, a0);
-            a1 = __builtin_fmaf(q1, q1, a1);
-        }
-        // the row's 4 threads are one quad of lanes: lane 0 gathers lanes 1..3
-        const float b0 = dpp_f32<0xF9>(a0), b1 = dpp_f32<0xF9>(a1);   // quad_perm [1,2,3,3]
-        const float c0 = dpp_f32<0xFE>(a0), c1 = dpp_f32<0xFE>(a1);   // quad_perm [2,3,3,3]
-        const float d0 = dpp_f32<0xFF>(a0), d1 = dpp_f32<0xFF>(a1);   // quad_perm [3,3,3,3]
-        if ((tid & 3) == 0) {
-            const float acc[8] = {a0, a1, b0, b1, c0, c1, d0, d1};
-            set_row(r, sqrt_rn(lane8_sum(acc)));
-        }
-    } else {
-        if (tid < kBlockTok) {
-            float s = 0.f;
-            for (int c = 0; c < kDim; ++c) {
-                const float q = Elem<DT>::load(xs[tid * kXPadT + c]);
-                s = __builtin_fmaf(q, q, s);
-            }
-            set_row(tid, sqrt_rn(s));
-        }
-    }
-    __syncthreads();
-
-    // ---- directions d = x / max(n, eps), and the thread's min / max per channel
-    float d[4][8];
-    const float neg0 = keep_f32(-0.f);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = r0 + 16 * j;
-        if constexpr (DT == NSN_DTYPE_F16) {
-            const float dn = den_s[r], rc = rcp_s[r];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t w = xw[j][e >> 1];
-                d[j][e] = div_f16_markstein((e & 1) ? half_hi(w) : half_lo(w), dn, rc, neg0);
-            }
-        } else {
-            const double rd = rden_s[r];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float v;
-                if constexpr (DT == NSN_DTYPE_F32) v = __uint_as_float(xw[j][e]);
-                else v = __uint_as_float((e & 1) ? (xw[j][e >> 1] & 0xffff0000u) : (xw[j][e >> 1] << 16));
-                d[j][e] = div_by_recip(v, rd);
-            }
-        }
-    }
     {
-        float mn[8], mx[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            mn[e] = fminf(fminf(fminf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
-            mx[e] = fmaxf(fmaxf(fmaxf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
-        }
-        float4 *pn = reinterpret_cast<float4 *>(&pmin[r0][8 * cg]);
-        float4 *px = reinterpret_cast<float4 *>(&pmax[r0][8 * cg]);
-        pn[0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
-        pn[1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
-        px[0] = make_float4(mx[0], mx[1], mx[2], mx[3]);
-        px[1] = make_float4(mx[4], mx[5], mx[6], mx[7]);
-    }
-    __syncthreads();
-
-    // ---- per-channel min / scale over the 16 row-group partials; fp16 metadata
-    int meta_flags = 0;
-    if (tid < kDim) {
-        float lo = pmin[0][tid], hi = pmax[0][tid];
-#pragma unroll
-        for (int w = 1; w < 16; ++w) {
-            lo = fminf(lo, pmin[w][tid]);
-            hi = fmaxf(hi, pmax[w][tid]);
-        }
-        const float s = div_by_recip(hi - lo, recip_rn(kLevels));
-        m_s[tid] = lo;
-        // 1/s; for s == 0 the reference divides by 1 (every d - m is 0 then),
-        // or zeroes the codes when zero_flat_scale is set: a factor of 0
-        rs_s[tid] = (s == 0.f) ? (p.zero_flat_scale ? 0.0 : 1.0) : recip_rn(s);
-        // With a subnormal s the quotient (d - m) / s can pass the top level
-        // (s then also underflows fp16, which the status word reports): the
-        // code pass clamps only in that case.
-        if (s != 0.f && !(s >= 1.17549435e-38f)) clamp_s = 1;
-        const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
-        p.mins[ob * kDim + tid] = hm;
-        p.scales[ob * kDim + tid] = hs;
-        mh_s[tid] = f16_bits_to_f32(hm);
-        sh_s[tid] = f16_bits_to_f32(hs);
-        if ((hm & 0x7c00u) == 0x7c00u || (hs & 0x7c00u) == 0x7c00u) meta_flags |= NSN_ST_META_NONFINITE;
-        if (s != 0.f && (hs & 0x7fffu) == 0) meta_flags |= NSN_ST_META_UNDERFLOW;
-    } else if (tid < kDim + kBlockTok) {
-        const int t = tid - kDim;
-        const float n = nrm_s[t];
-        const uint16_t hn = f32_to_f16_bits(n);
-        p.norms[ob * kBlockTok + t] = hn;
-        nh_s[t] = f16_bits_to_f32(hn);
-        if ((hn & 0x7c00u) == 0x7c00u) meta_flags |= NSN_ST_META_NONFINITE;
-        if (n != 0.f && (hn & 0x7fffu) == 0) meta_flags |= NSN_ST_META_UNDERFLOW;
-    }
-    __syncthreads();
-
-    // ---- codes clamp(round_half_even((d - m) / s), 0, 2^b - 1), packed in place.
-    // q = RN32(t / s) lies in [0, 2^b - 1 + 2^-20] for a normal s, so q + 1.5*2^23
-    // rounds it half-even to an integer held in the low mantissa bits; the
-    // shift-add of those words into the bitstream carries the constant
-    // exponent bits along, removed once per row.
-    float mreg[8];
-    double rsreg[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        mreg[e] = m_s[8 * cg + e];
-        rsreg[e] = rs_s[8 * cg + e];
-    }
-    // the lane's first output word (row r0); row r0 + 16j is 16j rows further on
-    const int k4 = cg & 3, a4 = cg >> 2;
-    uint8_t *const cbase = p.codes + ob * packed_block_bytes(BITS) + r0 * (16 * BITS);
-    uint32_t *const cdst = reinterpret_cast<uint32_t *>(
-        cbase + (BITS == 4 ? 4 * cg : (BITS == 3 ? 12 * a4 : 20 * a4) + 4 * k4));
-    constexpr int kRowStride = 16 * 16 * BITS / 4;   // dwords per 16 rows
-    uint2 *const udst = p.codes_unpacked
-        ? reinterpret_cast<uint2 *>(p.codes_unpacked + (o * p.n_blocks + i) * (kBlockTok * kDim) + r0 * kDim + 8 * cg)
-        : nullptr;
-    uint2 *const sdst = reinterpret_cast<uint2 *>(&codes_s[r0 * 32 + 2 * cg]);
-    auto code_rows = [&](auto clamp_c) {
-        constexpr bool CLAMP = decltype(clamp_c)::value;
+        // ---- load: the thread's 4 rows x 8 channels as raw dwords (16-byte
+        // loads; a wave reads 1 KiB of consecutive input per row group)
+        const T *x = static_cast<const T *>(p.x) + static_cast<int64_t>(o) * p.x_outer_stride +
+                     (p.x_token_offset + static_cast<int64_t>(i) * kBlockTok) * kDim;
+        uint32_t xw[4][NW];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint32_t v[8];
+            const uint4 *src = reinterpret_cast<const uint4 *>(x + (r0 + 16 * j) * kDim + 8 * cg);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float t = d[j][e] - mreg[e];
-                float q = static_cast<float>(static_cast<double>(t) * rsreg[e]);
-                if (CLAMP) q = fminf(q, kLevels);
-                v[e] = __float_as_uint(q + kRoundMagic);
-            }
-            uint32_t lo = v[0] - magic_sum_lo<BITS>();
-            lo = lshl_add<BITS>(v[1], lo);
-            lo = lshl_add<2 * BITS>(v[2], lo);
-            lo = lshl_add<3 * BITS>(v[3], lo);
-            lo = lshl_add<4 * BITS>(v[4], lo);
-            lo = lshl_add<5 * BITS>(v[5], lo);
-            lo = lshl_add<6 * BITS>(v[6], lo);
-            if constexpr (BITS < 5) lo = lshl_add<7 * BITS>(v[7], lo);
-            uint32_t *const dst = cdst + kRowStride * j;
-            if constexpr (BITS == 3) {
-                // a quad of lanes holds 96 consecutive bits: lane k writes dword k < 3
-                const uint32_t nxt = dpp_u32<0xF9>(lo);   // quad_perm [1,2,3,3]: lane k+1
-                const uint32_t D = (lo >> (8 * k4)) | (nxt << (24 - 8 * k4));
-                if (k4 < 3) *dst = D;
-            } else if constexpr (BITS == 4) {
-                *dst = lo;
-            } else {
-                // 40 bits per lane, 160 per quad: lane k writes dword k, lane 3 also dword 4
-                const uint32_t hi = lshl_add<3>(v[7], (v[6] >> 2) - ((0x4B400000u >> 2) + (0x4B400000u << 3)));
-                const uint32_t plo = dpp_u32<0x90>(lo), phi = dpp_u32<0x90>(hi);   // quad_perm [0,0,1,2]: lane k-1
-                const uint64_t P = (static_cast<uint64_t>(phi) << 32) | plo;
-                *dst = static_cast<uint32_t>(P >> (40 - 8 * k4)) | (lo << (8 * k4));
-                if (k4 == 3) dst[1] = (lo >> 8) | (hi << 24);
-            }
-            if (p.factors || p.codes_unpacked) {
-                // u8 codes: the low byte of each word
-                const uint32_t b0 = perm_b32(v[1], v[0], 0x0C0C0400u) | perm_b32(v[3], v[2], 0x04000C0Cu);
-                const uint32_t b1 = perm_b32(v[5], v[4], 0x0C0C0400u) | perm_b32(v[7], v[6], 0x04000C0Cu);
-                if (udst) udst[256 * j] = make_uint2(b0, b1);
-                if (p.factors) sdst[256 * j] = make_uint2(b0, b1);
+            for (int h = 0; h < NW / 4; ++h) {
+                const uint4 a = src[h];
+                xw[j][4 * h] = a.x; xw[j][4 * h + 1] = a.y; xw[j][4 * h + 2] = a.z; xw[j][4 * h + 3] = a.w;
             }
         }
-    };
-    if (clamp_s) code_rows(std::true_type{});
-    else code_rows(std::false_type{});
 
-    if (p.factors) {
+        // ---- stage the block in LDS for the norm pass
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint4 *dst = reinterpret_cast<uint4 *>(xs + (r0 + 16 * j) * kXPadT + 8 * cg);
+#pragma unroll
+            for (int h = 0; h < NW / 4; ++h)
+                dst[h] = make_uint4(xw[j][4 * h], xw[j][4 * h + 1], xw[j][4 * h + 2], xw[j][4 * h + 3]);
+        }
         __syncthreads();
-        block_factors_lds(reinterpret_cast<const uint8_t *>(codes_s), mh_s, sh_s, nh_s, p.factors + ob * kBlockTok);
+
+        // ---- token norms, in torch's order.  A nonfinite input makes its row's
+        // norm nonfinite; for fp16 the converse holds too (128 squares of finite
+        // fp16 values stay below 2^40), otherwise the row is scanned.
+        auto set_row = [&](int r, float n) {
+            nrm_s[r] = n;
+            const float den = clamp_eps(n);
+            const double rd = recip_rn(den);
+            den_s[r] = den;
+            if constexpr (DT != NSN_DTYPE_F16) rden_s[r] = rd;
+            rcp_s[r] = static_cast<float>(rd);   // RN32(RN64(1/den)) = RN32(1/den): 1/den is never that close to a tie
+            if (!finite(n)) {
+                bool row_bad = DT == NSN_DTYPE_F16;
+                if (!row_bad)
+                    for (int c = 0; c < kDim; ++c) row_bad |= !finite(Elem<DT>::load(xs[r * kXPadT + c]));
+                if (row_bad) bad_s = 1;
+            }
+        };
+        if constexpr (ORDER == NSN_NORM_LANES8) {
+            const int r = tid >> 2, jp = (tid & 3) * 2;
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                float q0, q1;
+                if constexpr (DT == NSN_DTYPE_F32) {
+                    const float2 q = *reinterpret_cast<const float2 *>(xs + r * kXPadT + 8 * k + jp);
+                    q0 = q.x;
+                    q1 = q.y;
+                } else {
+                    const uint32_t q = *reinterpret_cast<const uint32_t *>(xs + r * kXPadT + 8 * k + jp);
+                    q0 = Elem<DT>::load(static_cast<uint16_t>(q & 0xffffu));
+                    q1 = Elem<DT>::load(static_cast<uint16_t>(q >> 16));
+                }
+                a0 = __builtin_fmaf(q0, q0, a0);
+                a1 = __builtin_fmaf(q1, q1, a1);
+            }
+            // the row's 4 threads are one quad of lanes: lane 0 gathers lanes 1..3
+            const float b0 = dpp_f32<0xF9>(a0), b1 = dpp_f32<0xF9>(a1);   // quad_perm [1,2,3,3]
+            const float c0 = dpp_f32<0xFE>(a0), c1 = dpp_f32<0xFE>(a1);   // quad_perm [2,3,3,3]
+            const float d0 = dpp_f32<0xFF>(a0), d1 = dpp_f32<0xFF>(a1);   // quad_perm [3,3,3,3]
+            if ((tid & 3) == 0) {
+                const float acc[8] = {a0, a1, b0, b1, c0, c1, d0, d1};
+                set_row(r, sqrt_rn(lane8_sum(acc)));
+            }
+        } else {
+            if (tid < kBlockTok) {
+                float s = 0.f;
+                for (int c = 0; c < kDim; ++c) {
+                    const float q = Elem<DT>::load(xs[tid * kXPadT + c]);
+                    s = __builtin_fmaf(q, q, s);
+                }
+                set_row(tid, sqrt_rn(s));
+            }
+        }
+        __syncthreads();
+
+        // ---- directions d = x / max(n, eps), and the thread's min / max per channel
+        float d[4][8];
+        const float neg0 = keep_f32(-0.f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = r0 + 16 * j;
+            if constexpr (DT == NSN_DTYPE_F16) {
+                const float dn = den_s[r], rc = rcp_s[r];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t w = xw[j][e >> 1];
+                    d[j][e] = div_f16_markstein((e & 1) ? half_hi(w) : half_lo(w), dn, rc, neg0);
+                }
+            } else {
+                const double rd = rden_s[r];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float v;
+                    if constexpr (DT == NSN_DTYPE_F32) v = __uint_as_float(xw[j][e]);
+                    else v = __uint_as_float((e & 1) ? (xw[j][e >> 1] & 0xffff0000u) : (xw[j][e >> 1] << 16));
+                    d[j][e] = div_by_recip(v, rd);
+                }
+            }
+        }
+        {
+            float mn[8], mx[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                mn[e] = fminf(fminf(fminf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
+                mx[e] = fmaxf(fmaxf(fmaxf(d[0][e], d[1][e]), d[2][e]), d[3][e]);
+            }
+            float4 *pn = reinterpret_cast<float4 *>(&pmin[r0][8 * cg]);
+            float4 *px = reinterpret_cast<float4 *>(&pmax[r0][8 * cg]);
+            pn[0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+            pn[1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
+            px[0] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+            px[1] = make_float4(mx[4], mx[5], mx[6], mx[7]);
+        }
+        __syncthreads();
+
+        // ---- per-channel min / scale over the 16 row-group partials; fp16 metadata
+        if (tid < kDim) {
+            float lo = pmin[0][tid], hi = pmax[0][tid];
+#pragma unroll
+            for (int w = 1; w < 16; ++w) {
+                lo = fminf(lo, pmin[w][tid]);
+                hi = fmaxf(hi, pmax[w][tid]);
+            }
+            const float s = div_by_recip(hi - lo, recip_rn(kLevels));
+            m_s[tid] = lo;
+            // 1/s; for s == 0 the reference divides by 1 (every d - m is 0 then),
+            // or zeroes the codes when zero_flat_scale is set: a factor of 0
+            const double rs = (s == 0.f) ? (p.zero_flat_scale ? 0.0 : 1.0) : recip_rn(s);
+            rs_s[tid] = rs;
+            // 1/s as yh + yl: yh = RN32(1/s) (= RN32(RN64(1/s)): 1/s is never
+            // within 2^-48 of an fp32 midpoint), yl = RN32(RN64(1/s) - yh).  s == 0
+            // multiplies by 1 (or by 0 under zero_flat_scale) with yl = 0: exact.
+            const float yh = static_cast<float>(rs);
+            yh_s[tid] = yh;
+            yl_s[tid] = static_cast<float>(rs - static_cast<double>(yh));
+            // A nonzero s below 2^-64 takes the fp64 loop: the low product could
+            // leave the normal range, and with a subnormal s the quotient
+            // (d - m) / s can pass the top level (s then also underflows fp16,
+            // which the status word reports), so that loop clamps.
+            if (s != 0.f && !(s >= 5.42101086e-20f)) clamp_s = 1;
+            const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
+            p.mins[ob * kDim + tid] = hm;
+            p.scales[ob * kDim + tid] = hs;
+            mh_s[tid] = f16_bits_to_f32(hm);
+            sh_s[tid] = f16_bits_to_f32(hs);
+            if ((hm & 0x7c00u) == 0x7c00u || (hs & 0x7c00u) == 0x7c00u) status_acc |= NSN_ST_META_NONFINITE;
+            if (s != 0.f && (hs & 0x7fffu) == 0) status_acc |= NSN_ST_META_UNDERFLOW;
+        } else if (tid < kDim + kBlockTok) {
+            const int t = tid - kDim;
+            const float n = nrm_s[t];
+            const uint16_t hn = f32_to_f16_bits(n);
+            p.norms[ob * kBlockTok + t] = hn;
+            nh_s[t] = f16_bits_to_f32(hn);
+            if ((hn & 0x7c00u) == 0x7c00u) status_acc |= NSN_ST_META_NONFINITE;
+            if (n != 0.f && (hn & 0x7fffu) == 0) status_acc |= NSN_ST_META_UNDERFLOW;
+        }
+        __syncthreads();
+
+        // ---- codes clamp(round_half_even((d - m) / s), 0, 2^b - 1), packed in place.
+        // q = RN32(t / s) lies in [0, 2^b - 1 + 2^-20] for a normal s, so q + 1.5*2^23
+        // rounds it half-even to an integer held in the low mantissa bits; the
+        // shift-add of those words into the bitstream carries the constant
+        // exponent bits along, removed once per row.
+        // the lane's first output word (row r0); row r0 + 16j is 16j rows further on
+        const int k4 = cg & 3, a4 = cg >> 2;
+        uint8_t *const cbase = p.codes + ob * packed_block_bytes(BITS) + r0 * (16 * BITS);
+        uint32_t *const cdst = reinterpret_cast<uint32_t *>(
+            cbase + (BITS == 4 ? 4 * cg : (BITS == 3 ? 12 * a4 : 20 * a4) + 4 * k4));
+        constexpr int kRowStride = 16 * 16 * BITS / 4;   // dwords per 16 rows
+        uint2 *const udst = p.codes_unpacked
+            ? reinterpret_cast<uint2 *>(p.codes_unpacked + static_cast<int64_t>(f) * (kBlockTok * kDim) +
+                                        r0 * kDim + 8 * cg)
+            : nullptr;
+        float fsum[4];
+        auto code_rows = [&](auto clamp_c, auto fac_c) {
+            constexpr bool CLAMP = decltype(clamp_c)::value;
+            constexpr bool FAC = decltype(fac_c)::value;
+            // Channel-outer order: each channel's constants are loaded once and
+            // used for the thread's 4 rows; every row's bitstream word (and, at
+            // 5 bits, its fifth byte) and factor sum accumulate as it goes.
+            uint32_t lo[4], hi5[4], v6[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fsum[j] = 0.f;
+            auto channel = [&](auto e_c) {
+                constexpr int e = decltype(e_c)::value;
+                const int c = 8 * cg + e;
+                float yh = 0.f, yl = 0.f, mh = 0.f, sh = 0.f;
+                double rs = 0.0;
+                if (CLAMP) {
+                    rs = rs_s[c];
+                } else {
+                    yh = yh_s[c];
+                    yl = yl_s[c];
+                }
+                if (FAC) {
+                    mh = mh_s[c];
+                    sh = sh_s[c];
+                }
+                const float m = m_s[c];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float t = d[j][e] - m;
+                    float q;
+                    if (CLAMP) q = fminf(static_cast<float>(static_cast<double>(t) * rs), kLevels);
+                    else q = __builtin_fmaf(t, yh, t * yl);
+                    const float qm = q + kRoundMagic;
+                    const uint32_t v = __float_as_uint(qm);
+                    if (FAC) {
+                        // the reconstructed direction from the fp16 metadata: m + s * code
+                        const float dd = __builtin_fmaf(sh, qm - kRoundMagic, mh);
+                        fsum[j] = __builtin_fmaf(dd, dd, fsum[j]);
+                    }
+                    if constexpr (e == 0) lo[j] = v - magic_sum_lo<BITS>();
+                    else if constexpr (BITS * e < 32) lo[j] = lshl_add<BITS * e>(v, lo[j]);
+                    if constexpr (BITS == 5 && e == 6) v6[j] = v;
+                    if constexpr (BITS == 5 && e == 7)
+                        hi5[j] = lshl_add<3>(v, (v6[j] >> 2) - ((0x4B400000u >> 2) + (0x4B400000u << 3)));
+                }
+            };
+            // (scheduling barriers keep each channel's LDS loads next to their
+            // use: hoisted together they would hold 40 registers at once)
+            channel(std::integral_constant<int, 0>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 1>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 2>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 3>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 4>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 5>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 6>{});
+            __builtin_amdgcn_sched_barrier(0);
+            channel(std::integral_constant<int, 7>{});
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t *const dst = cdst + kRowStride * j;
+                if constexpr (BITS == 3) {
+                    // a quad of lanes holds 96 consecutive bits: lane k writes dword k < 3
+                    const uint32_t nxt = dpp_u32<0xF9>(lo[j]);   // quad_perm [1,2,3,3]: lane k+1
+                    const uint32_t D = (lo[j] >> (8 * k4)) | (nxt << (24 - 8 * k4));
+                    if (k4 < 3) *dst = D;
+                } else if constexpr (BITS == 4) {
+                    *dst = lo[j];
+                } else {
+                    // 40 bits per lane, 160 per quad: lane k writes dword k, lane 3 also dword 4
+                    const uint32_t plo = dpp_u32<0x90>(lo[j]), phi = dpp_u32<0x90>(hi5[j]);   // quad_perm [0,0,1,2]: lane k-1
+                    const uint64_t P = (static_cast<uint64_t>(phi) << 32) | plo;
+                    *dst = static_cast<uint32_t>(P >> (40 - 8 * k4)) | (lo[j] << (8 * k4));
+                    if (k4 == 3) dst[1] = (lo[j] >> 8) | (hi5[j] << 24);
+                }
+            }
+        };
+        const bool want_factors = p.factors != nullptr;
+        const bool clamp = clamp_s != 0;
+        if (udst) {
+            // u8 codes (the reference API's output), by the same rule as the packed codes below
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t w[2] = {0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int c = 8 * cg + e;
+                    const float t = d[j][e] - m_s[c];
+                    const float q = clamp ? fminf(static_cast<float>(static_cast<double>(t) * rs_s[c]), kLevels)
+                                          : __builtin_fmaf(t, yh_s[c], t * yl_s[c]);
+                    w[e >> 2] |= (__float_as_uint(q + kRoundMagic) & 0xffu) << (8 * (e & 3));
+                }
+                udst[256 * j] = make_uint2(w[0], w[1]);
+            }
+        }
+
+        if (clamp) {
+            if (want_factors) code_rows(std::true_type{}, std::true_type{});
+            else code_rows(std::true_type{}, std::false_type{});
+        } else {
+            if (want_factors) code_rows(std::false_type{}, std::true_type{});
+            else code_rows(std::false_type{}, std::false_type{});
+        }
+        if (want_factors) {
+            // Sum the 16 lanes of each row (a DPP row is one r0): after the quad
+            // butterflies, the half-row and row mirrors every lane holds the row's
+            // sum.  Lane cg = j < 4 finishes row r0 + 16j:
+            // f = n / max(sqrt(sum), 1e-12), 0 where n == 0.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float x = fsum[j];
+                x += dpp_f32<0xB1>(x);    // quad_perm [1,0,3,2]
+                x += dpp_f32<0x4E>(x);    // quad_perm [2,3,0,1]
+                x += dpp_f32<0x141>(x);   // row_half_mirror
+                x += dpp_f32<0x140>(x);   // row_mirror
+                fsum[j] = x;
+            }
+            if (cg < 4) {
+                const float sum = cg == 0 ? fsum[0] : cg == 1 ? fsum[1] : cg == 2 ? fsum[2] : fsum[3];
+                const int r = r0 + 16 * cg;
+                const float n = nh_s[r];
+                const float den = fmaxf(__builtin_sqrtf(sum), kEps);
+                p.factors[ob * kBlockTok + r] = (n == 0.f) ? 0.f : n * __builtin_amdgcn_rcpf(den);
+            }
+        }
+        if (tid == 0) {
+            if (p.headers) {
+                const uint64_t tok = static_cast<uint64_t>(p.header_start_token + static_cast<int64_t>(i) * kBlockTok);
+                uint32_t *h = reinterpret_cast<uint32_t *>(p.headers + ob * 12);
+                h[0] = static_cast<uint32_t>(tok);
+                h[1] = static_cast<uint32_t>(tok >> 32);
+                h[2] = 64u | (static_cast<uint32_t>(BITS) << 16);
+            }
+            if (bad_s) status_acc |= NSN_ST_NONFINITE_INPUT;
+        }
     }
-    if (tid == 0 && p.headers) {
-        const uint64_t tok = static_cast<uint64_t>(p.header_start_token + i * kBlockTok);
-        uint32_t *h = reinterpret_cast<uint32_t *>(p.headers + ob * 12);
-        h[0] = static_cast<uint32_t>(tok);
-        h[1] = static_cast<uint32_t>(tok >> 32);
-        h[2] = 64u | (static_cast<uint32_t>(BITS) << 16);
-    }
-    if (tid == 0 && bad_s) meta_flags |= NSN_ST_NONFINITE_INPUT;
-    raise_status(p.status, meta_flags);
+    raise_status(p.status, status_acc);
 }
 
 // =====================================================================
@@ -759,19 +847,22 @@ bool bits_ok(int bits) { return bits == 3 || bits == 4 || bits == 5; }
 bool dtype_ok(int dt) { return dt == NSN_DTYPE_F16 || dt == NSN_DTYPE_BF16 || dt == NSN_DTYPE_F32; }
 int launch_status() { return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH; }
 
+template <int DT, int BITS, int ORDER>
+void encode_launch(hipStream_t s, const EncodeParams &p) {
+    hipLaunchKernelGGL((encode_kernel<DT, BITS, ORDER>), dim3(static_cast<unsigned>(p.total)), dim3(256), 0, s, p);
+}
+
 template <int DT, int BITS>
-void encode_dispatch_order(int order, dim3 grid, hipStream_t s, const EncodeParams &p) {
-    if (order == NSN_NORM_SEQUENTIAL)
-        hipLaunchKernelGGL((encode_kernel<DT, BITS, NSN_NORM_SEQUENTIAL>), grid, dim3(256), 0, s, p);
-    else
-        hipLaunchKernelGGL((encode_kernel<DT, BITS, NSN_NORM_LANES8>), grid, dim3(256), 0, s, p);
+void encode_dispatch_order(int order, hipStream_t s, const EncodeParams &p) {
+    if (order == NSN_NORM_SEQUENTIAL) encode_launch<DT, BITS, NSN_NORM_SEQUENTIAL>(s, p);
+    else encode_launch<DT, BITS, NSN_NORM_LANES8>(s, p);
 }
 
 template <int DT>
-void encode_dispatch_bits(int bits, int order, dim3 grid, hipStream_t s, const EncodeParams &p) {
-    if (bits == 3) encode_dispatch_order<DT, 3>(order, grid, s, p);
-    else if (bits == 4) encode_dispatch_order<DT, 4>(order, grid, s, p);
-    else encode_dispatch_order<DT, 5>(order, grid, s, p);
+void encode_dispatch_bits(int bits, int order, hipStream_t s, const EncodeParams &p) {
+    if (bits == 3) encode_dispatch_order<DT, 3>(order, s, p);
+    else if (bits == 4) encode_dispatch_order<DT, 4>(order, s, p);
+    else encode_dispatch_order<DT, 5>(order, s, p);
 }
 
 template <int BITS, int OUT_DT>
@@ -822,16 +913,13 @@ int nsn_encode_blocks(const void *x, int x_dtype, int64_t n_outer, int64_t n_blo
     if (out_outer_blocks < out_block_offset + n_blocks) return NSN_EINVAL;
     const int64_t total = n_outer * n_blocks;
     if (total > 0x7fffffff) return NSN_EINVAL;
-    const int grid2d = n_outer <= 65535;
     EncodeParams p{x, n_blocks, x_outer_stride, x_token_offset, codes, norms, mins, scales, headers, factors,
                    out_outer_blocks, out_block_offset, header_start_token, codes_unpacked, status,
-                   zero_flat_scale, grid2d};
-    const dim3 grid = grid2d ? dim3(static_cast<unsigned>(n_blocks), static_cast<unsigned>(n_outer))
-                             : dim3(static_cast<unsigned>(total));
+                   zero_flat_scale, total};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (x_dtype == NSN_DTYPE_F16) encode_dispatch_bits<NSN_DTYPE_F16>(bits, norm_order, grid, s, p);
-    else if (x_dtype == NSN_DTYPE_BF16) encode_dispatch_bits<NSN_DTYPE_BF16>(bits, norm_order, grid, s, p);
-    else encode_dispatch_bits<NSN_DTYPE_F32>(bits, norm_order, grid, s, p);
+    if (x_dtype == NSN_DTYPE_F16) encode_dispatch_bits<NSN_DTYPE_F16>(bits, norm_order, s, p);
+    else if (x_dtype == NSN_DTYPE_BF16) encode_dispatch_bits<NSN_DTYPE_BF16>(bits, norm_order, s, p);
+    else encode_dispatch_bits<NSN_DTYPE_F32>(bits, norm_order, s, p);
     return launch_status();
 }
 

@@ -169,8 +169,11 @@ def test_decode_factors_vs_oracle(bits):
         q_o, n_o, m_o, s_o, _ = O.nsn_encode(x[b, :, :nb * 64].astype(np.float32).reshape(3, nb, 64, 128), bits)
         want = O.decode_factors(q_o, n_o, m_o, s_o)
         got = kv.factor[b, :, :nb].cpu().numpy()
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-        # standalone factor kernel on the same packed blocks
+        # the encoder sums in its own order (8-channel fma chains + a 16-lane
+        # tree) and finishes with the hardware root and reciprocal: a few ulps
+        assert np.array_equal(got == 0, want == 0)
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 2.0 ** -20 * np.abs(want))
+        # standalone factor kernel on the same packed blocks: the oracle's order, bitwise
         f2 = kernels.block_factors(kv.codes[b, :, :nb].contiguous(), kv.norm[b, :, :nb], kv.min[b, :, :nb],
                                    kv.scale[b, :, :nb], bits).cpu().numpy()
         assert np.array_equal(f2.view(np.uint32), want.view(np.uint32))
