@@ -712,15 +712,16 @@ def main_c4(args):
         f"{mfma:.0f} TFLOP/s = {mfma / 2500:.1%} of 2.5 PFLOP/s dense bf16")
     # the prefill kernel alone, on the last chunk of one slot (context 7680 tokens)
     qc, kc, vc = acts[-1]
-    saved = (cache.length[0], cache.compressed[0])
-    cache.length[0], cache.compressed[0] = T - ch, ((T - ch - 64) // 64) * 64   # state before the last chunk
+    saved = (list(cache.seq_length[0]), list(cache.seq_compressed[0]))
+    cache.seq_length[0] = [T - ch] * b_                             # state before the last chunk
+    cache.seq_compressed[0] = [((T - ch - 64) // 64) * 64] * b_
     for name in ("K", "V"):
         cache.side(0, name).blocks.fill_(cache.compressed[0] // 64)
     pk_ms = timed(lambda: cache.prefill(0, qc, kc, vc, check=False), 5, 2, stream)
     last_flops = 2.0 * 2 * b_ * h * ch * D * ((T - ch) + (ch + 1) / 2)
     log(f"[bench] C4 prefill kernel, last chunk (context {T - ch}): {pk_ms * 1e3:.0f} us, "
         f"{last_flops / (pk_ms * 1e-3) / 1e12:.0f} TFLOP/s")
-    cache.length[0], cache.compressed[0] = saved
+    cache.seq_length[0], cache.seq_compressed[0] = saved
     for name in ("K", "V"):
         cache.side(0, name).blocks.fill_(cache.compressed[0] // 64)
 

@@ -280,7 +280,7 @@ class PackedKVCache(Cache):
                                         self.status.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_rope_append")
         if not self.graph_mode:
-            st.length[slot] += 1
+            st.advance(slot)
         return q_out
 
     def append_for_attention(self, slot, key, value, kwargs=None):
@@ -616,7 +616,7 @@ class DecodeGraph:
         finally:
             self.cache.graph_mode = False
         for s in range(st.slots):
-            st.length[s] += 1
+            st.advance(s)
             self.cache.connection_calls[s] += 1
         before = st.compressed[0]
         try:

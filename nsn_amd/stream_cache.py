@@ -20,9 +20,14 @@ The policy is the reference's:
 
 so after either call the tail holds 64..127 tokens (fewer only for short
 sequences).  Headers carry the token offset of each block ('<QHBB', as
-``encode_group`` writes them, ``:31-37``).  Every sequence of the batch has
-the same length (the reference runs batch 1; the C4 workload is uniform), so
-lengths are host integers and nothing here synchronises with the device.
+``encode_group`` writes them, ``:31-37``).
+
+Sequences of a batch may have different lengths (the ragged decode batch of
+the C2 workload): every sequence has its own length and compressed prefix,
+the policy applies per sequence, and appends may carry a per-sequence token
+count.  Lengths are host integers, so nothing here synchronises with the
+device; while every sequence of a slot has the same state, each operation is
+one launch for the whole batch, otherwise one per sequence that changes.
 """
 from __future__ import annotations
 
@@ -61,6 +66,11 @@ class StreamingKVCache:
     prefill chunk, or 1 per decode step).  ``dtype`` is the tail's dtype
     (fp16 or bf16; both kernels read either); appended K/V of another dtype
     are converted to it.
+
+    ``seq_length[slot]`` / ``seq_compressed[slot]`` hold each sequence's token
+    count and packed prefix; ``length[slot]`` / ``compressed[slot]`` are the
+    longest sequence's length and the shortest packed prefix (the common
+    values when the batch is uniform).
     """
 
     def __init__(self, slots, batch, heads, max_tokens, *, bits=3, dtype=torch.float16, max_append=512,
@@ -87,8 +97,8 @@ class StreamingKVCache:
                     bits=bits)
                 hdr = torch.zeros((batch, heads, self.block_cap, 12), dtype=torch.uint8, device=device)
                 self._sides[(s, name)] = _Side(kv, hdr)
-        self.length = [0] * slots        # tokens held per slot
-        self.compressed = [0] * slots    # of which packed
+        self.seq_length = [[0] * batch for _ in range(slots)]       # tokens held per slot and sequence
+        self.seq_compressed = [[0] * batch for _ in range(slots)]   # of which packed
         self._len_dev = {}               # cached int32 length tensors
         self.status = _dev.new_status(device)
         self.encoded_blocks = [0] * slots
@@ -100,82 +110,159 @@ class StreamingKVCache:
     def headers(self, slot, name) -> torch.Tensor:
         return self._sides[(slot, name)].headers
 
+    @property
+    def length(self):
+        """Per slot: the longest sequence's token count."""
+        return [max(x) for x in self.seq_length]
+
+    @property
+    def compressed(self):
+        """Per slot: the shortest packed prefix."""
+        return [min(x) for x in self.seq_compressed]
+
+    def uniform(self, slot) -> bool:
+        """Every sequence of the slot holds the same tokens and packed prefix."""
+        L, C = self.seq_length[slot], self.seq_compressed[slot]
+        return min(L) == max(L) and min(C) == max(C)
+
     def lengths(self, slot) -> torch.Tensor:
-        """int32 [B] device tensor of the slot's length (every sequence equal)."""
-        return self.length_tensor(self.length[slot])
+        """int32 [B] device tensor of the slot's per-sequence lengths."""
+        return self.length_tensor(self.seq_length[slot])
 
     def length_tensor(self, L) -> torch.Tensor:
-        """int32 [B] device tensor filled with L (made once per L and kept)."""
-        t = self._len_dev.get(L)
+        """int32 [B] device tensor of the lengths L (an int for every sequence, or
+        one per sequence), made once per distinct value and kept."""
+        key = tuple(L) if isinstance(L, (list, tuple)) else (int(L),) * self.batch
+        t = self._len_dev.get(key)
         if t is None:
-            t = torch.full((self.batch,), L, dtype=torch.int32, device=self.device)
-            self._len_dev[L] = t
+            t = torch.tensor(key, dtype=torch.int32).to(self.device)
+            self._len_dev[key] = t
         return t
 
     def tail_len(self, slot):
-        return self.length[slot] - self.compressed[slot]
+        """Tail tokens of the slot (the batch must be uniform)."""
+        if not self.uniform(slot):
+            raise IntegrityError("Ragged slot: use seq_tail_len")
+        return self.seq_length[slot][0] - self.seq_compressed[slot][0]
+
+    def seq_tail_len(self, slot, b):
+        return self.seq_length[slot][b] - self.seq_compressed[slot][b]
+
+    def advance(self, slot, n=1):
+        """Count n more tokens in every sequence of the slot: the host side of
+        an append its caller made on the device (a device-position tail
+        append, replayed from a HIP graph)."""
+        L = self.seq_length[slot]
+        for b in range(self.batch):
+            L[b] += n
 
     # ------------------------------------------------------------------ updates
-    def append(self, slot, k, v):
-        """Append k, v [B, H, n, 128] to the slot's tail (converted to the tail dtype if needed)."""
+    def append(self, slot, k, v, counts=None):
+        """Append k, v [B, H, n, 128] to the slot's tails (converted to the tail
+        dtype if needed).  ``counts`` (one int per sequence, each <= n) appends
+        only sequence b's first counts[b] tokens; default n for every sequence."""
         require(k.shape == v.shape and k.ndim == 4 and tuple(k.shape[:2]) == (self.batch, self.heads)
                 and k.shape[3] == DIM, "Append shape")
         n = k.shape[2]
-        t0 = self.tail_len(slot)
-        if t0 + n > self.tail_cap:
-            raise IntegrityError("Tail overflow: compress before appending more tokens")
-        if self.length[slot] + n > self.block_cap * BLOCK + self.tail_cap:
-            raise IntegrityError("Cache capacity exceeded")
+        counts = [n] * self.batch if counts is None else [int(c) for c in counts]
+        require(len(counts) == self.batch and all(0 <= c <= n for c in counts), "Append counts")
+        L, C = self.seq_length[slot], self.seq_compressed[slot]
+        for b in range(self.batch):
+            if L[b] - C[b] + counts[b] > self.tail_cap:
+                raise IntegrityError("Tail overflow: compress before appending more tokens")
+            if L[b] + counts[b] > self.block_cap * BLOCK + self.tail_cap:
+                raise IntegrityError("Cache capacity exceeded")
         require(k.dtype in (torch.float16, torch.bfloat16, torch.float32) and v.dtype == k.dtype, "Append dtype")
         if k.dtype != self.dtype:
             k, v = k.to(self.dtype), v.to(self.dtype)
         k, v = k.contiguous(), v.contiguous()
         kt, vt = self._sides[(slot, "K")].kv.tail, self._sides[(slot, "V")].kv.tail
-        rc = _lib.lib().nsn_tail_append(k.data_ptr(), v.data_ptr(), self.batch * self.heads, n, n, kt.data_ptr(),
-                                        vt.data_ptr(), self.tail_cap, t0, _dev.dtype_code(self.dtype), _dev.stream())
-        _lib.check(rc, "nsn_tail_append")
-        self.length[slot] += n
+        lib = _lib.lib()
+        dt = _dev.dtype_code(self.dtype)
+        offs = [L[b] - C[b] for b in range(self.batch)]
+        if len(set(offs)) == 1 and len(set(counts)) == 1:
+            if counts[0]:
+                rc = lib.nsn_tail_append(k.data_ptr(), v.data_ptr(), self.batch * self.heads, counts[0], n,
+                                         kt.data_ptr(), vt.data_ptr(), self.tail_cap, offs[0], dt, _dev.stream())
+                _lib.check(rc, "nsn_tail_append")
+        else:
+            for b in range(self.batch):   # one launch per sequence: its own offset and count
+                if counts[b]:
+                    rc = lib.nsn_tail_append(k[b].data_ptr(), v[b].data_ptr(), self.heads, counts[b], n,
+                                             kt[b].data_ptr(), vt[b].data_ptr(), self.tail_cap, offs[b], dt,
+                                             _dev.stream())
+                    _lib.check(rc, "nsn_tail_append")
+        for b in range(self.batch):
+            L[b] += counts[b]
 
     def compress_to(self, slot, target):
         """Encode tail tokens up to absolute position `target` (a multiple of
-        64) into packed blocks, in place; the tail keeps the rest."""
-        start = self.compressed[slot]
-        if not (target >= start and (target - start) % BLOCK == 0):
-            raise IntegrityError("Block overlap/ordering")
-        if target == start:
+        64; an int for every sequence or one per sequence) into packed
+        blocks, in place; the tails keep the rest."""
+        targets = [int(target)] * self.batch if not isinstance(target, (list, tuple)) else [int(t) for t in target]
+        require(len(targets) == self.batch, "Compress targets")
+        L, C = self.seq_length[slot], self.seq_compressed[slot]
+        for b in range(self.batch):
+            start, tgt = C[b], targets[b]
+            if not (tgt >= start and (tgt - start) % BLOCK == 0):
+                raise IntegrityError("Block overlap/ordering")
+            if tgt == start:
+                continue
+            if L[b] < tgt + BLOCK:
+                raise IntegrityError("Tail/compressed divergence")
+            if tgt // BLOCK > self.block_cap:
+                raise IntegrityError("Cache capacity exceeded")
+        moving = [b for b in range(self.batch) if targets[b] != C[b]]
+        if not moving:
             return
-        if self.length[slot] < target + BLOCK:
-            raise IntegrityError("Tail/compressed divergence")
+        if len(moving) == self.batch and len(set(C)) == 1 and len(set(targets)) == 1 and len(set(L)) == 1:
+            self._encode_rows(slot, None, C[0], targets[0], L[0])   # the whole batch in one launch per side
+        else:
+            for b in moving:
+                self._encode_rows(slot, b, C[b], targets[b], L[b])
+        # blocks added per sequence (the most any sequence gained in this call)
+        self.encoded_blocks[slot] += max((targets[b] - C[b]) // BLOCK for b in moving)
+        for b in moving:
+            C[b] = targets[b]
+        nblocks = [c // BLOCK for c in C]
+        for name in ("K", "V"):
+            kv = self._sides[(slot, name)].kv
+            if len(set(nblocks)) == 1:
+                kv.blocks.fill_(nblocks[0])
+            else:
+                kv.blocks.copy_(torch.tensor(nblocks, dtype=torch.int32))
+
+    def _encode_rows(self, slot, b, start, target, length):
+        """Encode tokens [start, target) of sequence b (or of every sequence,
+        b None) from the tail into blocks start/64 .., then re-base the tail."""
+        lib = _lib.lib()
         n = target - start
         nb = n // BLOCK
-        if target // BLOCK > self.block_cap:
-            raise IntegrityError("Cache capacity exceeded")
-        lib = _lib.lib()
-        rest = self.length[slot] - target
+        rest = length - target
+        rows = self.heads if b is not None else self.batch * self.heads
+        sel = (lambda t: t[b]) if b is not None else (lambda t: t)
         for name in ("K", "V"):
             sd = self._sides[(slot, name)]
             kv = sd.kv
             rc = lib.nsn_encode_blocks(
-                kv.tail.data_ptr(), _dev.dtype_code(self.dtype), self.batch * self.heads, nb,
+                sel(kv.tail).data_ptr(), _dev.dtype_code(self.dtype), rows, nb,
                 self.tail_cap * DIM, 0, self.bits, _lib.NORM_LANES8, 1,
-                kv.codes.data_ptr(), kv.norm.data_ptr(), kv.min.data_ptr(), kv.scale.data_ptr(),
-                sd.headers.data_ptr(), kv.factor.data_ptr(), self.block_cap, start // BLOCK, start,
-                None, self.status.data_ptr(), _dev.stream())
+                sel(kv.codes).data_ptr(), sel(kv.norm).data_ptr(), sel(kv.min).data_ptr(),
+                sel(kv.scale).data_ptr(), sel(sd.headers).data_ptr(), sel(kv.factor).data_ptr(), self.block_cap,
+                start // BLOCK, start, None, self.status.data_ptr(), _dev.stream())
             _lib.check(rc, "nsn_encode_blocks")
             # re-base the surviving tail tokens (source and target may overlap)
-            src = kv.tail[:, :, n:n + rest]
-            kv.tail[:, :, :rest] = src.clone() if rest > n else src
-            kv.blocks.fill_(target // BLOCK)
-        self.compressed[slot] = target
-        self.encoded_blocks[slot] += nb
+            tail = sel(kv.tail)
+            src = tail[..., n:n + rest, :]
+            tail[..., :rest, :] = src.clone() if rest > n else src
 
     def post_prefill(self):
         for s in range(self.slots):
-            self.compress_to(s, prefill_target(self.length[s]))
+            self.compress_to(s, [prefill_target(L) for L in self.seq_length[s]])
 
     def post_decode(self):
         for s in range(self.slots):
-            self.compress_to(s, decode_target(self.length[s], self.compressed[s]))
+            self.compress_to(s, [decode_target(L, C) for L, C in zip(self.seq_length[s], self.seq_compressed[s])])
 
     def check_status(self):
         """Raise if any compression flagged nonfinite input or fp16 metadata trouble (syncs)."""
@@ -186,15 +273,16 @@ class StreamingKVCache:
 
     # ------------------------------------------------------------------ attention
     def decode(self, slot, q, **kw):
-        """Decode attention of q [B, Hq, 128] over the slot (packed blocks + tail)."""
-        L = self.length[slot]
+        """Decode attention of q [B, Hq, 128] over the slot (packed blocks + tail;
+        each sequence over its own length)."""
+        L = max(self.seq_length[slot])
         return _attn().decode_attention(q, self.side(slot, "K"), self.side(slot, "V"), self.lengths(slot),
                                         max_seq_len=L, **kw)
 
     def prefill(self, slot, q, k_chunk, v_chunk, **kw):
         """Chunked-prefill attention of q [B, Hq, n, 128] over the slot's
         context plus the chunk's own K/V (not yet appended)."""
-        has_ctx = self.length[slot] > 0
+        has_ctx = max(self.seq_length[slot]) > 0
         return _attn().prefill_attention(q, self.side(slot, "K") if has_ctx else None,
                                          self.side(slot, "V") if has_ctx else None, self.lengths(slot),
                                          k_chunk, v_chunk, **kw)

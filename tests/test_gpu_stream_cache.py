@@ -107,3 +107,100 @@ def test_stream_cache_prefill_then_decode():
     check_blocks(cache, slot, k, v)
     assert cache.compressed[slot] == 256 and cache.encoded_blocks[slot] == 4
     cache.check_status()
+
+
+def check_blocks_ragged(cache, slot, hist_k, hist_v):
+    """Per sequence: packed prefix == oracle encode, headers, block count, tail."""
+    for name, x in (("K", hist_k), ("V", hist_v)):
+        side = cache.side(slot, name)
+        blocks = side.blocks.cpu().numpy()
+        for b in range(cache.batch):
+            C, L = cache.seq_compressed[slot][b], cache.seq_length[slot][b]
+            nb = C // 64
+            assert blocks[b] == nb
+            H = x.shape[1]
+            if nb:
+                q, n, m, s, err = O.nsn_encode(x[b, :, :C].astype(np.float32).reshape(H, nb, 64, 128), 3)
+                assert err == 0
+                codes = O.pack_codes(q.reshape(H * nb, -1), 3).reshape(H, nb, -1)
+                assert np.array_equal(side.codes[b, :, :nb].cpu().numpy(), codes)
+                assert np.array_equal(side.norm[b, :, :nb].cpu().numpy().view(np.uint16), n.reshape(H, nb, 64))
+                assert np.array_equal(side.min[b, :, :nb].cpu().numpy().view(np.uint16), m.reshape(H, nb, 128))
+                assert np.array_equal(side.scale[b, :, :nb].cpu().numpy().view(np.uint16), s.reshape(H, nb, 128))
+                hdr = cache.headers(slot, name)[b, :, :nb].cpu().numpy()
+                tok = hdr[..., :8].copy().view(np.uint64)[..., 0]
+                assert np.array_equal(tok, np.broadcast_to(64 * np.arange(nb, dtype=np.uint64), (H, nb)))
+            tail = side.tail[b, :, :L - C].cpu().numpy()
+            assert np.array_equal(tail.view(np.uint16), x[b, :, C:L].view(np.uint16))
+
+
+def test_stream_cache_ragged_lengths():
+    """A ragged batch (prompts of 300, 171 and 69 tokens) streams through one
+    slot: chunked prefill with per-sequence token counts, then 140 decode
+    steps of one token each with the compression policy applied per sequence
+    (each sequence compresses at its own steps); every packed block and tail
+    checked against the oracle's encode, every attention output against
+    float64 attention over that sequence's own restored history."""
+    rng = np.random.default_rng(37)
+    B, H, chunk, steps = 3, 2, 128, 140
+    prompt = [300, 171, 69]
+    T = max(prompt) + steps
+    k = normal_tokens(rng, (B, H), T)
+    v = normal_tokens(rng, (B, H), T)
+    cache = StreamingKVCache(1, B, H, 1024, bits=3, dtype=torch.float16, max_append=chunk, device=DEV)
+    slot = 0
+
+    def hist(x, b, C, L):
+        return np.concatenate([restore_ctx(x[b], C, 3, torch.float16)[:, :C], x[b][:, C:L].astype(np.float32)], 1)
+
+    for c0 in range(0, max(prompt), chunk):
+        counts = [max(0, min(chunk, P - c0)) for P in prompt]
+        n = max(counts)
+        q = rng.standard_normal((B, H, n, 128)).astype(np.float16)
+        kc = torch.from_numpy(k[:, :, c0:c0 + n].copy()).to(DEV)
+        vc = torch.from_numpy(v[:, :, c0:c0 + n].copy()).to(DEV)
+        out = cache.prefill(slot, torch.from_numpy(q).to(DEV), kc, vc).float().cpu().numpy()
+        for b in range(B):
+            nb_q = counts[b]
+            if not nb_q:
+                continue
+            C, L = cache.seq_compressed[slot][b], cache.seq_length[slot][b]
+            assert L == c0
+            ref = O.prefill_attention64(q[b, :, :nb_q].astype(np.float32), hist(k, b, C, L), hist(v, b, C, L),
+                                        k[b][:, c0:c0 + nb_q].astype(np.float32),
+                                        v[b][:, c0:c0 + nb_q].astype(np.float32))
+            ok, err = within(out[b, :, :nb_q], ref, 2.0 ** -11)
+            assert ok, (c0, b, err)
+        cache.append(slot, kc, vc, counts=counts)
+        cache.compress_to(slot, [max(C, (max(0, L - 64) // 64) * 64)
+                                 for C, L in zip(cache.seq_compressed[slot], cache.seq_length[slot])])
+        check_blocks_ragged(cache, slot, k, v)
+    cache.post_prefill()
+    assert cache.seq_length[slot] == prompt
+    assert cache.seq_compressed[slot] == [192, 64, 0]
+    assert not cache.uniform(slot)
+    compressions = set()
+    for i in range(steps):
+        pos = list(cache.seq_length[slot])
+        kt = torch.from_numpy(np.stack([k[b, :, pos[b]:pos[b] + 1] for b in range(B)])).to(DEV)
+        vt = torch.from_numpy(np.stack([v[b, :, pos[b]:pos[b] + 1] for b in range(B)])).to(DEV)
+        cache.append(slot, kt, vt)
+        q = rng.standard_normal((B, 2 * H, 128)).astype(np.float32)
+        qb = torch.from_numpy(q).to(torch.bfloat16)
+        _, ctx = cache.decode(slot, qb.to(DEV), kernel="fast")
+        for b in range(B):
+            C, L = cache.seq_compressed[slot][b], cache.seq_length[slot][b]
+            ref, _ = O.decode_attention64(qb[b:b + 1].float().numpy(), hist(k, b, C, L)[None], hist(v, b, C, L)[None])
+            ok, err = within(ctx[b].cpu().numpy(), ref[0], 0.0)
+            assert ok, (i, b, err)
+        before = list(cache.seq_compressed[slot])
+        cache.post_decode()
+        compressions |= {(b, i) for b in range(B) if cache.seq_compressed[slot][b] != before[b]}
+        for b in range(B):
+            assert 64 <= cache.seq_tail_len(slot, b) < 128
+    check_blocks_ragged(cache, slot, k, v)
+    assert cache.seq_length[slot] == [P + steps for P in prompt]
+    # each sequence compressed at its own steps (a uniform batch would share them)
+    steps_of = [sorted(i for bb, i in compressions if bb == b) for b in range(B)]
+    assert all(steps_of) and len({tuple(x) for x in steps_of}) == B
+    cache.check_status()
