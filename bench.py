@@ -1140,28 +1140,31 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
-    # the same steps again with HIP events around each kernel on the launch
-    # stream: the split kernel's and the merge's own durations, in the same
-    # warm state (each step's events bracket its two kernels)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    for a_, b_, c_ in ev:
-        a_.record(stream)
-        split_kernel()
-        b_.record(stream)
-        merge_kernel()
-        c_.record(stream)
-    torch.cuda.synchronize()
-    split_ts = sorted(a_.elapsed_time(b_) for a_, b_, _ in ev)
-    merge_ts = sorted(b_.elapsed_time(c_) for _, b_, c_ in ev)
-    ms_split = sum(split_ts) / len(split_ts)
-    ms_merge = sum(merge_ts) / len(merge_ts)
+    # Per-kernel durations in the same warm state: rounds of back-to-back
+    # batches -- steps, split-only launches, merge-only launches -- each batch
+    # bracketed by HIP events on the launch stream.  A batch of split launches
+    # has no merge between them, so its per-launch time is the split kernel's
+    # own duration plus the dispatch gap, and the interleaving keeps all three
+    # at one clock.
+    rounds = 5
+    per = max(4, args.steps // rounds)
+    round_step, round_split, round_merge = [], [], []
+    for _ in range(rounds):
+        round_step.append(timed(step, per, 0, stream))
+        round_split.append(timed(split_kernel, per, 0, stream))
+        round_merge.append(timed(merge_kernel, per, 0, stream))
+    split_ts = sorted(round_split)
+    ms_split = sum(round_split) / rounds
+    ms_merge = sum(round_merge) / rounds
+    ms_step_rounds = sum(round_step) / rounds
     st_val = _dev.read_status(status)
     assert st_val == 0, f"status word {st_val:#x}"
     nbytes = algorithmic_bytes(lengths, 3)
     achieved = nbytes / (ms_split * 1e-3) / 1e9
-    log(f"[bench] step {ms_step * 1e3:.1f} us; per kernel: split {ms_split * 1e3:.1f} us (median "
-        f"{split_ts[len(split_ts) // 2] * 1e3:.1f}), merge {ms_merge * 1e3:.1f} us; "
-        f"{nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    log(f"[bench] step {ms_step * 1e3:.1f} us; interleaved rounds: step {ms_step_rounds * 1e3:.1f} us, "
+        f"split {ms_split * 1e3:.1f} us (median of rounds {split_ts[len(split_ts) // 2] * 1e3:.1f}), "
+        f"merge {ms_merge * 1e3:.1f} us; {nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s "
+        f"({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     # parity spot check of this step against the exact-order kernel (untimed)
     if args.kernel != "reference":
@@ -1189,7 +1192,9 @@ def main():
                      "traffic": measured_traffic() if args.kernel == "fast" else None,
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
                      "kernel_us": round(ms_split * 1e3, 2), "kernel_us_median": round(split_ts[len(split_ts) // 2] * 1e3, 2),
-                     "merge_us": round(ms_merge * 1e3, 2)},
+                     "merge_us": round(ms_merge * 1e3, 2), "step_us_same_rounds": round(ms_step_rounds * 1e3, 2),
+                     "timing": f"{rounds} interleaved rounds of {per} steps / {per} split-only / {per} merge-only "
+                               "launches, HIP events around each batch on the launch stream"},
         "encode_roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(enc_gbs / HBM_PEAK_GBS, 4), "traffic": measured_encode_traffic(),
                             "kernel": "encode (C2 K, fp16 -> INT3 + fp16 metadata + fp32 decode factors)",
