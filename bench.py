@@ -19,6 +19,8 @@ Profiling (the commands behind the committed summaries under profiles/):
     rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --profile
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o fetch -- python3 bench.py --profile
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o write -- python3 bench.py --profile
+    rocprofv3 --pmc SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_INSTS_SALU SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv -d OUT/sq1 -o sq1 -- python3 bench.py --profile
+    rocprofv3 --pmc SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS SQ_VALU_MFMA_BUSY_CYCLES SQ_INST_LEVEL_VMEM SQ_LEVEL_WAVES --output-format csv -d OUT/sq2 -o sq2 -- python3 bench.py --profile
     python3 bench.py --summarize OUT      # writes profiles/attn_fast_c2.{md,json}, profiles/encode_c2.{md,json}
 
 ``--profile`` runs one 1 GiB device-to-device copy (the counter calibration:
@@ -209,7 +211,7 @@ PROFILE_JSON = ROOT / "profiles" / "attn_fast_c2.json"
 PROFILE_MD = ROOT / "profiles" / "attn_fast_c2.md"
 FAST_SOURCE = ROOT / "nsn_amd" / "csrc" / "nsn_fast.hip"
 CALIB_BYTES = 1 << 30
-SPLIT_KERNEL = "nsn::fast::attn_fast_kernel<3, 1, false, 4>"
+SPLIT_KERNEL = "nsn::fast::attn_fast_kernel<3, 1, false, 4, false>"
 MERGE_KERNEL = "nsn::attn_merge_kernel<1>"
 CALIB_KERNEL = "__amd_rocclr_copyBuffer"
 PROFILE_STEPS = 100   # decode steps of `--profile` (the first launch runs cold)
@@ -254,6 +256,68 @@ def _counter(dirname, counter):
             out["calib"].append(val)
     out["encode"] = [v for _, v in sorted(enc)[:ENCODE_PROFILE_STEPS]]
     return out
+
+
+SQ_NOTES = {
+    "SQ_WAVES": "waves",
+    "SQ_INSTS_VALU": "VALU instructions (MFMA included)",
+    "SQ_INSTS_MFMA": "MFMA instructions",
+    "SQ_INSTS_SALU": "SALU instructions",
+    "SQ_INSTS_LDS": "LDS instructions",
+    "SQ_WAVE_CYCLES": "wave-lifetime quad-cycles (sum over waves)",
+    "SQ_ACTIVE_INST_VALU": "VALU-issue quad-cycles (sum over waves)",
+    "SQ_ACTIVE_INST_ANY": "any-issue quad-cycles (sum over waves)",
+    "SQ_WAIT_ANY": "quad-cycles waves wait on anything (counters, dependencies)",
+    "SQ_WAIT_INST_ANY": "quad-cycles waves wait for an instruction dependency",
+    "SQ_ACTIVE_INST_LDS": "LDS-issue quad-cycles",
+    "SQ_LDS_BANK_CONFLICT": "LDS bank-conflict cycles (sum over CUs)",
+    "SQ_VALU_MFMA_BUSY_CYCLES": "MFMA-busy cycles (sum over SIMDs)",
+    "SQ_BUSY_CYCLES": "SQ-busy cycles (sum over SEs)",
+    "GRBM_GUI_ACTIVE": "GPU-active cycles (sum over the 8 XCDs)",
+}
+
+
+def _sq(d, kernel, first=None):
+    """Per-dispatch SQ/GRBM counter readings of one kernel from the sq1/sq2
+    passes (median over its dispatches; `first` keeps only the first ones)."""
+    vals = {}
+    for sub in ("sq1", "sq2"):
+        if not (Path(d) / sub).exists():
+            return {}
+        per = {}
+        for r in _rows((Path(d) / sub, "**/*counter_collection.csv")):
+            if kernel in r["Kernel_Name"]:
+                per.setdefault(r["Counter_Name"], []).append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+        for c, v in per.items():
+            xs = sorted(x for _, x in (sorted(v)[:first] if first else v))
+            vals[c] = xs[len(xs) // 2]
+    return vals
+
+
+def _sq_lines(sq, blocks_per_wave=None):
+    """Markdown rows of the counters and the ratios quoted in the notes."""
+    if not sq:
+        return []
+    L = ["| counter | median per dispatch | meaning |", "|---|---|---|"]
+    for c in SQ_NOTES:
+        if c in sq:
+            L.append(f"| {c} | {sq[c]:.4g} | {SQ_NOTES[c]} |")
+    w = sq.get("SQ_WAVES", 0)
+    if w:
+        L += ["", "Derived (per wave; quad-cycles x 4 = cycles):", ""]
+        valu = sq["SQ_INSTS_VALU"] - sq.get("SQ_INSTS_MFMA", 0)
+        L.append(f"- VALU (without MFMA) {valu / w:.0f}, MFMA {sq.get('SQ_INSTS_MFMA', 0) / w:.0f}, "
+                 f"SALU {sq['SQ_INSTS_SALU'] / w:.0f}, LDS {sq['SQ_INSTS_LDS'] / w:.0f} instructions per wave"
+                 + (f" ({valu / w / blocks_per_wave:.0f} / {sq.get('SQ_INSTS_MFMA', 0) / w / blocks_per_wave:.0f} / "
+                    f"{sq['SQ_INSTS_SALU'] / w / blocks_per_wave:.0f} / {sq['SQ_INSTS_LDS'] / w / blocks_per_wave:.0f} "
+                    f"per 64-token block)" if blocks_per_wave else "") + ";")
+        L.append(f"- wave lifetime {4 * sq['SQ_WAVE_CYCLES'] / w:.0f} cycles; of it VALU issue "
+                 f"{sq['SQ_ACTIVE_INST_VALU'] / sq['SQ_WAVE_CYCLES']:.1%}, any issue "
+                 f"{sq['SQ_ACTIVE_INST_ANY'] / sq['SQ_WAVE_CYCLES']:.1%}, waiting "
+                 f"{sq['SQ_WAIT_ANY'] / sq['SQ_WAVE_CYCLES']:.1%};")
+        if "GRBM_GUI_ACTIVE" in sq:
+            L.append(f"- GPU-active cycles per XCD {sq['GRBM_GUI_ACTIVE'] / 8:.0f}.")
+    return L
 
 
 def summarize(d):
@@ -312,10 +376,19 @@ def summarize(d):
           f"-> {alg / split_avg / 1e3:.0f} GB/s algorithmic, median {split_med:.1f} us "
           f"-> {alg / split_med / 1e3:.0f} GB/s (the mean includes the cold first launch).", "",
           f"Kernel source sha256: `{fig['source_sha256']}`", ""]
+    sq = _sq(d, SPLIT_KERNEL)
+    if sq:
+        L += ["## SQ counters (rocprofv3 --pmc, the sq1 and sq2 passes above)", ""]
+        L += _sq_lines(sq, blocks_per_wave=sum((x + 63) // 64 for x in lens) * HKV / sq["SQ_WAVES"])
+        L += ["", f"With 2 waves per SIMD the SIMD's VALU port is busy about twice the per-wave VALU-issue "
+              f"share while the waves live; the mean wave lifetime ({4 * sq['SQ_WAVE_CYCLES'] / sq['SQ_WAVES'] / (sq['GRBM_GUI_ACTIVE'] / 8) :.0%} of the "
+              f"dispatch's GPU-active cycles) shows the end-of-kernel imbalance.", ""]
     PROFILE_MD.write_text("\n".join(L))
     print("\n".join(L))
     if fetch["encode"] and write["encode"]:
         summarize_encode(d, fetch, write, f_scale, w_scale)
+    elif fetch["encode"] or write["encode"]:
+        raise SystemExit("encode counters incomplete")
 
 
 def summarize_encode(d, fetch, write, f_scale, w_scale):
@@ -332,30 +405,33 @@ def summarize_encode(d, fetch, write, f_scale, w_scale):
     rd = mean(fetch["encode"]) * 1024 * f_scale
     wr = mean(write["encode"]) * 1024 * w_scale
     fig = {"kernel": ENCODE_KERNEL, "source_sha256": hashlib.sha256(CODEC_SOURCE.read_bytes()).hexdigest(),
-           "workload": "C2 K, 128 rows x 512 blocks, fp16 in, 3-bit out, no decode factors",
+           "workload": "C2 K, 128 rows x 512 blocks, fp16 in, 3-bit codes + fp16 metadata + fp32 decode factors out",
            "token_heads": tokens, "median_us": round(med, 2), "mean_us": round(avg, 2), "min_us": round(durs[0], 2),
            "read_bytes": int(rd), "write_bytes": int(wr), "traffic": int(rd + wr), "algorithmic_bytes": alg}
     ENCODE_JSON.write_text(json.dumps(fig, indent=1) + "\n")
     L = ["# encode_kernel on C2 (all 64-token blocks of K: 128 rows x 512 blocks, fp16 -> INT3)", "",
          "Same rocprofv3 runs as profiles/attn_fast_c2.md (commands there): `bench.py --profile` runs "
-         f"{ENCODE_PROFILE_STEPS} encode launches of the C2 bench's encode (no decode factors, no headers) "
-         "right after the calibration copy, before it packs the decode cache.", "",
+         f"{ENCODE_PROFILE_STEPS} encode launches of the C2 bench's encode (codes, fp16 metadata and the "
+         "fp32 decode factors; no headers) right after the calibration copy, before it packs the decode "
+         "cache.", "",
          "| item | value |", "|---|---|",
          f"| launches | {len(durs)} |",
          f"| duration, median / mean / min | {med:.1f} / {avg:.1f} / {durs[0]:.1f} us |",
          f"| durations in launch order | {', '.join(f'{x:.0f}' for x in seq)} us |",
          f"| token-heads per launch | {tokens} |",
-         f"| algorithmic bytes (256 in + 58 out per token-head) | {alg / 1e6:.1f} MB |",
+         f"| algorithmic bytes (256 in + 58 out per token-head; the 4-byte factors are not counted) | {alg / 1e6:.1f} MB |",
          f"| FETCH_SIZE / WRITE_SIZE per launch | {mean(fetch['encode']):.0f} / {mean(write['encode']):.0f} KiB |",
          f"| HBM traffic (scaled by the calibration copy) | {rd / 1e6:.1f} MB read + {wr / 1e6:.1f} MB written = "
          f"**{(rd + wr) / 1e6:.1f} MB** (ratio {(rd + wr) / alg:.3f} to algorithmic) |",
          f"| rate | {tokens / med / 1e3:.2f} G token-heads/s = {alg / med / 1e3:.0f} GB/s algorithmic "
          f"({alg / med / 1e3 / HBM_PEAK_GBS * 100:.1f} % of 8 TB/s) at the median; "
          f"{alg / avg / 1e3:.0f} GB/s at the mean |", "",
-         "The kernel is bound by VALU issue (about 530 VALU instructions per wave, 92 % VALU-busy "
-         "under SQ counters); back-to-back launches lengthen as the engine clock drops under the "
-         "sustained load, which is what the bench's 10-launch average sees.", "",
+         "Back-to-back launches lengthen as the engine clock drops under the sustained load "
+         "(durations in launch order above).", "",
          f"Kernel source sha256 (nsn_amd/csrc/nsn_codec.hip): `{fig['source_sha256']}`", ""]
+    sq = _sq(d, ENCODE_KERNEL, first=ENCODE_PROFILE_STEPS)
+    if sq:
+        L += ["## SQ counters (the first launches of the sq1 and sq2 passes)", ""] + _sq_lines(sq) + [""]
     ENCODE_MD.write_text("\n".join(L))
     print("\n".join(L))
 
