@@ -60,6 +60,7 @@ def parse():
     p.add_argument("--kernel", default="fast", choices=["fast", "reference"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-baselines", action="store_true", help="skip the bridge / fp16 comparators")
+    p.add_argument("--c2-only", action="store_true", help="default run: skip the C3 and C4 figures")
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
     p.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "k1c", "adapter"],
@@ -520,7 +521,21 @@ def profile_run(args):
 C3 = dict(B=64, HQ=16, HKV=4, L=8192, bits=5)
 
 
-def main_c3(args):
+def interleaved_rounds(step, split, merge, steps, stream, rounds=5):
+    """Mean per-launch ms of a decode step, its split kernel alone and its
+    merge alone, from `rounds` interleaved rounds of back-to-back batches
+    (HIP events around each batch on the launch stream), so that all three
+    run at one clock.  Also returns the per-round split times (sorted)."""
+    per = max(4, steps // rounds)
+    rs, rk, rm = [], [], []
+    for _ in range(rounds):
+        rs.append(timed(step, per, 0, stream))
+        rk.append(timed(split, per, 0, stream))
+        rm.append(timed(merge, per, 0, stream))
+    return sum(rs) / rounds, sum(rk) / rounds, sum(rm) / rounds, sorted(rk), per
+
+
+def main_c3(args, emit=True):
     """C3: 5-bit codes, B=64, 16q/4kv heads, every
     sequence 8192 tokens (128 packed blocks, no tail), K and V heavy-tailed
     (per-channel Student-t df=3 x lognormal token norms; GPU generator seed 3).
@@ -576,12 +591,17 @@ def main_c3(args):
     def step(merge=True):
         kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
                                  workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=merge)
+    lib = _lib.lib()
+
+    def merge_kernel():
+        _lib.check(lib.nsn_attention_merge(ws.data_ptr(), b_, hq, n_splits, ctx.data_ptr(), out.data_ptr(),
+                                           _lib.DTYPE_BF16, status.data_ptr(), stream.cuda_stream), "nsn_attention_merge")
     ms_step = timed(step, args.steps, args.warmup, stream)
-    ms_split = timed_median(lambda: step(merge=False), args.steps, stream)
+    _, ms_split, ms_merge, _, _ = interleaved_rounds(step, lambda: step(merge=False), merge_kernel, args.steps, stream)
     assert _dev.read_status(status) == 0
     nbytes = b_ * hkv * 2 * L * (bits * 16 + 10) + 2 * b_ * hq * D * 2
     achieved = nbytes / (ms_split * 1e-3) / 1e9
-    log(f"[bench] C3 decode step {ms_step * 1e3:.1f} us, split kernel {ms_split * 1e3:.1f} us, "
+    log(f"[bench] C3 decode step {ms_step * 1e3:.1f} us, split kernel {ms_split * 1e3:.1f} us, merge {ms_merge * 1e3:.1f} us, "
         f"{nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
     _, ref_ctx = kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel="reference",
                                           kv_round_dtype=torch.float32)
@@ -592,7 +612,7 @@ def main_c3(args):
         "metric": "C3 5-bit fused decode-attn µs/step (B=64, 16q/4kv, ctx 8192) + encode of all K/V blocks",
         "value": round(ms_step * 1e3, 2), "unit": "µs/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic (GPU torch.Generator seed 3)",
+        "vs_baseline": None, "dtype": "f16x2/f32", "data": "synthetic (GPU torch.Generator seed 3)",
         "config": {"workload": "C3: 5-bit packed K+V, B=64, 16q/4kv heads, d=128, ctx 8192 (128 blocks, no tail)",
                    "batch": b_, "heads_q": hq, "heads_kv": hkv, "head_dim": D, "ctx": L, "bits": bits,
                    "kernel": args.kernel, "split_tokens": split, "n_splits": n_splits},
@@ -605,7 +625,9 @@ def main_c3(args):
                             "frac": round(enc_gbs / HBM_PEAK_GBS, 4)},
         "parity_ok": ok,
     }
-    print(json.dumps(result), flush=True)
+    if emit:
+        print(json.dumps(result), flush=True)
+    return result
 
 
 K1C_MODELS = {"Qwen3-30B-A3B": dict(n_kv=8, head_dim=128, n_q=32), "Gemma4-26B-A4B": dict(n_kv=8, head_dim=256, n_q=32)}
@@ -738,7 +760,7 @@ def k1c_summary(d):
 C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
 
 
-def main_c4(args):
+def main_c4(args, emit=True):
     """C4: a streaming packed cache of Ouro-like
     slots (MHA, 16 kv heads, d=128, batch 32, N(0,1) bf16 activations, GPU
     generator seed 4, fp16 tails).  Per slot: an 8192-token chunked prefill
@@ -856,7 +878,9 @@ def main_c4(args):
                      "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "decode step (append + fast decode + merge + policy)", "algorithmic_bytes": dec_bytes},
     }
-    print(json.dumps(result), flush=True)
+    if emit:
+        print(json.dumps(result), flush=True)
+    return result
 
 
 STATS_DOC = {
@@ -1316,6 +1340,24 @@ def main():
         log("[bench] CPU baseline (PyTorch-CPU restatement, all threads and one) ...")
         result["cpu_baseline"] = cpu_baseline(kk, vv, q, lengths)
         log(f"[bench] CPU baseline {result['cpu_baseline']['value']:.0f} us/step (scaled)")
+    if not args.c2_only:
+        # the other BASELINE.json configs at their own shapes, reduced repeat counts
+        # (C3: 60 steps; C4: one slot, 32 decode steps), as sub-objects of this line
+        del kk, vv, q, ws, k, v
+        torch.cuda.empty_cache()
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup, sub.slots, sub.decode_steps = 60, 20, 1, 32
+        r3 = main_c3(sub, emit=False)
+        result["c3"] = {"workload": r3["config"]["workload"], "step_us": r3["value"],
+                        "split_kernel_us": r3["roofline"]["kernel_us"], "hbm_frac": r3["roofline"]["frac"],
+                        "encode_us": r3["encode_us"], "encode_hbm_frac": r3["encode_roofline"]["frac"],
+                        "parity_ok": r3["parity_ok"]}
+        torch.cuda.empty_cache()
+        r4 = main_c4(sub, emit=False)
+        result["c4"] = {"workload": r4["config"]["workload"], "prefill_ms_per_slot": r4["prefill_ms_per_slot"],
+                        "prefill_mfma_frac": r4["prefill_roofline"]["frac"],
+                        "prefill_kernel_last_chunk_us": r4["prefill_kernel_last_chunk_us"],
+                        "decode_us_per_slot_step": r4["value"], "decode_hbm_frac": r4["roofline"]["frac"]}
     print(json.dumps(result), flush=True)
 
 
