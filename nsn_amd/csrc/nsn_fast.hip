@@ -154,11 +154,6 @@ __device__ __forceinline__ void vpair5(uint32_t w0a, uint32_t w1a, uint32_t w0b,
     D[7] = X4 & 0x00F800F8u;
 }
 
-template <int QDT>
-__device__ __forceinline__ float load_q(const void *q, int64_t idx) {
-    return Elem<QDT>::load(static_cast<const uint16_t *>(q)[idx]);
-}
-
 struct FastSide {
     const uint8_t *codes;
     const uint16_t *mins, *scales;
@@ -207,16 +202,17 @@ __device__ __forceinline__ float red16_sum(float x) {
     return x;
 }
 
-// Wave-wide (64-lane) inclusive prefix sum, and a uniform read of one lane.
-__device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
-    const int l = threadIdx.x;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int64_t y = __shfl_up(static_cast<long long>(x), d);
-        if (l >= d) x += y;
-    }
-    return x;
+// Quotient and remainder of uniform a >= 0 by b > 0.  A 64-bit division
+// expands to over a hundred scalar instructions, and every wave of a CU
+// shares one scalar unit while it partitions the work, so operands that fit
+// in 32 bits (all practical sizes) take the 32-bit expansion.
+__device__ __forceinline__ int64_t udivq(int64_t a, int64_t b) {
+    if (((static_cast<uint64_t>(a) | static_cast<uint64_t>(b)) >> 32) == 0)
+        return static_cast<int64_t>(static_cast<uint32_t>(a) / static_cast<uint32_t>(b));
+    return a / b;
 }
+__device__ __forceinline__ int64_t uremq(int64_t a, int64_t b) { return a - udivq(a, b) * b; }
+
 // 32-bit wave reductions and scan on DPP row operations plus scalar reads of
 // the four row results: a few cycles per step instead of an LDS permute each.
 template <int CTRL>
@@ -415,7 +411,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     // which measurably helps the HBM (~2 % on the C2 workload).
     const int64_t nfb = (t_fast > t_begin) ? (t_fast - t_begin) / kBlockTok : 0;
     const int64_t rot =
-        (nfb > 1) ? static_cast<int64_t>((static_cast<uint32_t>(blockIdx.x) * 2654435761u) >> 8) % nfb : 0;
+        (nfb > 1) ? uremq(static_cast<int64_t>((static_cast<uint32_t>(blockIdx.x) * 2654435761u) >> 8), nfb) : 0;
     auto fast_blk = [&](int64_t j) {   // token start of the j-th fast block walked
         const int64_t x = j + rot;
         return t_begin + ((x < nfb) ? x : x - nfb) * kBlockTok;
@@ -440,6 +436,22 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
     float c1[NJ], c1s[NJ];             // score scale: scale * log2(e) * 2^-sigma_h (c1s: times 2^24)
     uint32_t quh[NJ][4], qul[NJ][4];   // q * 2^sigma in element order (hi, lo): q.m and dense keys
     uint32_t qkh[NJ][4], qkl[NJ][4];   // the same * 2^-kE: the coefficient rows
+    // Every lane loads its 8 channels (16 bytes) of an in-bounds head (the
+    // group's first where head grp + 4j is past the group) without a branch,
+    // so that the loads are in flight together and one wait covers them.
+    uint16_t qraw[NJ][8];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int h = grp + 4 * j;
+        const uint16_t *qr = static_cast<const uint16_t *>(p.q) +
+                             (static_cast<int64_t>(b) * p.heads_q + hq0 + (h < G ? h : 0)) * kDim + pch;
+        uint4 w;
+        __builtin_memcpy(&w, qr, 16);
+        asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));   // (kept unconditional)
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qraw[j][c] = static_cast<uint16_t>(ww[c / 2] >> (16 * (c % 2)));
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int h = grp + 4 * j;
@@ -448,7 +460,7 @@ __device__ __forceinline__ void segment(const FastParams &p, const Lds<BITS, GRP
         float mx = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            qv[c] = valid ? load_q<QDT>(p.q, (static_cast<int64_t>(b) * p.heads_q + hq0 + h) * kDim + pch + c) : 0.f;
+            qv[c] = valid ? Elem<QDT>::load(qraw[j][c]) : 0.f;
             mx = fmaxf(mx, fabsf(qv[c]));
             bad_in |= !finite(qv[c]);
         }
@@ -865,27 +877,37 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     __shared__ uint32_t s_m0[S::MW], s_m1[S::MW];
     const Lds<BITS, GRP> sh{s_afrag, s_pbuf, s_k0, s_k1, s_v0, s_v1, s_m0, s_m1};
     const int l = threadIdx.x;
+    // Lane l of a chunk holds sequence c0 + l: its length, packed K / V block
+    // counts and 64-token block count -- one vector load per field for 64
+    // sequences rather than one dependent scalar load per sequence.  The
+    // first chunk's fields are loaded before the LDS set-up, which then
+    // overlaps their latency.
+    auto fields = [&](int64_t bb, int32_t &t, int32_t &nk, int32_t &nv) {
+        t = nk = nv = 0;
+        if (bb < p.batch) {
+            t = p.seq_len[bb];
+            nk = (!SCORES && p.k.blocks) ? p.k.blocks[bb] : 0;
+            nv = p.v.blocks ? p.v.blocks[bb] : 0;
+        }
+    };
+    int32_t t_0, nk_0, nv_0;
+    fields(l, t_0, nk_0, nv_0);
     // empty A rows and the zero entries stay zero
     for (int i = l; i < S::ROWS * 16 + 1; i += 64) s_afrag[i] = u32x4{0u, 0u, 0u, 0u};
     for (int i = l; i < S::ROWS * 36 + 4; i += 64) s_pbuf[i] = 0u;
     lds_sync();
 
-    // Lane l of a chunk holds sequence c0 + l: its length, packed K / V block
-    // counts and 64-token block count -- one vector load per field for 64
-    // sequences rather than one dependent scalar load per sequence.
     const int64_t H = p.heads_kv;
     int64_t c0 = 0;
     int32_t t_l = 0, nk_l = 0, nv_l = 0, nb_l = 0;
     int64_t incl = 0;   // blocks of sequences c0 .. c0 + l, all kv-heads
-    // Sequence bb's length, or 0 when its blocks or tail lie past the cache's
-    // capacity (the launch-time host checks cover checked calls; a graph
-    // replay with device lengths has only this one): nothing of such a
-    // sequence is read, and the status word says why.
+    // A sequence's length t, or 0 when its blocks (nk, nv) or tail lie past
+    // the cache's capacity (the launch-time host checks cover checked calls;
+    // a graph replay with device lengths has only this one): nothing of such
+    // a sequence is read, and the status word says why.  (Lanes past the
+    // batch hold t = nk = nv = 0, which is usable and empty.)
     bool over = false;
-    auto usable = [&](int64_t bb, int32_t &nk, int32_t &nv) -> int32_t {
-        const int32_t t = p.seq_len[bb];
-        nk = (!SCORES && p.k.blocks) ? p.k.blocks[bb] : 0;
-        nv = p.v.blocks ? p.v.blocks[bb] : 0;
+    auto usable = [&](int32_t t, int32_t &nk, int32_t &nv) -> int32_t {
         auto fits = [&](const FastSide &sd, int32_t nb, bool present) {
             if (!present) return true;
             if (nb < 0 || nb > sd.block_cap) return false;
@@ -900,21 +922,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         }
         return t > 0 ? t : 0;
     };
-    auto load_chunk = [&]() {
-        const int64_t bb = c0 + l;
-        int32_t nk = 0, nv = 0;
-        t_l = (bb < p.batch) ? usable(bb, nk, nv) : 0;
+    auto take_chunk = [&](int32_t t, int32_t nk, int32_t nv) {
+        t_l = usable(t, nk, nv);
         nk_l = nk;
         nv_l = nv;
         nb_l = static_cast<int32_t>((static_cast<int64_t>(t_l) + kBlockTok - 1) / kBlockTok);
-        incl = H * wave_incl_scan(nb_l);
+        incl = H * static_cast<int64_t>(static_cast<uint32_t>(wave_incl_scan32(nb_l)));   // (< 2^32: nb_l <= 2^25)
     };
-    load_chunk();
+    auto load_chunk = [&]() {
+        int32_t t, nk, nv;
+        fields(c0 + l, t, nk, nv);
+        take_chunk(t, nk, nv);
+    };
+    take_chunk(t_0, nk_0, nv_0);
     int64_t N = lane_get(incl, 63);
     for (int64_t c = 64; c < p.batch; c += 64) {   // sequences past the first 64
-        int32_t nk = 0, nv = 0;
-        const int32_t t = (c + l < p.batch) ? usable(c + l, nk, nv) : 0;
-        N += lane_get(H * wave_incl_scan((static_cast<int64_t>(t) + kBlockTok - 1) / kBlockTok), 63);
+        int32_t tr, nk, nv;
+        fields(c + l, tr, nk, nv);
+        const int32_t t = usable(tr, nk, nv);
+        const int32_t nbt = static_cast<int32_t>((static_cast<int64_t>(t) + kBlockTok - 1) / kBlockTok);
+        N += H * static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(wave_incl_scan32(nbt), 63)));
     }
     if (blockIdx.x == 0 && __ballot(over)) raise_status(p.status, l == 0 ? NSN_ST_CAPACITY : 0);
     if (N == 0) return;
@@ -929,10 +956,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         // smallest block count per wave with sum_s n_s <= W.  Each wave runs
         // exactly one segment.  Since sum_s ceil(nb_s / P) <= N / P + nstr,
         // the search starts below ceil(N / (W - nstr)).
-        int64_t lo = (N + W - 1) / W, hi = wave_max(nb_l);
+        int64_t lo = udivq(N + W - 1, W), hi = wave_max(nb_l);
         lo = (lo > p.min_blocks) ? lo : p.min_blocks;
         if (nstr < W) {   // (any P >= ub fits; the answer is the first fit >= lo)
-            int64_t ub = (N + (W - nstr) - 1) / (W - nstr);
+            int64_t ub = udivq(N + (W - nstr) - 1, W - nstr);
             ub = (ub > lo) ? ub : lo;
             hi = (ub < hi) ? ub : hi;
         }
@@ -960,7 +987,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
         const int64_t n = at(n_l), nb = at(nb_l);
         const int64_t r = w - (lane_get(wincl, lane) - H * n);
-        const int kvh = static_cast<int>(r / n);
+        const int kvh = static_cast<int>(udivq(r, n));
         const int64_t k = r - kvh * n;
         const int64_t w0 = w - k;   // the stream's first wave
         auto cw = [&](int64_t j) {   // summed weight of the stream's waves 0 .. j-1
@@ -974,7 +1001,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         nbp = (nbp < nb) ? nbp : nb;
         const int64_t U = nbp + 3 * (nb - nbp), ctot = cw(n);
         auto blk = [&](int64_t c) { return (c <= nbp) ? c : nbp + (c - nbp + 1) / 3; };
-        const int64_t i0 = blk(cw(k) * U / ctot), i1 = blk(cw(k + 1) * U / ctot);
+        const int64_t i0 = blk(udivq(cw(k) * U, ctot)), i1 = blk(udivq(cw(k + 1) * U, ctot));
         const int64_t T = at(t_l);
         if (n <= p.n_splits) {
             segment<BITS, QDT, SCORES, GRP, TBF>(p, sh, lane, kvh, i0 * kBlockTok, (i1 * kBlockTok < T) ? i1 * kBlockTok : T,
@@ -987,7 +1014,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
 
     // Stream-K partition (more streams than waves, or more than 64
     // sequences): the blocks of all streams laid end to end, P per wave.
-    int64_t P = (N + W - 1) / W;
+    int64_t P = udivq(N + W - 1, W);
     if (P < p.min_blocks) P = p.min_blocks;
     int64_t g = static_cast<int64_t>(blockIdx.x) * P;
     const int64_t g1 = (g + P < N) ? g + P : N;
@@ -1008,14 +1035,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     }
     int64_t nb = at(nb_l);
     int64_t start_b = base + lane_get(incl, lane) - H * nb;   // first block of sequence c0 + lane
-    int kvh = static_cast<int>((g - start_b) / nb);
+    int kvh = static_cast<int>(udivq(g - start_b, nb));
     int64_t i0 = g - start_b - kvh * nb;
     while (g < g1) {
         const int64_t start_s = start_b + kvh * nb;
         const int64_t i1 = (i0 + (g1 - g) < nb) ? i0 + (g1 - g) : nb;
         const int64_t T = at(t_l);
-        const int slot = static_cast<int>(blockIdx.x - start_s / P);
-        const int count = static_cast<int>((start_s + nb - 1) / P - start_s / P + 1);
+        const int64_t s0 = udivq(start_s, P);
+        const int slot = static_cast<int>(blockIdx.x - s0);
+        const int count = static_cast<int>(udivq(start_s + nb - 1, P) - s0 + 1);
         if (slot < p.n_splits && count <= p.n_splits) {
             segment<BITS, QDT, SCORES, GRP, TBF>(p, sh, static_cast<int>(c0 + lane), kvh, i0 * kBlockTok,
                                             (i1 * kBlockTok < T) ? i1 * kBlockTok : T, at(nk_l), at(nv_l), slot,
