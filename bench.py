@@ -769,7 +769,8 @@ def main_c4(args, emit=True):
     append one token, attend over packed + tail with the fast kernel and
     compress a block every 64 tokens.  The 96
     slots of the configuration do identical work; `--slots` of them are run
-    and the figures are per slot."""
+    and the figures are per slot, after one untimed warm-up prefill (of slot 0,
+    which is then emptied)."""
     import torch
     from nsn_amd import _dev, kernels
     from nsn_amd.stream_cache import StreamingKVCache
@@ -792,6 +793,8 @@ def main_c4(args, emit=True):
             cache.prefill(s, qc, kc, vc, check=False)
             cache.append(s, kc, vc)
             cache.compress_to(s, max(cache.compressed[s], ((cache.length[s] - 64) // 64) * 64))
+    prefill_slot(0)   # untimed warm-up: one slot's whole prefill, then the slot is emptied again
+    cache.reset(0)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0 = torch.cuda.Event(enable_timing=True)

@@ -286,6 +286,20 @@ int nsn_tail_append(const void *k_new, const void *v_new, int64_t rows, int64_t 
                     void *k_tail, void *v_tail, int64_t tail_cap, int64_t offset, int dtype, nsn_stream_t stream);
 
 /*
+ * nsn_tail_append with a dtype conversion: k_new / v_new hold src_dtype
+ * (NSN_DTYPE_F16, NSN_DTYPE_BF16 or NSN_DTYPE_F32) and every element is
+ * rounded to the tail dtype (NSN_DTYPE_F16 or NSN_DTYPE_BF16, round to
+ * nearest even), so that an append of model activations in another dtype
+ * needs no separate conversion pass.  Same layout and checks as
+ * nsn_tail_append.  Replaces the same tail concatenation
+ * (experiments/ac08/source/loop_kv_pk01_cache.py:101-102) where the new
+ * tokens' dtype differs from the preallocated tail's.
+ */
+int nsn_tail_append_cast(const void *k_new, const void *v_new, int src_dtype, int64_t rows, int64_t n,
+                         int64_t new_row_stride, void *k_tail, void *v_tail, int64_t tail_cap, int64_t offset,
+                         int dtype, nsn_stream_t stream);
+
+/*
  * nsn_tail_append with the position in device memory: the n new tokens of
  * each row go to [*tail_end - n, *tail_end).  The launch then has no host
  * argument that changes from step to step, so a captured HIP graph of a

@@ -45,6 +45,43 @@ __global__ __launch_bounds__(256) void tail_append_to_kernel(const uint4 *k_new,
     v_tail[dst] = v_new[src];
 }
 
+// The copy with a dtype conversion: one thread per 8 elements of a new token
+// row (16 bytes of a 16-bit tail), each element read as SDT, rounded to DDT
+// (round to nearest even; what torch's Tensor.to does).
+template <int SDT, int DDT>
+__global__ __launch_bounds__(256) void tail_append_cast_kernel(const void *k_new, const void *v_new, int64_t rows,
+                                                               int64_t n, int64_t new_row_stride, uint4 *k_tail,
+                                                               uint4 *v_tail, int64_t tail_cap, int64_t offset) {
+    using S = Elem<SDT>;
+    using D = Elem<DDT>;
+    constexpr int G = kDim / 8;   // 8-element groups per row
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= rows * n * G) return;
+    const int64_t c = i % G, tok = (i / G) % n, r = i / (G * n);
+    const int64_t src = (r * new_row_stride + tok) * kDim + 8 * c;
+    const int64_t dst = (r * tail_cap + offset + tok) * G + c;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+        const typename S::T *x = static_cast<const typename S::T *>(side ? v_new : k_new) + src;
+        typename S::T v[8];
+        if constexpr (SDT == NSN_DTYPE_F32) {
+            const float4 a = reinterpret_cast<const float4 *>(x)[0], b = reinterpret_cast<const float4 *>(x)[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+            const uint4 a = *reinterpret_cast<const uint4 *>(x);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = static_cast<uint32_t>(D::store(S::load(v[2 * e]))) |
+                   (static_cast<uint32_t>(D::store(S::load(v[2 * e + 1]))) << 16);
+        (side ? v_tail : k_tail)[dst] = uint4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 struct RopeParams {
     const uint16_t *q, *k, *v, *cos, *sin;
     int64_t cs_stride;   // elements between the cos/sin rows of two sequences (0: one row for all)
@@ -156,6 +193,37 @@ extern "C" int nsn_tail_append(const void *k_new, const void *v_new, int64_t row
                        reinterpret_cast<hipStream_t>(stream), static_cast<const uint4 *>(k_new),
                        static_cast<const uint4 *>(v_new), rows, n, new_row_stride, static_cast<uint4 *>(k_tail),
                        static_cast<uint4 *>(v_tail), tail_cap, offset, chunks);
+    return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
+}
+
+extern "C" int nsn_tail_append_cast(const void *k_new, const void *v_new, int src_dtype, int64_t rows, int64_t n,
+                                    int64_t new_row_stride, void *k_tail, void *v_tail, int64_t tail_cap,
+                                    int64_t offset, int dtype, nsn_stream_t stream) {
+    if (rows < 0 || n < 0 || offset < 0 || new_row_stride < n || tail_cap < offset + n) return NSN_EINVAL;
+    if (src_dtype != NSN_DTYPE_F16 && src_dtype != NSN_DTYPE_BF16 && src_dtype != NSN_DTYPE_F32) return NSN_EINVAL;
+    if (dtype != NSN_DTYPE_F16 && dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
+    if (rows == 0 || n == 0) return NSN_OK;
+    if (!k_new || !v_new || !k_tail || !v_tail) return NSN_EINVAL;
+    for (const void *ptr : {k_new, v_new, static_cast<const void *>(k_tail), static_cast<const void *>(v_tail)})
+        if (reinterpret_cast<uintptr_t>(ptr) & 15u) return NSN_EINVAL;
+    const int64_t total = rows * n * (kDim / 8);
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffff) return NSN_EINVAL;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint4 *kt = static_cast<uint4 *>(k_tail), *vt = static_cast<uint4 *>(v_tail);
+#define NSN_CAST_LAUNCH(S_, D_)                                                                                     \
+    hipLaunchKernelGGL((tail_append_cast_kernel<S_, D_>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, k_new, \
+                       v_new, rows, n, new_row_stride, kt, vt, tail_cap, offset)
+    if (dtype == NSN_DTYPE_F16) {
+        if (src_dtype == NSN_DTYPE_F16) NSN_CAST_LAUNCH(NSN_DTYPE_F16, NSN_DTYPE_F16);
+        else if (src_dtype == NSN_DTYPE_BF16) NSN_CAST_LAUNCH(NSN_DTYPE_BF16, NSN_DTYPE_F16);
+        else NSN_CAST_LAUNCH(NSN_DTYPE_F32, NSN_DTYPE_F16);
+    } else {
+        if (src_dtype == NSN_DTYPE_F16) NSN_CAST_LAUNCH(NSN_DTYPE_F16, NSN_DTYPE_BF16);
+        else if (src_dtype == NSN_DTYPE_BF16) NSN_CAST_LAUNCH(NSN_DTYPE_BF16, NSN_DTYPE_BF16);
+        else NSN_CAST_LAUNCH(NSN_DTYPE_F32, NSN_DTYPE_BF16);
+    }
+#undef NSN_CAST_LAUNCH
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;
 }
 

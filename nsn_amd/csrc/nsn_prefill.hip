@@ -372,7 +372,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    // Row sums of the weights on the matrix core: a constant A tile whose row
+    // 0 is all ones, so row 0 of lsum[qt] = sum over tokens of the P operand
+    // (the rounded weights the PV product uses); lanes 0-15 hold it.
+    f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint32_t one2 = (row == 0) ? (DT == NSN_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u) : 0u;
+    const u32x4 ones_a = u32x4{one2, one2, one2, one2};
     bool bad = false;
 
     // Block j: packed (j < nb), tail (nb <= j < nb + nt_blk), or chunk; its rows
@@ -457,12 +463,6 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            if (!QPRE) {
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) s[tt][qt][i] *= p.qscale;
-            }
             if (masked) {
                 // allowed tokens of this block: tok < valid and (chunk blocks) tok <= query - cpos
                 const int64_t rel = (cpos >= 0) ? qw + 16 * qt + row - cpos : kBlockTok;
@@ -479,26 +479,23 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qt][0], s[tt][qt][1]), fmaxf(s[tt][qt][2], s[tt][qt][3])));
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
+            if (!QPRE) mx *= p.qscale;   // (bf16: the scores scale inside the exponent below)
             if (__builtin_amdgcn_ballot_w64(mx > m_run[qt])) {
                 const float mnew = fmaxf(m_run[qt], mx);
                 const float alpha = (m_run[qt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qt] - mnew);
-                l_run[qt] *= alpha;
+                lsum[qt] *= alpha;
 #pragma unroll
                 for (int ct = 0; ct < 8; ++ct) acc[ct][qt] *= alpha;
                 m_run[qt] = mnew;
             }
             const float msafe = (m_run[qt] == -INFINITY) ? 0.f : m_run[qt];
-            float ls = 0.f;
             float pw[4][4];
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = __builtin_amdgcn_exp2f(s[tt][qt][i] - msafe);
-                    ls += e;
-                    pw[tt][i] = e;
-                }
-            l_run[qt] += ls;
+                for (int i = 0; i < 4; ++i)
+                    pw[tt][i] = __builtin_amdgcn_exp2f(QPRE ? s[tt][qt][i] - msafe
+                                                            : __builtin_fmaf(s[tt][qt][i], p.qscale, -msafe));
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2)
                 pb[ks2][qt] = u32x4{pk<DT>(pw[2 * ks2][0], pw[2 * ks2][1]), pk<DT>(pw[2 * ks2][2], pw[2 * ks2][3]),
@@ -515,14 +512,16 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma<DT>(a, pb[ks2][qt], acc[ct][qt]);
             }
         }
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) lsum[qt] = mfma<DT>(ones_a, pb[ks2][qt], lsum[qt]);
     }
 
     // ---- output: O[q][c] = O^T / l, channels 16*ct + 4*g + i of query qw + 16*qt + row
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        float lt = l_run[qt];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        const float lt = __shfl(lsum[qt][0], row);   // (query row's sum, from lane row)
         const int64_t qi = qw + 16 * qt + row;
         if (qi >= p.n_q) continue;
         const float r = 1.f / lt;

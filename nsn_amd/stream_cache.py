@@ -135,7 +135,15 @@ class StreamingKVCache:
         key = tuple(L) if isinstance(L, (list, tuple)) else (int(L),) * self.batch
         t = self._len_dev.get(key)
         if t is None:
-            t = torch.tensor(key, dtype=torch.int32).to(self.device)
+            # Uploaded from pinned memory without a host wait: a pageable copy
+            # would drain the stream first, so every new length (each chunk,
+            # each decode step) would leave the GPU idle while the host issues
+            # the next launches.  The oldest entries are dropped (a dropped
+            # tensor's memory is reused only by later work on the stream).
+            gpu = torch.device(self.device).type == "cuda"
+            t = torch.tensor(key, dtype=torch.int32, pin_memory=gpu).to(self.device, non_blocking=gpu)
+            if len(self._len_dev) >= 256:
+                self._len_dev.pop(next(iter(self._len_dev)))
             self._len_dev[key] = t
         return t
 
@@ -156,6 +164,16 @@ class StreamingKVCache:
         for b in range(self.batch):
             L[b] += n
 
+    def reset(self, slot):
+        """Empty the slot for a new batch of sequences (its storage is kept;
+        nothing past a sequence's length is ever read)."""
+        for b in range(self.batch):
+            self.seq_length[slot][b] = 0
+            self.seq_compressed[slot][b] = 0
+        for name in ("K", "V"):
+            self._sides[(slot, name)].kv.blocks.zero_()
+        self.encoded_blocks[slot] = 0
+
     # ------------------------------------------------------------------ updates
     def append(self, slot, k, v, counts=None):
         """Append k, v [B, H, n, 128] to the slot's tails (converted to the tail
@@ -173,25 +191,35 @@ class StreamingKVCache:
             if L[b] + counts[b] > self.block_cap * BLOCK + self.tail_cap:
                 raise IntegrityError("Cache capacity exceeded")
         require(k.dtype in (torch.float16, torch.bfloat16, torch.float32) and v.dtype == k.dtype, "Append dtype")
-        if k.dtype != self.dtype:
-            k, v = k.to(self.dtype), v.to(self.dtype)
         k, v = k.contiguous(), v.contiguous()
+        # another dtype converts inside the append kernel (no separate pass);
+        # an fp32 tail takes the converted copy
+        cast = k.dtype != self.dtype and self.dtype in (torch.float16, torch.bfloat16)
+        if k.dtype != self.dtype and not cast:
+            k, v = k.to(self.dtype), v.to(self.dtype)
         kt, vt = self._sides[(slot, "K")].kv.tail, self._sides[(slot, "V")].kv.tail
         lib = _lib.lib()
         dt = _dev.dtype_code(self.dtype)
         offs = [L[b] - C[b] for b in range(self.batch)]
+        sdt = _dev.dtype_code(k.dtype)
+
+        def launch(kp, vp, ktp, vtp, rows, cnt, off):
+            if cast:
+                rc = lib.nsn_tail_append_cast(kp, vp, sdt, rows, cnt, n, ktp, vtp, self.tail_cap, off, dt,
+                                              _dev.stream())
+                _lib.check(rc, "nsn_tail_append_cast")
+            else:
+                rc = lib.nsn_tail_append(kp, vp, rows, cnt, n, ktp, vtp, self.tail_cap, off, dt, _dev.stream())
+                _lib.check(rc, "nsn_tail_append")
         if len(set(offs)) == 1 and len(set(counts)) == 1:
             if counts[0]:
-                rc = lib.nsn_tail_append(k.data_ptr(), v.data_ptr(), self.batch * self.heads, counts[0], n,
-                                         kt.data_ptr(), vt.data_ptr(), self.tail_cap, offs[0], dt, _dev.stream())
-                _lib.check(rc, "nsn_tail_append")
+                launch(k.data_ptr(), v.data_ptr(), kt.data_ptr(), vt.data_ptr(), self.batch * self.heads, counts[0],
+                       offs[0])
         else:
             for b in range(self.batch):   # one launch per sequence: its own offset and count
                 if counts[b]:
-                    rc = lib.nsn_tail_append(k[b].data_ptr(), v[b].data_ptr(), self.heads, counts[b], n,
-                                             kt[b].data_ptr(), vt[b].data_ptr(), self.tail_cap, offs[b], dt,
-                                             _dev.stream())
-                    _lib.check(rc, "nsn_tail_append")
+                    launch(k[b].data_ptr(), v[b].data_ptr(), kt[b].data_ptr(), vt[b].data_ptr(), self.heads,
+                           counts[b], offs[b])
         for b in range(self.batch):
             L[b] += counts[b]
 

@@ -204,3 +204,51 @@ def test_stream_cache_ragged_lengths():
     steps_of = [sorted(i for bb, i in compressions if bb == b) for b in range(B)]
     assert all(steps_of) and len({tuple(x) for x in steps_of}) == B
     cache.check_status()
+
+
+def test_tail_append_cast_matches_torch_conversion():
+    """nsn_tail_append_cast through the C ABI: every (source, tail) dtype pair
+    writes, bit for bit, what torch's Tensor.to(tail dtype) + nsn_tail_append
+    write (round to nearest even; values past fp16's range become inf,
+    values below it subnormal or zero), and leaves the rest of the tail
+    untouched."""
+    from nsn_amd import _dev, _lib
+    lib = _lib.lib()
+    rows, n, cap, off = 5, 7, 24, 9
+    g = torch.Generator(device=DEV).manual_seed(11)
+    base = torch.randn((rows, n, 128), generator=g, device=DEV)
+    base[0, 0, :8] = torch.tensor([7e4, -1e5, 3e-6, -6e-8, 1e-9, 65519.0, 65520.0, 0.0], device=DEV)
+    stream = _dev.stream()
+    for sdt in (torch.float16, torch.bfloat16, torch.float32):
+        for ddt in (torch.float16, torch.bfloat16):
+            k = base.to(sdt)
+            v = (-2 * base).to(sdt)
+            kt_a = torch.full((rows, cap, 128), 3.0, dtype=ddt, device=DEV)
+            vt_a, kt_b, vt_b = kt_a.clone(), kt_a.clone(), kt_a.clone()
+            assert lib.nsn_tail_append_cast(k.data_ptr(), v.data_ptr(), _dev.dtype_code(sdt), rows, n, n,
+                                            kt_a.data_ptr(), vt_a.data_ptr(), cap, off, _dev.dtype_code(ddt),
+                                            stream) == 0
+            kc, vc = k.to(ddt), v.to(ddt)
+            assert lib.nsn_tail_append(kc.data_ptr(), vc.data_ptr(), rows, n, n, kt_b.data_ptr(), vt_b.data_ptr(),
+                                       cap, off, _dev.dtype_code(ddt), stream) == 0
+            assert torch.equal(kt_a.view(torch.int16), kt_b.view(torch.int16)), (sdt, ddt)
+            assert torch.equal(vt_a.view(torch.int16), vt_b.view(torch.int16)), (sdt, ddt)
+
+
+def test_append_in_another_dtype_equals_append_of_converted_tokens():
+    """StreamingKVCache.append of bf16 (or fp32) tokens into fp16 tails: the
+    same tails, bit for bit, as appending the tokens converted first, for a
+    uniform append and a ragged one (per-sequence counts)."""
+    g = torch.Generator(device=DEV).manual_seed(12)
+    B, H, n = 3, 2, 40
+    for sdt in (torch.bfloat16, torch.float32):
+        caches = [StreamingKVCache(1, B, H, 1024, dtype=torch.float16, max_append=64, device=DEV) for _ in range(2)]
+        for counts in (None, [n, 5, 0]):
+            k = torch.randn((B, H, n, 128), generator=g, device=DEV).to(sdt)
+            v = torch.randn((B, H, n, 128), generator=g, device=DEV).to(sdt)
+            caches[0].append(0, k, v, counts=counts)
+            caches[1].append(0, k.to(torch.float16), v.to(torch.float16), counts=counts)
+        for name in ("K", "V"):
+            a, b = caches[0].side(0, name).tail, caches[1].side(0, name).tail
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (sdt, name)
+        assert caches[0].seq_length == caches[1].seq_length

@@ -48,7 +48,7 @@ def test_library_rejects_bad_arguments_without_gpu_work():
 
 
 def test_device_position_appends_reject_bad_arguments_without_gpu_work():
-    """nsn_tail_append_to and nsn_rope_append validate on the host before any
+    """nsn_tail_append_to, nsn_tail_append_cast and nsn_rope_append validate on the host before any
     launch (fake, never dereferenced addresses stand in for device buffers)."""
     lib = _lib.lib()
     E, OK, F16 = _lib.NSN_EINVAL, _lib.NSN_OK, _lib.DTYPE_F16
@@ -63,6 +63,18 @@ def test_device_position_appends_reject_bad_arguments_without_gpu_work():
     assert tail_to(end=None) == E                      # no device position
     assert tail_to(k=A + 8) == E                       # misaligned source
     assert tail_to(rows=0) == OK                       # empty: no work
+
+    def cast(rows=2, n=1, stride=1, cap=8, off=0, sdt=_lib.DTYPE_BF16, dtype=F16, k=A):
+        return lib.nsn_tail_append_cast(k, A, sdt, rows, n, stride, A, A, cap, off, dtype, None)
+    assert cast(rows=-1) == E
+    assert cast(n=3, stride=2) == E                    # row stride shorter than the tokens
+    assert cast(n=4, stride=4, cap=8, off=5) == E      # past the tail's end
+    assert cast(off=-1) == E
+    assert cast(sdt=9) == E
+    assert cast(dtype=_lib.DTYPE_F32) == E             # the tail is fp16 or bf16
+    assert cast(k=A + 8) == E                          # misaligned source
+    assert cast(k=None) == E
+    assert cast(rows=0) == OK                          # empty: no work
 
     def rope(q_stride=8 * 128, kv_stride=2 * 128, cs=128, b=2, cap=8, end=A, offset=0, dtype=F16, q=A):
         return lib.nsn_rope_append(q, A, A, q_stride, kv_stride, A, A, cs, b, 8, 2, A, A, A, cap, end, offset,
