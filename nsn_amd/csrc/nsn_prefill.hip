@@ -14,8 +14,9 @@
 // Workgroup = 8 waves = 256 consecutive chunk queries of one (b, q-head);
 // each wave owns 32 queries (two 16-query MFMA column tiles).  Per 64-token
 // block:
-//   1. the raw block (K/V codes, K/V min and scale, K/V decode factors) is
-//      staged into LDS by DMA two blocks ahead;
+//   1. the raw block (K/V codes, K/V min and scale, K/V decode factors; for
+//      a tail or chunk block its dense K/V rows) is staged into LDS by DMA
+//      two blocks ahead;
 //   2. the 512 threads dequantise it once for the workgroup (threads 0-255
 //      K', 256-511 V'^T) into K' [64 tok][128 ch] and V'^T [128 ch][64 tok]
 //      (the reconstructed values f_t * (m + s*z), rounded to the compute
@@ -183,6 +184,29 @@ __device__ __forceinline__ void stage_block(const PrefillParams &p, int64_t rk, 
     }
 }
 
+// A dense block (tail or chunk tokens, 2-byte elements) is staged by DMA
+// like a packed one: K rows then V rows, 256 B each.  The 16-byte chunk c of
+// row t sits at chunk position c ^ ((t >> 2) & 15) of the row, so that the
+// 16 lanes of either fill role's reads (one row, 16 chunks; or 16 rows 4
+// apart, one chunk) fall on 16 different bank groups.
+constexpr int kDenseStage = 2 * kBlockTok * kDim * 2;   // 32 KiB
+__device__ __forceinline__ int dswz(int t, int c) { return c ^ ((t >> 2) & 15); }
+
+// DMA of the first `valid` rows of a dense block (K rows from xk, V rows
+// from xv, 128-element row pitch) into a stage: instruction i writes rows
+// 4*(i%16) .. +3 of side i/16 and is issued by wave i % kWaves; lane l
+// writes chunk position l%16 of row l/16 and so reads chunk dswz(row, l%16).
+// Rows past `valid` are neither read nor written.
+__device__ __forceinline__ void stage_dense(const uint16_t *xk, const uint16_t *xv, int valid, int wave, int l,
+                                            uint8_t *st) {
+    const int r = l >> 4, cp = l & 15;
+    for (int i = wave; i < 32; i += kWaves) {
+        if (4 * (i & 15) >= valid) continue;   // (wave-uniform)
+        const int t = 4 * (i & 15) + r;
+        if (t < valid) dma16(((i < 16) ? xk : xv) + t * kDim + 8 * dswz(t, cp), st + 1024 * i);
+    }
+}
+
 // V'^T keeps each channel's 64 tokens in the k order of the PV product:
 // token t = 32a + 16h + 4g + i sits at position 32a + 8g + 4h + i, so the 8
 // tokens that lane group g of 32-token step a contracts (4g..4g+3 of both
@@ -196,12 +220,12 @@ struct KV {
     uint16_t *kt, *vt;
 };
 
-// Fill one side of a KV buffer from a dense token source x of dtype DT (row
-// pitch 128, `valid` rows; rows past it are zero), rounded to CT.  Thread:
-// tokens 4*rg .. 4*rg+3, channels 8*cg .. 8*cg+7; side 0 writes K' rows,
-// side 1 V'^T columns.
+// Fill one side of a KV buffer from a staged dense block of dtype DT
+// (`valid` rows; rows past it are zero), rounded to CT.  Thread: tokens
+// 4*rg .. 4*rg+3, channels 8*cg .. 8*cg+7; side 0 writes K' rows, side 1
+// V'^T columns.
 template <int BITS, int DT, int CT, int side>
-__device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg, int cg, const KV &kv) {
+__device__ __forceinline__ void fill_dense(const uint8_t *st, int valid, int rg, int cg, const KV &kv) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
     float vprev[8];
@@ -210,7 +234,7 @@ __device__ __forceinline__ void fill_dense(const uint16_t *x, int valid, int rg,
         const int t = 4 * rg + i;
         float f[8];
         if (t < valid) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(t) * kDim + 8 * cg);
+            const uint4 a = *reinterpret_cast<const uint4 *>(st + kDenseStage / 2 * side + 256 * t + 16 * dswz(t, cg));
             const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
@@ -309,7 +333,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     constexpr bool QPRE = DT == NSN_DTYPE_F16;   // fp16 queries carry scale*log2(e); bf16 ones stay exact
     __shared__ __align__(16) uint16_t kt[2][kBlockTok * kKP];
     __shared__ __align__(16) uint16_t vt[2][kDim * kVP];
-    __shared__ __align__(16) uint8_t stg[2][S::BYTES];
+    __shared__ __align__(16) uint8_t stg[2][S::BYTES > kDenseStage ? S::BYTES : kDenseStage];
 
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: the DMA targets are scalar)
@@ -406,22 +430,39 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             int64_t cpos;
             block_rows(j, valid, cpos);
             if (cpos < 0) {
-                const int64_t t0 = (j - nb) * kBlockTok;
-                if (side) fill_dense<BITS, TDT, DT, 1>(p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim, valid, rg, cg, kv);
-                else fill_dense<BITS, TDT, DT, 0>(p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim, valid, rg, cg, kv);
+                if (side) fill_dense<BITS, TDT, DT, 1>(stg[j & 1], valid, rg, cg, kv);
+                else fill_dense<BITS, TDT, DT, 0>(stg[j & 1], valid, rg, cg, kv);
             } else {
-                const uint16_t *src = (side ? p.vc : p.kc) + (seqrow * p.n_q + cpos) * kDim;
-                if (side) fill_dense<BITS, DT, DT, 1>(src, valid, rg, cg, kv);
-                else fill_dense<BITS, DT, DT, 0>(src, valid, rg, cg, kv);
+                if (side) fill_dense<BITS, DT, DT, 1>(stg[j & 1], valid, rg, cg, kv);
+                else fill_dense<BITS, DT, DT, 0>(stg[j & 1], valid, rg, cg, kv);
+            }
+        }
+    };
+    // Stage the raw data of block j into stage j & 1: packed codes and
+    // metadata, or the valid rows of its tail / chunk tokens.
+    auto stage = [&](int64_t j) {
+        if (j < nb) {
+            stage_block<BITS>(p, seqrow * p.k.block_cap + j, seqrow * p.v.block_cap + j, wave, l, stg[j & 1]);
+        } else {
+            int valid;
+            int64_t cpos;
+            block_rows(j, valid, cpos);
+            if (cpos < 0) {
+                const int64_t t0 = (j - nb) * kBlockTok;
+                stage_dense(p.k.tail + (seqrow * p.k.tail_cap + t0) * kDim,
+                            p.v.tail + (seqrow * p.v.tail_cap + t0) * kDim, valid, wave, l, stg[j & 1]);
+            } else {
+                stage_dense(p.kc + (seqrow * p.n_q + cpos) * kDim, p.vc + (seqrow * p.n_q + cpos) * kDim, valid,
+                            wave, l, stg[j & 1]);
             }
         }
     };
 
     // ---- prologue: raw block 0 staged and filled, raw block 1 in flight
-    if (nb > 0) stage_block<BITS>(p, seqrow * p.k.block_cap, seqrow * p.v.block_cap, wave, l, stg[0]);
+    stage(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (nb > 1) stage_block<BITS>(p, seqrow * p.k.block_cap + 1, seqrow * p.v.block_cap + 1, wave, l, stg[1]);
+    if (nblk > 1) stage(1);
     fill(0);
 
     // ---- one barrier per block: compute block j from KV buffer j & 1 while
@@ -431,9 +472,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         // and raw stage j & 1 are free
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (j + 2 < nb)
-            stage_block<BITS>(p, seqrow * p.k.block_cap + j + 2, seqrow * p.v.block_cap + j + 2, wave, l,
-                              stg[j & 1]);
+        if (j + 2 < nblk) stage(j + 2);
         if (j + 1 < nblk) fill(j + 1);
         if (qw >= p.n_q) continue;   // (a wave past the chunk end only helps fill)
         const bool packed = j < nb;
