@@ -278,9 +278,10 @@ SQ_NOTES = {
 }
 
 
-def _sq(d, kernel, first=None):
+def _sq(d, kernel, first=None, last=None):
     """Per-dispatch SQ/GRBM counter readings of one kernel from the sq1/sq2
-    passes (median over its dispatches; `first` keeps only the first ones)."""
+    passes (median over its dispatches; `first` / `last` keep only the first
+    or the last ones)."""
     vals = {}
     for sub in ("sq1", "sq2"):
         if not (Path(d) / sub).exists():
@@ -290,7 +291,9 @@ def _sq(d, kernel, first=None):
             if kernel in r["Kernel_Name"]:
                 per.setdefault(r["Counter_Name"], []).append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
         for c, v in per.items():
-            xs = sorted(x for _, x in (sorted(v)[:first] if first else v))
+            v = sorted(v)
+            v = v[:first] if first else (v[-last:] if last else v)
+            xs = sorted(x for _, x in v)
             vals[c] = xs[len(xs) // 2]
     return vals
 
@@ -317,7 +320,12 @@ def _sq_lines(sq, blocks_per_wave=None):
                  f"{sq['SQ_ACTIVE_INST_ANY'] / sq['SQ_WAVE_CYCLES']:.1%}, waiting "
                  f"{sq['SQ_WAIT_ANY'] / sq['SQ_WAVE_CYCLES']:.1%};")
         if "GRBM_GUI_ACTIVE" in sq:
-            L.append(f"- GPU-active cycles per XCD {sq['GRBM_GUI_ACTIVE'] / 8:.0f}.")
+            gui = sq["GRBM_GUI_ACTIVE"] / 8   # cycles of the dispatch (per XCD)
+            L.append(f"- GPU-active cycles per XCD {gui:.0f}"
+                     + (f"; MFMA busy {sq['SQ_VALU_MFMA_BUSY_CYCLES'] / (gui * 1024):.1%} of the 1024 SIMDs' cycles"
+                        if "SQ_VALU_MFMA_BUSY_CYCLES" in sq else "")
+                     + (f"; LDS bank-conflict cycles {sq['SQ_LDS_BANK_CONFLICT'] / (gui * 256):.1%} of the 256 CUs' "
+                        "cycles" if "SQ_LDS_BANK_CONFLICT" in sq else "") + ".")
     return L
 
 
@@ -891,8 +899,16 @@ STATS_DOC = {
            "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c3 --no-cpu"),
     "c4": ("prefill_c4", "C4: streaming cache, MHA 16 kv-heads, batch 32 -- 8192-token chunked prefill + decode steps",
            "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c4 "
-           "--slots 1 --decode-steps 16"),
+           "--slots 1 --decode-steps 16\n"
+           "rocprofv3 --pmc SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS "
+           "SQ_INSTS_SALU SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv -d OUT/sq1 -o sq1 -- python3 bench.py "
+           "--workload c4 --slots 1 --decode-steps 16\n"
+           "rocprofv3 --pmc SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS "
+           "SQ_VALU_MFMA_BUSY_CYCLES SQ_INST_LEVEL_VMEM SQ_LEVEL_WAVES --output-format csv -d OUT/sq2 -o sq2 -- "
+           "python3 bench.py --workload c4 --slots 1 --decode-steps 16"),
 }
+PREFILL_KERNEL = "nsn::prefill::prefill_kernel"
+PREFILL_LAST_CALLS = 7   # the last-chunk timing of main_c4: 2 warm-up + 5 timed prefill launches, the run's last
 
 
 ADAPTER = dict(layers=24, hidden=2048, heads=16, inter=5632, vocab=49152, B=32, T=8192, chunk=512)
@@ -1134,6 +1150,12 @@ def stats_summary(d, workload):
                  f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
                  f"{float(r['TotalDurationNs']) / 1e6:.2f} |")
     L.append("")
+    sq = _sq(d, PREFILL_KERNEL, last=PREFILL_LAST_CALLS) if workload == "c4" else {}
+    if sq:
+        L += ["## SQ counters of the prefill kernel on the last chunk (the sq1 and sq2 passes above)", "",
+              f"Median over the run's last {PREFILL_LAST_CALLS} prefill launches (context 7680 tokens + the 512-token "
+              "chunk: 119 packed blocks, 1 tail block and 4 or 8 chunk blocks per workgroup, 126 on average).", ""]
+        L += _sq_lines(sq, blocks_per_wave=126) + [""]
     (ROOT / "profiles" / f"{name}.md").write_text("\n".join(L))
     print("\n".join(L))
 
