@@ -72,6 +72,15 @@ __device__ __forceinline__ uint32_t pk(float a, float b) {
         return __builtin_bit_cast(uint32_t, h);
     }
 }
+// Maximum over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48),
+// on every lane, without LDS: v_permlane16_swap gives rows (0,0,2,2) and
+// (1,1,3,3), v_permlane32_swap the halves (lo,lo) and (hi,hi).
+__device__ __forceinline__ float rows4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float h16(uint32_t w, int hi) {
     return static_cast<float>(__builtin_bit_cast(half2v, w)[hi]);
 }
@@ -516,8 +525,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
                 mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qt][0], s[tt][qt][1]), fmaxf(s[tt][qt][2], s[tt][qt][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = rows4_max(mx);
             if (!QPRE) mx *= p.qscale;   // (bf16: the scores scale inside the exponent below)
             if (__builtin_amdgcn_ballot_w64(mx > m_run[qt])) {
                 const float mnew = fmaxf(m_run[qt], mx);
