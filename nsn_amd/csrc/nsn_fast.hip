@@ -177,7 +177,7 @@ struct FastParams {
     int64_t scores_cap;
     float *partials;
     int32_t *status;
-    int weighted;              // the grid is two waves per SIMD: weight first-slot waves 5:4
+    int weighted;              // slot weighting: 0 none, 1 two waves per SIMD (5:4), 2 six waves per CU (8:7)
 };
 
 // Reductions over the 16 lanes of a row with DPP (quad_perm [1,0,3,2],
@@ -973,15 +973,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int32_t P = static_cast<int32_t>(lo);
         const int32_t n_l = (nb_l + P - 1) / P;
         const int64_t wincl = H * static_cast<int64_t>(wave_incl_scan32(n_l));   // waves of sequences 0 .. l
-        // Wave index: even indices are the workgroups dispatched first
-        // (blockIdx < W/2: the first wave slot of every SIMD), odd ones the
-        // second; each stream's consecutive waves alternate between the two.
-        // The first-slot wave of a SIMD wins most issue conflicts with the
-        // other (measured: ~20% more blocks per unit time), so its ranges
-        // are longer by 5:4.
+        // Wave index w.  The workgroups dispatched first take the first wave
+        // slot of every SIMD; a second-slot wave shares its SIMD and loses
+        // most issue conflicts, so first-slot waves get longer ranges, and
+        // each stream's consecutive waves mix the slots:
+        //   8 waves per CU (weighted 1): blockIdx < W/2 are first-slot waves
+        //   at even w, the others at odd w; ranges 5:4 (measured: ~20 % more
+        //   blocks per unit time);
+        //   6 waves per CU (weighted 2; 4 SIMDs hold 4 first-slot and 2
+        //   second-slot waves): blockIdx < 2W/3 are first-slot waves at
+        //   w % 3 in {0, 1}, the others at w % 3 == 2; ranges 8:7 (measured:
+        //   2.71 against 3.09 us per block).
         const int64_t bx = blockIdx.x;
-        const bool wt = p.weighted && W % 2 == 0;
-        const int64_t w = !wt ? bx : (bx < W / 2) ? 2 * bx : 2 * (bx - W / 2) + 1;
+        const int wm = (p.weighted == 1 && W % 2 == 0) ? 1 : (p.weighted == 2 && W % 6 == 0) ? 2 : 0;
+        int64_t w = bx;
+        if (wm == 1) w = (bx < W / 2) ? 2 * bx : 2 * (bx - W / 2) + 1;
+        else if (wm == 2) w = (bx < 2 * W / 3) ? 3 * (bx >> 1) + (bx & 1) : 3 * (bx - 2 * W / 3) + 2;
         const uint64_t hit = __ballot(l < p.batch && wincl > w);
         if (!hit) return;   // a spare wave
         lane = __ffsll(static_cast<unsigned long long>(hit)) - 1;
@@ -990,9 +997,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         const int kvh = static_cast<int>(udivq(r, n));
         const int64_t k = r - kvh * n;
         const int64_t w0 = w - k;   // the stream's first wave
-        auto cw = [&](int64_t j) {   // summed weight of the stream's waves 0 .. j-1
-            const int64_t first = !wt ? 0 : (w0 + j + 1) / 2 - (w0 + 1) / 2;
-            return 5 * first + 4 * (j - first);
+        auto cw = [&](int64_t j) -> int64_t {   // summed weight of the stream's waves 0 .. j-1
+            if (wm == 1) {
+                const int64_t first = (w0 + j + 1) / 2 - (w0 + 1) / 2;   // even w in [w0, w0 + j)
+                return 5 * first + 4 * (j - first);
+            }
+            if (wm == 2) {
+                const int64_t second = (w0 + j) / 3 - w0 / 3;   // w % 3 == 2 in [w0, w0 + j)
+                return 8 * (j - second) + 7 * second;
+            }
+            return j;
         };
         // Cost units: a packed block 1, a block of dense fp16 tokens 3 (its
         // 32 KB per side are read without the prefetch pipeline).
@@ -1131,7 +1145,7 @@ int launch_attn_fast(const nsn_attn_args *a, hipStream_t st) {
     // as a second, mostly idle round.
     // (Measured on C3: 6 per CU 84 us, 4 or 5 per CU 87 us, 8 per CU 100 us.)
     const int per_cu = (a->bits == 3) ? 8 : 6;
-    p.weighted = per_cu == 8;
+    p.weighted = per_cu == 8 ? 1 : (per_cu == 6 ? 2 : 0);
     const dim3 grid(static_cast<unsigned>(per_cu * (cus[dev] > 0 ? cus[dev] : 256)));
     const bool bf = a->q_dtype == NSN_DTYPE_BF16;
 #define NSN_FAST_LAUNCH2(B_, Q_, S_, G_, T_) \
