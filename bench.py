@@ -1371,7 +1371,7 @@ def main():
         del kk, vv, q, ws, k, v
         torch.cuda.empty_cache()
         sub = argparse.Namespace(**vars(args))
-        sub.steps, sub.warmup, sub.slots, sub.decode_steps = 60, 20, 1, 32
+        sub.steps, sub.warmup, sub.slots, sub.decode_steps = 60, 500, 1, 32
         r3 = main_c3(sub, emit=False)
         result["c3"] = {"workload": r3["config"]["workload"], "step_us": r3["value"],
                         "split_kernel_us": r3["roofline"]["kernel_us"], "hbm_frac": r3["roofline"]["frac"],

@@ -353,9 +353,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     const int side = __builtin_amdgcn_readfirstlane(tid >> 8);   // (wave-uniform)
     const int rg = side ? (tid & 15) : ((tid >> 4) & 15);
     const int cg = side ? ((tid >> 4) & 15) : (tid & 15);
-    const int b = blockIdx.z, hq = blockIdx.y;
+    // Grid (q-head, sequence, query tile), tiles last and in reverse: every
+    // workgroup of the last (longest: it sees the most causal chunk blocks)
+    // tile is dispatched before any of the shorter ones, so the short ones
+    // fill the CUs' last rounds.
+    const int hq = blockIdx.x, b = blockIdx.y;
     const int kvh = hq / p.group;
-    const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQTile;
+    const int64_t q0 = static_cast<int64_t>(gridDim.z - 1 - blockIdx.z) * kQTile;
     const int64_t qw = q0 + 32 * wave;                     // this wave's first query
     const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
 
@@ -623,7 +627,7 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     for (const void *ptr : {static_cast<const void *>(a->q), a->k_chunk, a->v_chunk, static_cast<const void *>(a->out)})
         if (reinterpret_cast<uintptr_t>(ptr) & 15u) return NSN_EINVAL;
     const int64_t qt = (a->n_q + kQTile - 1) / kQTile;
-    if (qt > 0x7fffffff || a->heads_q > 65535 || a->batch > 65535) return NSN_EINVAL;
+    if (qt > 65535 || a->heads_q > 0x7fffffff || a->batch > 65535) return NSN_EINVAL;
     PrefillParams p{};
     p.q = static_cast<const uint16_t *>(a->q);
     p.batch = a->batch;
@@ -643,7 +647,7 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     p.vc = static_cast<const uint16_t *>(a->v_chunk);
     p.out = static_cast<uint16_t *>(a->out);
     p.status = a->status;
-    const dim3 grid(static_cast<unsigned>(qt), static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch));
+    const dim3 grid(static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch), static_cast<unsigned>(qt));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool bf = a->dtype == NSN_DTYPE_BF16;
 #define NSN_PREFILL_LAUNCH(B_, D_)                                                                              \
