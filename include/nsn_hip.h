@@ -200,6 +200,14 @@ typedef struct {
     int out_dtype;
     int32_t *status;
     int merge;              /* 1: also run the split merge; 0: partials only */
+    /* REFERENCE kernel only (nullable; NSN_ATTN_FAST rejects them): what the kernel itself
+       computed, for tokens t < seq_len[b] -- trace_scores [B, Hq, trace_cap] fp32 (the scaled
+       q.k, or the given logits) and trace_v [B, Hkv, trace_cap, 128] fp32 (the V rows as
+       restored and multiplied); trace_cap >= max_seq_len.  Replaces the TRACE stores of
+       experiments/ac08/source/loop_kv_vf01_kernel.py:104,113. */
+    float *trace_scores;
+    float *trace_v;
+    int64_t trace_cap;
 } nsn_attn_args;
 
 /*

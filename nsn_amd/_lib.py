@@ -49,7 +49,7 @@ class AttnArgs(ctypes.Structure):
                 ("k_mode", I32), ("k", KVSide), ("v", KVSide), ("scores", P), ("scores_cap", I64),
                 ("kernel", I32), ("kv_round_dtype", I32), ("split_tokens", I32), ("n_splits", I32),
                 ("partials", P), ("ctx", P), ("out", P), ("out_dtype", I32), ("status", P),
-                ("merge", I32)]
+                ("merge", I32), ("trace_scores", P), ("trace_v", P), ("trace_cap", I64)]
 
 
 class PrefillArgs(ctypes.Structure):

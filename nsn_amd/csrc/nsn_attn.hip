@@ -47,6 +47,8 @@ struct AttnParams {
     int64_t scores_cap;
     float *partials;
     int32_t *status;
+    float *trace_scores, *trace_v;   // nullable: the kernel's own scores and V rows
+    int64_t trace_cap;
 };
 
 template <int DT>
@@ -222,6 +224,8 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
                 if (t < valid) {
                     s = p.scores[(static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.scores_cap + t0 + t];
                     bad_attn |= !finite(s);
+                    if (p.trace_scores && t0 + t < p.trace_cap)
+                        p.trace_scores[(static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.trace_cap + t0 + t] = s;
                 }
                 sc_s[i] = s;
             }
@@ -245,6 +249,8 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
                     float s = ((part + o1) + o2) + o3;
                     s = s * p.scale;
                     if (r < valid) bad_attn |= !finite(s);
+                    if (r < valid && p.trace_scores && t0 + r < p.trace_cap)
+                        p.trace_scores[(static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.trace_cap + t0 + r] = s;
                     sc_s[h * kBlockTok + r] = (r < valid) ? s : -INFINITY;
                 }
             }
@@ -282,6 +288,11 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
             bad_in |= (fl & kBadInput) != 0;
         }
         __syncthreads();
+        if (p.trace_v)   // the V rows this block multiplies (row = b * Hkv + kv-head)
+            for (int i = tid; i < valid * kDim; i += 256) {
+                const int t = i / kDim, c = i - t * kDim;
+                if (t0 + t < p.trace_cap) p.trace_v[(row * p.trace_cap + t0 + t) * kDim + c] = tile[t * kXP + c];
+            }
 #pragma unroll
         for (int k = 0; k < kMaxGroup / 4; ++k) {
             const int h = wave + 4 * k;
@@ -464,6 +475,11 @@ int nsn_decode_attention(const nsn_attn_args *a, nsn_stream_t stream) {
     p.scores_cap = a->scores_cap;
     p.partials = a->partials;
     p.status = a->status;
+    const bool trace = a->trace_scores || a->trace_v;
+    if (trace && (a->kernel != NSN_ATTN_REFERENCE || a->trace_cap < a->max_seq_len)) return NSN_EINVAL;
+    p.trace_scores = a->trace_scores;
+    p.trace_v = a->trace_v;
+    p.trace_cap = a->trace_cap;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(a->n_splits), static_cast<unsigned>(a->heads_kv),
                     static_cast<unsigned>(a->batch));

@@ -113,7 +113,7 @@ def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
 def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
                      kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
                      scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True,
-                     static_workspace=False):
+                     static_workspace=False, trace_scores=None, trace_v=None):
     """Batched single-query decode attention.
 
     q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
@@ -123,6 +123,10 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     nsn_decode_attention_static: the partials live in the library's per-device
     scratch array (at most ``_lib.STATIC_SCRATCH_FLOATS`` floats), so with
     ``out``, ``ctx`` and ``status`` given the call allocates nothing.
+    ``trace_scores`` [B, Hq, cap] and ``trace_v`` [B, Hkv, cap, 128] (fp32,
+    cap >= max_seq_len; reference kernel only) receive what the kernel itself
+    computed for every token t < seq_len[b]: its scores and the V rows it
+    multiplied (the TRACE stores of loop_kv_vf01_kernel.py:104,113).
     """
     _dev.require_gpu(q, seq_len)
     require(q.ndim == 3 and q.shape[2] == DIM and q.is_contiguous(), "Query shape/type")
@@ -196,6 +200,19 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     a.out_dtype = _dev.dtype_code(out_dtype)
     a.status = st.data_ptr()
     a.merge = 1 if merge else 0
+    if trace_scores is not None or trace_v is not None:
+        require(kernel == "reference", "Trace outputs come from the exact-order kernel")
+        cap = (trace_scores if trace_scores is not None else trace_v).shape[2]
+        if trace_scores is not None:
+            require(trace_scores.dtype == torch.float32 and trace_scores.is_contiguous() and trace_scores.is_cuda
+                    and tuple(trace_scores.shape) == (B, Hq, cap), "Trace score shape/type")
+            a.trace_scores = trace_scores.data_ptr()
+        if trace_v is not None:
+            require(trace_v.dtype == torch.float32 and trace_v.is_contiguous() and trace_v.is_cuda
+                    and tuple(trace_v.shape) == (B, Hkv, cap, DIM), "Trace V shape/type")
+            a.trace_v = trace_v.data_ptr()
+        require(cap >= max_seq_len, "Trace capacity below max_seq_len")
+        a.trace_cap = cap
     entry = "nsn_decode_attention_static" if static_workspace else "nsn_decode_attention"
     rc = getattr(_lib.lib(), entry)(a, _dev.stream())
     _lib.check(rc, entry)
@@ -421,22 +438,31 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
     """Fused packed-K/V readout (loop_kv_vf01_kernel.py:128-139; GQA: loop_kv_nb06_kernel.py:142-154).
 
     Returns (out [1,1,Hq,128] bf16, context [1,Hq,1,128] fp32, score, v): score
-    and v are only produced with ``trace`` (computed from the exactly restored
-    K/V; the fused kernel itself keeps neither).  With ``status`` (an int32
-    device word) nothing is raised: the caller reads the NSN_ST_* bits.
+    [1,Hq,T] fp32 and v [1,Hkv,T,128] are only produced with ``trace``; the
+    exact-order kernel writes them itself (its scores and the V rows it
+    multiplied, loop_kv_vf01_kernel.py:104,113), for the fast kernel, which
+    keeps neither, they come from an exact restore.  With ``status`` (an
+    int32 device word) nothing is raised: the caller reads the NSN_ST_* bits.
     """
     Hq = q.shape[1]
     T = _length(g, kt)
     fast = kernel == "fast"
     ks, vs = _fast_sides(((g, kt), (vg, vt)), fast, status, q.device)
     seq = torch.full((1,), T, dtype=torch.int32, device=q.device)
+    Hkv = kt.shape[1]
+    tr_s = tr_v = None
+    if trace and not fast:
+        tr_s = torch.empty((1, Hq, T), dtype=torch.float32, device=q.device)
+        tr_v = torch.empty((1, Hkv, T, DIM), dtype=torch.float32, device=q.device)
     out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
-                                kv_round_dtype=kt.dtype, status=status)
+                                kv_round_dtype=kt.dtype, status=status, trace_scores=tr_s, trace_v=tr_v)
     score = vtr = None
-    if trace:
+    if trace and not fast:   # what the exact-order kernel itself computed
+        score, vtr = tr_s, tr_v.to(vt.dtype)
+    elif trace:   # the fast kernel keeps neither: the scores and V of an exact restore
         kk = restore_v(g, kt).float()
         vtr = restore_v(vg, vt)
-        G = Hq // kt.shape[1]
+        G = Hq // Hkv
         score = (torch.einsum("hd,htd->ht", q.reshape(Hq, DIM).float(), kk[0].repeat_interleave(G, 0)) * SCALE)[None]
     return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM), score, vtr
 
@@ -452,6 +478,49 @@ def _fast_sides(groups, fast, status, device):
             and _dev.read_status(st) & _lib.ST_NONFINITE_ATTN_INPUT:
         raise NumericalFailure("Nonfinite raw attention input (block metadata)")
     return sides
+
+
+def af_validate(g, tail, q):
+    """AF01 input checks before any launch (loop_kv_qk01_kernel.py:66-77):
+    tail [1,H,T,128] bf16 and query [1,H,1,128] bf16, contiguous, on the GPU,
+    a nonempty sequence, and every raw value finite (NumericalFailure).
+    Returns (heads, compressed tokens, total tokens)."""
+    require(tail.ndim == 4 and tail.shape[0] == 1 and tail.shape[-1] == DIM and tail.dtype == torch.bfloat16
+            and tail.is_contiguous(), "Tail shape/type")
+    h = tail.shape[1]
+    require(h > 0 and tuple(q.shape) == (1, h, 1, DIM) and q.dtype == torch.bfloat16 and q.is_contiguous(),
+            "Query shape/type")
+    _dev.require_gpu(q, tail)
+    compressed = 0
+    if g is not None:
+        b, gh, n, _ = g["codes"].shape
+        require(b == 1 and gh == h and g["codes"].device == tail.device, "Packed head/device mismatch")
+        compressed = n * BLOCK
+    require(tail.shape[-2] + compressed > 0, "Empty sequence")
+    values = [q, tail] + ([] if g is None else list(g["metas"]))
+    if not bool(torch.stack([torch.isfinite(x).all() for x in values]).all()):
+        raise NumericalFailure("Nonfinite QK input")
+    return h, compressed, compressed + tail.shape[-2]
+
+
+def validate_v(v, q, total):
+    """AF01 V check (loop_kv_af01_kernel.py:88-92): bf16 [1,H,total,128],
+    contiguous, on the query's GPU, finite."""
+    require(v.dtype == torch.bfloat16 and v.is_contiguous() and tuple(v.shape) == (1, q.shape[1], total, DIM),
+            "V shape/type")
+    _dev.require_gpu(v, q)
+    if not bool(torch.isfinite(v).all()):
+        raise NumericalFailure("Nonfinite V")
+
+
+def validate_score(score, v):
+    """AF01 score check (loop_kv_af01_kernel.py:94-98): fp32 [1,H,T] logits,
+    contiguous, on V's GPU, finite."""
+    require(score.dtype == torch.float32 and score.is_contiguous() and tuple(score.shape) == (1, v.shape[1], v.shape[2]),
+            "Score shape/type")
+    _dev.require_gpu(score, v)
+    if not bool(torch.isfinite(score).all()):
+        raise NumericalFailure("Nonfinite score")
 
 
 def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):

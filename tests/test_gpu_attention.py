@@ -211,6 +211,52 @@ def test_vf01_normal_fixtures_fused_equals_bridge_and_oracle():
         assert ok, (f["id"], err)
 
 
+def test_vf01_fused_trace_is_the_kernels_own():
+    """The fused route's trace is what the exact-order kernel itself computed
+    (the TRACE stores of loop_kv_vf01_kernel.py:104,113), over the 16 normal
+    fixtures: the traced V rows equal the exact restore bitwise, the traced
+    scores the fp64 q.k*scale of the restored K within fp32 rounding, and the
+    context is the fp64 softmax readout of the traced scores and V within the
+    reference's budget 2e-6 + 2e-6*sum_t|p_t v_t| (loop_kv_af01_contract.py:66-72,
+    applied to its traces as loop_kv_ac08_audit.py:41 does)."""
+    import json
+    from pathlib import Path
+    rec = json.loads((Path(__file__).parent / "golden" / "vf01_input_hashes.json").read_text())
+    for f in rec["fixtures"]:
+        a, data = _fixture_data(f)
+        g, kt, q, vg, vt = data
+        out, ctx, score, v = kernels.pipeline("V_FUSED", data, trace=True)
+        T = f["length"]
+        assert score.shape == (1, 2, T) and v.shape == (1, 2, T, 128)
+        assert torch.equal(v.view(torch.int16), kernels.restore_v(vg, vt).view(torch.int16)), f["id"]
+        k64 = kernels.restore_v(g, kt).float().cpu().numpy().astype(np.float64)[0]
+        q64 = q.float().cpu().numpy().astype(np.float64).reshape(2, 128)
+        gold_s = np.einsum("hd,htd->ht", q64, k64) * O.SCALE
+        s = score.cpu().numpy().astype(np.float64)[0]
+        s_scale = np.einsum("hd,htd->ht", np.abs(q64), np.abs(k64)) * O.SCALE
+        assert (np.abs(s - gold_s) <= 4e-6 * s_scale + 1e-7).all(), f["id"]
+        p = O.softmax64(s)
+        prod = p[..., None] * v.float().cpu().numpy().astype(np.float64)[0]
+        gold = prod.sum(-2)
+        err = np.abs(ctx.cpu().numpy().astype(np.float64).reshape(2, 128) - gold)
+        assert (err <= 2e-6 + 2e-6 * np.abs(prod).sum(-2)).all(), (f["id"], float(err.max()))
+
+
+def test_trace_outputs_only_on_the_exact_order_kernel():
+    """The fast kernel keeps no per-token scores: a trace request on it is an
+    argument error (NSN_EINVAL from the library, IntegrityError here)."""
+    from nsn_amd.errors import IntegrityError
+    T = 100
+    v = torch.randn(1, 1, T, 128, device=DEV).to(torch.float16)
+    vv = kernels.PackedKV(None, None, None, None, None, None, v, 3)
+    seq = torch.full((1,), T, dtype=torch.int32, device=DEV)
+    q = torch.randn(1, 1, 128, device=DEV).to(torch.bfloat16)
+    sc = torch.zeros(1, 1, T, device=DEV)
+    tr = torch.empty(1, 1, T, device=DEV)
+    with pytest.raises(IntegrityError):
+        kernels.decode_attention(q, None, vv, seq, scores=sc, kernel="fast", trace_scores=tr)
+
+
 @pytest.mark.parametrize("kernel", ["reference", "fast"])
 def test_score_input_readout_config1(kernel):
     """C1: B=1, 32q/8kv, 64 packed blocks + 37-token fp16 tail; logits N(0,1)*4."""
