@@ -329,7 +329,8 @@ int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t rows, int64
  * 0 for one row shared by all) exactly as transformers'
  * apply_rotary_pos_emb computes it in that dtype (x*cos and rotate_half(x)*sin
  * each rounded, then their sum), the rotated q written to q_out, and the
- * rotated k and v converted to fp16 and appended to the tails
+ * rotated k and v converted to the tails' `tail_dtype` (fp16 or bf16, round
+ * to nearest even) and appended to them
  * ([batch*heads_kv, tail_cap, 128]) at token *tail_end - 1 (device position,
  * as nsn_tail_append_to; NSN_ST_TAIL_RANGE outside [1, tail_cap]) or, with
  * tail_end NULL, at `offset`.  Replaces, for the packed decode route, the
@@ -340,7 +341,7 @@ int nsn_tail_append_to(const void *k_new, const void *v_new, int64_t rows, int64
 int nsn_rope_append(const void *q, const void *k, const void *v, int64_t q_stride, int64_t kv_stride,
                     const void *cos, const void *sin, int64_t cs_stride, int64_t batch, int64_t heads_q, int64_t heads_kv, void *q_out, void *k_tail,
                     void *v_tail, int64_t tail_cap, const int32_t *tail_end, int64_t offset, int dtype,
-                    int32_t *status, nsn_stream_t stream);
+                    int tail_dtype, int32_t *status, nsn_stream_t stream);
 
 /*
  * NaN/Inf scan over up to 16 arrays; array i sets bit i of flags[0] (int32)

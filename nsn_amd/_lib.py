@@ -84,7 +84,7 @@ SIGNATURES = {
     "nsn_tail_append": (I32, [P, P, I64, I64, I64, P, P, I64, I64, I32, P]),
     "nsn_tail_append_cast": (I32, [P, P, I32, I64, I64, I64, P, P, I64, I64, I32, P]),
     "nsn_tail_append_to": (I32, [P, P, I64, I64, I64, P, P, I64, P, I32, P, P]),
-    "nsn_rope_append": (I32, [P, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, I32, P, P]),
+    "nsn_rope_append": (I32, [P, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, I32, I32, P, P]),
     "nsn_kscore": (I32, [ctypes.POINTER(KScoreArgs), P]),
 }
 

@@ -133,16 +133,22 @@ class PackedKVCache(Cache):
 
     batch, max_tokens: sequences and the token capacity per slot;
     max_prefill: the longest single append (the prompt) before compression.
-    The packed side is ``bits``-bit NSN codes; the tail is fp16 (the fused
-    kernel's tail format; bf16 activations convert exactly in fp16's normal
-    range).
+    The packed side is ``bits``-bit NSN codes; the tail holds ``tail_dtype``
+    (fp16 or bf16; every kernel reads either).  fp16, the default, keeps 3
+    more mantissa bits, and bf16 activations convert to it exactly inside
+    fp16's normal range; a bf16 model whose keys or values can pass 65504
+    (fp16's largest finite value) takes ``tail_dtype=torch.bfloat16``, with
+    which appends, the packed prefill and the fused rotary append stay in
+    bf16 end to end.
     """
 
     nsn_connection = True
 
     def __init__(self, config, batch, max_tokens, *, loops=1, bits=3, arm="PACKED_KV_FUSED", max_prefill=512,
-                 strict=True, prefill="native", fused_rope=True, auto_policy=False, device=None):
+                 strict=True, prefill="native", fused_rope=True, auto_policy=False, tail_dtype=torch.float16,
+                 device=None):
         require(arm in ARMS, "Unknown connection arm")
+        require(tail_dtype in (torch.float16, torch.bfloat16), "Tail dtype (fp16 or bf16)")
         require(prefill in ("native", "packed") and (prefill == "native" or arm != "NATIVE"), "Prefill route")
         heads_q = config.num_attention_heads
         heads = getattr(config, "num_key_value_heads", None) or heads_q
@@ -164,8 +170,9 @@ class PackedKVCache(Cache):
         for i in range(self.n_layers):
             _refuse_window(config, i, max_tokens)
         self.config = config
+        self.tail_dtype = tail_dtype
         self.store = StreamingKVCache(self.n_layers * loops, batch, heads, max_tokens, bits=bits,
-                                      dtype=torch.float16, max_append=max(max_prefill, 1),
+                                      dtype=tail_dtype, max_append=max(max_prefill, 1),
                                       device=device or torch.device("cuda:0"))
         super().__init__(layers=[_PackedLayer(self, s) for s in range(self.n_layers * loops)])
         self.status = _dev.new_status(self.store.device)   # attention flags (strict=False)
@@ -206,7 +213,8 @@ class PackedKVCache(Cache):
         require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
                 and key.shape[3] == DIM, "Packed KV coordinates")
         self._policy(slot, key.shape[2])
-        self.store.append(slot, key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous())
+        # another 16-bit dtype converts inside the append kernel
+        self.store.append(slot, key.contiguous(), value.contiguous())
 
     def _check_position(self, slot, n, kwargs):
         pos = kwargs.get("cache_position")
@@ -233,8 +241,9 @@ class PackedKVCache(Cache):
         self._check_position(slot, key.shape[2], kwargs or {})
         require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
                 and key.shape[3] == DIM, "Packed KV coordinates")
-        q16 = q.to(torch.float16).contiguous()
-        k16, v16 = key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous()
+        dt = self.tail_dtype
+        q16 = q.to(dt).contiguous()
+        k16, v16 = key.to(dt).contiguous(), value.to(dt).contiguous()
         self._policy(slot, key.shape[2])
         has_ctx = self.store.length[slot] > 0
         out = kernels.prefill_attention(q16, self.store.side(slot, "K") if has_ctx else None,
@@ -251,8 +260,8 @@ class PackedKVCache(Cache):
         sequences at any stride -- slices of one fused QKV output), cos / sin
         [B or 1, 1, 128].  Returns
         the rotated q [B, Hq, 128]; the rotated key and the value go to the
-        tail as fp16 -- at the device tail end in device-position mode, else
-        at the host tail length (then counted)."""
+        tail in the tail dtype -- at the device tail end in device-position
+        mode, else at the host tail length (then counted)."""
         B, st = self.batch, self.store
         dt = q.dtype
         require(dt in (torch.bfloat16, torch.float16) and all(t.dtype == dt for t in (key, value, cos, sin)),
@@ -277,7 +286,7 @@ class PackedKVCache(Cache):
         rc = _lib.lib().nsn_rope_append(q.data_ptr(), key.data_ptr(), value.data_ptr(), q.stride(0), key.stride(0),
                                         cos.data_ptr(), sin.data_ptr(), cs_stride, B, self.heads_q, self.heads, q_out.data_ptr(), kt.data_ptr(),
                                         vt.data_ptr(), st.tail_cap, tail_end, offset, _dev.dtype_code(dt),
-                                        self.status.data_ptr(), _dev.stream())
+                                        _dev.dtype_code(self.tail_dtype), self.status.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_rope_append")
         if not self.graph_mode:
             st.advance(slot)
@@ -294,12 +303,12 @@ class PackedKVCache(Cache):
             return
         require(key.shape == value.shape and key.ndim == 4 and tuple(key.shape[:2]) == (self.batch, self.heads)
                 and key.shape[3] == DIM, "Packed KV coordinates")
-        k16, v16 = key.to(torch.float16).contiguous(), value.to(torch.float16).contiguous()
+        k16, v16 = key.to(self.tail_dtype).contiguous(), value.to(self.tail_dtype).contiguous()
         kt, vt = self.store.side(slot, "K").tail, self.store.side(slot, "V").tail
         n = key.shape[2]
         rc = _lib.lib().nsn_tail_append_to(k16.data_ptr(), v16.data_ptr(), self.batch * self.heads, n, n,
                                            kt.data_ptr(), vt.data_ptr(), self.store.tail_cap,
-                                           self.counters.data_ptr() + 4 * self.batch, _lib.DTYPE_F16,
+                                           self.counters.data_ptr() + 4 * self.batch, _dev.dtype_code(self.tail_dtype),
                                            self.status.data_ptr(), _dev.stream())
         _lib.check(rc, "nsn_tail_append_to")
 
@@ -354,7 +363,7 @@ class PackedKVCache(Cache):
             L, seq = self.cap_len, self.counters[:self.batch]
         kw = dict(max_seq_len=L, scale=scale, check=self.strict, status=None if self.strict else self.status)
         if self.arm == "PACKED_GROUPED":
-            vd = PackedKV(None, None, None, None, None, None, self.materialize(slot, "V", torch.float16), kside.bits)
+            vd = PackedKV(None, None, None, None, None, None, self.materialize(slot, "V", self.tail_dtype), kside.bits)
             kw.update(kernel="fast", workspace=self._workspace(L))
             out, _ = kernels.decode_attention(q, kside, vd, seq, **kw)
         elif self.arm == "PACKED_KV_FUSED":

@@ -92,13 +92,14 @@ struct RopeParams {
     const int32_t *tail_end;
     int64_t offset;
     int32_t *status;
+    int tail_bf16;   // tails hold bf16 (else fp16)
 };
 
 // One decode token per sequence: rotary embedding of q and k as transformers'
 // apply_rotary_pos_emb computes it in the model dtype DT (x*cos and
 // rotate_half(x)*sin each rounded to DT, then their sum rounded to DT), the
-// rotated q written out, and the rotated k and the plain v converted to fp16
-// and appended to the tails.  16 threads per row (q rows, then k rows, then v
+// rotated q written out, and the rotated k and the plain v converted to the
+// tails' fp16 or bf16 and appended to them.  16 threads per row (q rows, then k rows, then v
 // rows); thread j owns the channel pairs (c, c + 64) for c = 4j .. 4j + 3.
 template <int DT>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
@@ -161,8 +162,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
         dst = (kind == 1 ? p.k_tail : p.v_tail) + (r * p.tail_cap + off) * kDim;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            h1[j] = f32_to_f16_bits(o1[j]);
-            h2[j] = f32_to_f16_bits(o2[j]);
+            h1[j] = p.tail_bf16 ? f32_to_bf16_bits(o1[j]) : f32_to_f16_bits(o1[j]);
+            h2[j] = p.tail_bf16 ? f32_to_bf16_bits(o2[j]) : f32_to_f16_bits(o2[j]);
         }
     }
     *reinterpret_cast<uint2 *>(dst + c0) = make_uint2(h1[0] | (static_cast<uint32_t>(h1[1]) << 16),
@@ -251,12 +252,13 @@ extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, int6
                                const void *cos, const void *sin, int64_t cs_stride, int64_t batch, int64_t heads_q,
                                int64_t heads_kv, void *q_out, void *k_tail,
                                void *v_tail, int64_t tail_cap, const int32_t *tail_end, int64_t offset, int dtype,
-                               int32_t *status, nsn_stream_t stream) {
+                               int tail_dtype, int32_t *status, nsn_stream_t stream) {
     if (batch < 0 || heads_q < 0 || heads_kv < 0 || tail_cap < 1 || (cs_stride != 0 && cs_stride < kDim))
         return NSN_EINVAL;
     if (q_stride < heads_q * kDim || kv_stride < heads_kv * kDim || (q_stride & 3) || (kv_stride & 3))
         return NSN_EINVAL;
     if (dtype != NSN_DTYPE_F16 && dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
+    if (tail_dtype != NSN_DTYPE_F16 && tail_dtype != NSN_DTYPE_BF16) return NSN_EINVAL;
     if (!tail_end && (offset < 0 || offset >= tail_cap)) return NSN_EINVAL;
     if (batch == 0 || heads_q + heads_kv == 0) return NSN_OK;
     if (!q || !k || !v || !cos || !sin || !q_out || !k_tail || !v_tail || !status) return NSN_EINVAL;
@@ -270,7 +272,7 @@ extern "C" int nsn_rope_append(const void *q, const void *k, const void *v, int6
                  static_cast<const uint16_t *>(cos), static_cast<const uint16_t *>(sin), cs_stride, q_stride, kv_stride,
                  batch, heads_q, heads_kv,
                  static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_tail), static_cast<uint16_t *>(v_tail),
-                 tail_cap, tail_end, offset, status};
+                 tail_cap, tail_end, offset, status, tail_dtype == NSN_DTYPE_BF16 ? 1 : 0};
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (dtype == NSN_DTYPE_BF16) hipLaunchKernelGGL(rope_append_kernel<NSN_DTYPE_BF16>, dim3(blocks), dim3(256), 0, st, p);
     else hipLaunchKernelGGL(rope_append_kernel<NSN_DTYPE_F16>, dim3(blocks), dim3(256), 0, st, p);

@@ -25,6 +25,7 @@ from oracle import oracle as O  # noqa: E402
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 B, P, STEPS = 2, 150, 60
+F16, BF16 = torch.float16, torch.bfloat16
 
 
 def model(family="llama"):
@@ -119,16 +120,19 @@ def forced_logits(m, cache, ids, tokens):
     return torch.stack(outs)
 
 
-@pytest.mark.parametrize("family,arm", [("llama", "PACKED_KV_FUSED"), ("llama", "PACKED_GROUPED"),
-                                        ("llama", "PACKED_KV_EXACT"), ("qwen3", "PACKED_KV_FUSED"),
-                                        ("qwen2", "PACKED_KV_FUSED")])
-def test_arms_agree_with_native(family, arm):
+@pytest.mark.parametrize("family,arm,tail_dtype", [("llama", "PACKED_KV_FUSED", F16), ("llama", "PACKED_GROUPED", F16),
+                                                   ("llama", "PACKED_KV_EXACT", F16), ("qwen3", "PACKED_KV_FUSED", F16),
+                                                   ("qwen2", "PACKED_KV_FUSED", F16), ("llama", "PACKED_KV_FUSED", BF16),
+                                                   ("llama", "PACKED_GROUPED", BF16), ("llama", "PACKED_KV_EXACT", BF16)])
+def test_arms_agree_with_native(family, arm, tail_dtype):
     m, cfg, ids = model(family)
     tokens = torch.randint(0, 256, (B, 40), generator=torch.Generator().manual_seed(2)).to(DEV)
     restore = adapter.install(m)
     try:
-        ref = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm="NATIVE", max_prefill=P), ids, tokens)
-        got = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm=arm, max_prefill=P), ids, tokens)
+        ref = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm="NATIVE", max_prefill=P, tail_dtype=tail_dtype),
+                            ids, tokens)
+        got = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm=arm, max_prefill=P, tail_dtype=tail_dtype),
+                            ids, tokens)
     finally:
         restore()
     assert torch.equal(got[0], ref[0])                    # the prefill is the native route in every arm
@@ -138,16 +142,20 @@ def test_arms_agree_with_native(family, arm):
     assert err <= 1e-2 * ref.abs().max().item() + 1e-3, err
 
 
-def test_native_arm_prefill_matches_unpatched_model():
+@pytest.mark.parametrize("tail_dtype", [F16, BF16])
+def test_native_arm_prefill_matches_unpatched_model(tail_dtype):
     m, cfg, ids = model()
     with torch.no_grad():
         ref = m(input_ids=ids).logits
         restore = adapter.install(m)
         try:
-            cache = adapter.PackedKVCache(cfg, B, 1024, arm="NATIVE", max_prefill=P)
+            cache = adapter.PackedKVCache(cfg, B, 1024, arm="NATIVE", max_prefill=P, tail_dtype=tail_dtype)
             got = m(input_ids=ids, past_key_values=cache, use_cache=True).logits
         finally:
             restore()
+    if tail_dtype == BF16:   # the model's own K/V stored and read back unchanged
+        assert torch.equal(got, ref)
+        return
     # the prefill appends bf16 K/V to the fp16 tail and reads them back:
     # exact down to 2^-17 (fp16 subnormal spacing 2^-24 against bf16's 8-bit
     # significand), so only the rare K/V element below that moves, by < 2^-24
@@ -245,6 +253,53 @@ def test_strict_decode_raises_on_nonfinite_tail():
         restore()
 
 
+@pytest.mark.parametrize("tail_dtype", [F16, BF16])
+def test_values_past_fp16_range_compute_on_bf16_tails(tail_dtype):
+    """Layer 0's value projection scaled by 1e5 after the prefill puts the
+    decode tokens' V past 65504, fp16's largest finite value.  On fp16 tails
+    they become Inf and the strict decode step raises NumericalFailure; on
+    bf16 tails they are kept as the model computed them, and every decode
+    step of the fused arm (fused rotary append into the bf16 tail, bf16 MFMA
+    over the tail, packed blocks from the prompt) meets the oracle, with the
+    tolerance's absolute term scaled by the slot's largest |V|."""
+    from nsn_amd.errors import NumericalFailure
+    m, cfg, ids = model()
+    cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P, tail_dtype=tail_dtype)
+    scale = m.model.layers[0].self_attn.scaling
+    seen = []
+
+    def capture(slot, total, q, out):
+        k, v = slot_kv_oracle(cache, slot)
+        ref, _ = O.decode_attention64(q.float().cpu().numpy(), k, v, scale=scale)
+        vmax = float(np.abs(v).max())
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert np.all(err <= 2e-3 * max(1.0, vmax) + 1e-2 * np.abs(ref)), (slot, total, float(err.max()))
+        seen.append((slot, vmax))
+
+    restore = adapter.install(m)
+    try:
+        with torch.no_grad():
+            out = m(input_ids=ids, past_key_values=cache, use_cache=True)
+            cache.post_prefill()
+            m.model.layers[0].self_attn.v_proj.weight.mul_(1e5)
+            nxt = out.logits[:, -1:].argmax(-1)
+            if tail_dtype == F16:
+                with pytest.raises(NumericalFailure):
+                    m(input_ids=nxt, past_key_values=cache, use_cache=True)
+                return
+            cache.capture = capture
+            for _ in range(20):
+                out = m(input_ids=nxt, past_key_values=cache, use_cache=True)
+                cache.post_decode()
+                nxt = out.logits[:, -1:].argmax(-1)
+            assert torch.isfinite(out.logits).all()
+        cache.check_status()
+    finally:
+        restore()
+    assert len(seen) == 40 and cache.store.compressed == [64, 64]
+    assert max(vm for s, vm in seen if s == 0) > 65504 > max(vm for s, vm in seen if s == 1)
+
+
 def test_check_status_reports_a_tail_range_flag():
     """A device-position step whose tail end was pushed past the tail
     capacity (from the host) appends nothing; check_status raises
@@ -270,8 +325,8 @@ def test_check_status_reports_a_tail_range_flag():
         restore()
 
 
-@pytest.mark.parametrize("family", ["llama", "qwen3"])
-def test_packed_prefill_is_as_accurate_as_the_native_route(family):
+@pytest.mark.parametrize("family,tail_dtype", [("llama", F16), ("qwen3", F16), ("llama", BF16)])
+def test_packed_prefill_is_as_accurate_as_the_native_route(family, tail_dtype):
     """A 600-token prompt in chunks of 200 (compressed after each), then 20
     forced decode steps.  The packed prefill route (chunk queries attend the
     packed context on the fp16 MFMA prefill kernel) and the reference's
@@ -279,7 +334,8 @@ def test_packed_prefill_is_as_accurate_as_the_native_route(family):
     truth is the same model in fp32 through the NATIVE arm (fp32 restore of
     the same packed storage, fp32 sdpa).  The packed route's logits must be
     no further from the truth than 1.5x the native route's, and layer 0's
-    packed blocks (independent of any attention) are bitwise equal."""
+    packed blocks (independent of any attention) are bitwise equal.  With
+    bf16 tails the chunk's products run on bf16 MFMA tiles."""
     prompt = torch.randint(0, 256, (B, 600), generator=torch.Generator().manual_seed(4)).to(DEV)
     tokens = torch.randint(0, 256, (B, 20), generator=torch.Generator().manual_seed(5)).to(DEV)
     runs = {}
@@ -291,7 +347,8 @@ def test_packed_prefill_is_as_accurate_as_the_native_route(family):
             m = m.float()
         restore = adapter.install(m)
         try:
-            cache = adapter.PackedKVCache(cfg, B, 1024, arm=arm, max_prefill=200, prefill=route)
+            cache = adapter.PackedKVCache(cfg, B, 1024, arm=arm, max_prefill=200, prefill=route,
+                                          tail_dtype=tail_dtype)
             logits = []
             with torch.no_grad():
                 for c in range(3):
@@ -389,13 +446,15 @@ def test_looped_model_slots_vs_oracle_and_graph():
         restore()
 
 
+@pytest.mark.parametrize("tail_dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shared_rows,fused", [(True, False), (False, False), (False, True)])
-def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows, fused):
+def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows, fused, tail_dtype):
     """nsn_rope_append against transformers' own apply_rotary_pos_emb (Llama
-    rotary, the model dtype's rounding) and a plain fp16 cast of k and v:
-    the rotated q and the appended tail rows are bit-identical, at a host
-    offset and at a device tail end; other tail rows stay untouched."""
+    rotary, the model dtype's rounding) and a plain cast of k and v to the
+    tail dtype (fp16 or bf16): the rotated q and the appended tail rows are
+    bit-identical, at a host offset and at a device tail end; other tail rows
+    stay untouched."""
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding, apply_rotary_pos_emb
     from nsn_amd import _dev, _lib
     lib = _lib.lib()
@@ -418,7 +477,7 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows, fus
                                   k.reshape(b_, 1, hkv, 128).transpose(1, 2), cos, sin)
     for device_end in (False, True):
         q_out = torch.empty((b_, hq, 128), dtype=dtype, device=DEV)
-        kt = torch.zeros((b_ * hkv, cap, 128), dtype=torch.float16, device=DEV)
+        kt = torch.zeros((b_ * hkv, cap, 128), dtype=tail_dtype, device=DEV)
         vt = torch.zeros_like(kt)
         st = _dev.new_status(DEV)
         end_t = torch.tensor([5], dtype=torch.int32, device=DEV)
@@ -426,11 +485,11 @@ def test_rope_append_matches_transformers_rotary_bitwise(dtype, shared_rows, fus
                                  sin.data_ptr(),
                                  0 if shared_rows else 128, b_, hq, hkv, q_out.data_ptr(), kt.data_ptr(), vt.data_ptr(),
                                  cap, end_t.data_ptr() if device_end else None, 4, _dev.dtype_code(dtype),
-                                 st.data_ptr(), _dev.stream())
+                                 _dev.dtype_code(tail_dtype), st.data_ptr(), _dev.stream())
         assert rc == 0 and _dev.read_status(st) == 0
         assert torch.equal(q_out.view(torch.int16), qr[:, :, 0].contiguous().view(torch.int16))
-        want_k = kr[:, :, 0].to(torch.float16).reshape(b_ * hkv, 128)
-        want_v = v.reshape(b_ * hkv, 128).to(torch.float16)
+        want_k = kr[:, :, 0].to(tail_dtype).reshape(b_ * hkv, 128)
+        want_v = v.reshape(b_ * hkv, 128).to(tail_dtype)
         assert torch.equal(kt[:, 4].view(torch.int16), want_k.view(torch.int16))
         assert torch.equal(vt[:, 4].view(torch.int16), want_v.view(torch.int16))
         rest = torch.ones(cap, dtype=torch.bool)

@@ -76,13 +76,14 @@ def test_device_position_appends_reject_bad_arguments_without_gpu_work():
     assert cast(k=None) == E
     assert cast(rows=0) == OK                          # empty: no work
 
-    def rope(q_stride=8 * 128, kv_stride=2 * 128, cs=128, b=2, cap=8, end=A, offset=0, dtype=F16, q=A):
+    def rope(q_stride=8 * 128, kv_stride=2 * 128, cs=128, b=2, cap=8, end=A, offset=0, dtype=F16, q=A, tdt=F16):
         return lib.nsn_rope_append(q, A, A, q_stride, kv_stride, A, A, cs, b, 8, 2, A, A, A, cap, end, offset,
-                                   dtype, A, None)
+                                   dtype, tdt, A, None)
     assert rope(cs=64) == E                            # cos/sin rows overlap
     assert rope(q_stride=8 * 128 - 4) == E             # q rows overlap
     assert rope(kv_stride=2 * 128 + 2) == E            # 8-byte row alignment
     assert rope(dtype=_lib.DTYPE_F32) == E
+    assert rope(tdt=_lib.DTYPE_F32) == E              # tails are fp16 or bf16
     assert rope(end=None, offset=8) == E               # host offset past the tail
     assert rope(cap=0) == E
     assert rope(q=A + 4) == E
