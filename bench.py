@@ -798,8 +798,7 @@ def main_c4(args, emit=True):
     def prefill_slot(s):
         for c in range(nchunks):
             qc, kc, vc = acts[c]
-            cache.prefill(s, qc, kc, vc, check=False)
-            cache.append(s, kc, vc)
+            cache.prefill(s, qc, kc, vc, check=False, append=True)   # attention + the chunk's append
             cache.compress_to(s, max(cache.compressed[s], ((cache.length[s] - 64) // 64) * 64))
     prefill_slot(0)   # untimed warm-up: one slot's whole prefill, then the slot is emptied again
     cache.reset(0)

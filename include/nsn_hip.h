@@ -257,15 +257,23 @@ int nsn_decode_attention_static(const nsn_attn_args *args, nsn_stream_t stream);
  * the sequence's context -- k.blocks[b] packed blocks, then ctx_len[b] -
  * 64*blocks[b] tail tokens -- and the chunk's own K/V causally (chunk query i
  * sees chunk tokens 0..i).  Packed blocks are dequantised tile by tile into
- * LDS (direction m + s*z times the decode factor, fp16) and never reach HBM
- * densely; QK^T and PV run on fp16 MFMA with fp32 accumulation and an online
- * log2-domain softmax.  Replaces the reference's prefill route: materialise
- * every packed block and the tail (PackedCache.materialize / update,
+ * LDS (direction m + s*z times the decode factor, in the compute dtype) and
+ * never reach HBM densely; QK^T and PV run on MFMA in the compute dtype
+ * (`dtype`: fp16 or bf16) with fp32 accumulation and an online log2-domain
+ * softmax.  Replaces the reference's prefill route: materialise every packed
+ * block and the tail (PackedCache.materialize / update,
  * experiments/ac08/source/loop_kv_pk01_cache.py:87-106, restore_group :40-42)
  * followed by dense attention over the materialised K/V.
+ * append != 0 also performs the chunk's cache update (the tail concatenation
+ * of PackedCache.update, loop_kv_pk01_cache.py:101-102) in the same launch:
+ * the chunk's K/V rows go to rows ctx_len[b] - 64*k.blocks[b] .. + n_q - 1
+ * of k.tail / v.tail (write access granted by the caller), rounded to the
+ * tail dtype -- what nsn_tail_append_cast writes.  Needs both tails; a
+ * sequence whose tail lacks the room raises NSN_ST_CAPACITY and is not
+ * appended.
  * Needs k.blocks and v.blocks equal per sequence (or both NULL), decode
- * factors, 16-byte aligned arrays, and one dtype (fp16 or bf16) for q, the
- * chunk K/V, the tails and out.
+ * factors, 16-byte aligned arrays, one dtype for q, the chunk K/V and out,
+ * and one tail dtype (fp16 or bf16) for both tails.
  */
 typedef struct {
     const void *q;          /* [B, Hq, n_q, 128] dtype */
@@ -278,7 +286,8 @@ typedef struct {
     const void *k_chunk;    /* [B, Hkv, n_q, 128] dtype: the chunk's own K */
     const void *v_chunk;    /* [B, Hkv, n_q, 128] dtype */
     void *out;              /* [B, Hq, n_q, 128] dtype */
-    int32_t *status;        /* NSN_ST_NONFINITE_OUTPUT; NSN_ST_NONFINITE_ATTN on an inconsistent cache */
+    int32_t *status;        /* NSN_ST_NONFINITE_OUTPUT; NSN_ST_CAPACITY on an inconsistent cache or no room to append */
+    int append;             /* 1: also append the chunk's K/V to the tails (see above) */
 } nsn_prefill_args;
 
 int nsn_prefill_attention(const nsn_prefill_args *args, nsn_stream_t stream);

@@ -245,12 +245,9 @@ class PackedKVCache(Cache):
         q16 = q.to(dt).contiguous()
         k16, v16 = key.to(dt).contiguous(), value.to(dt).contiguous()
         self._policy(slot, key.shape[2])
-        has_ctx = self.store.length[slot] > 0
-        out = kernels.prefill_attention(q16, self.store.side(slot, "K") if has_ctx else None,
-                                        self.store.side(slot, "V") if has_ctx else None, self.store.lengths(slot),
-                                        k16, v16, scale=scale, check=self.strict,
-                                        status=None if self.strict else self.status)
-        self.store.append(slot, k16, v16)
+        # the chunk's append to the tail happens inside the prefill launch
+        out = self.store.prefill(slot, q16, k16, v16, append=True, scale=scale, check=self.strict,
+                                 status=None if self.strict else self.status)
         return out.to(q.dtype)
 
     def rope_append(self, slot, q, key, value, cos, sin, kwargs=None):

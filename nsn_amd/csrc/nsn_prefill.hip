@@ -149,6 +149,7 @@ struct PrefillParams {
     const uint16_t *kc, *vc;   // chunk K/V [B, Hkv, n_q, 128] DT
     uint16_t *out;             // [B, Hq, n_q, 128] DT
     int32_t *status;
+    uint16_t *ka, *va;         // append: the K / V tails written (TDT), else null
 };
 
 #pragma clang diagnostic push
@@ -232,9 +233,11 @@ struct KV {
 // Fill one side of a KV buffer from a staged dense block of dtype DT
 // (`valid` rows; rows past it are zero), rounded to CT.  Thread: tokens
 // 4*rg .. 4*rg+3, channels 8*cg .. 8*cg+7; side 0 writes K' rows, side 1
-// V'^T columns.
-template <int BITS, int DT, int CT, int side>
-__device__ __forceinline__ void fill_dense(const uint8_t *st, int valid, int rg, int cg, const KV &kv) {
+// V'^T columns.  `app` (nullable): the block's rows also go to app + t*128,
+// rounded to ADT (the chunk's append to the tail).
+template <int BITS, int DT, int CT, int side, int ADT>
+__device__ __forceinline__ void fill_dense(const uint8_t *st, int valid, int rg, int cg, const KV &kv,
+                                           uint16_t *app) {
     using O = Order<BITS>;
     uint32_t vcol[8][2];   // V'^T: per channel, tokens 4rg..4rg+3 as 2 fp16 pairs
     float vprev[8];
@@ -247,6 +250,14 @@ __device__ __forceinline__ void fill_dense(const uint8_t *st, int valid, int rg,
             const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = Elem<DT>::load(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
+            if (app) {
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o[e] = static_cast<uint32_t>(Elem<ADT>::store(f[2 * e])) |
+                           (static_cast<uint32_t>(Elem<ADT>::store(f[2 * e + 1])) << 16);
+                *reinterpret_cast<uint4 *>(app + t * kDim + 8 * cg) = uint4{o[0], o[1], o[2], o[3]};
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = 0.f;
@@ -376,6 +387,12 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         if (tid == 0) raise_status(p.status, NSN_ST_CAPACITY);   // inconsistent cache (host checks first)
         return;
     }
+    // append: the workgroup of the last query tile (it stages every chunk
+    // block) of each kv-head's first q-head writes the chunk's K/V to tail
+    // rows ntail .. ntail + n_q - 1 as it fills them; no room: flag, no append
+    const bool app_wg = p.ka && blockIdx.z == 0 && hq % p.group == 0;
+    const bool app_ok = app_wg && ntail + p.n_q <= p.k.tail_cap && ntail + p.n_q <= p.v.tail_cap;
+    if (app_wg && !app_ok && tid == 0) raise_status(p.status, NSN_ST_CAPACITY);
 
     // ---- Q fragments (B operand of S^T = K' Q^T): query qw + 16*qt + row,
     // channels 32*ks + 8*g + chE[e] (fp16: times scale*log2(e))
@@ -443,11 +460,15 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             int64_t cpos;
             block_rows(j, valid, cpos);
             if (cpos < 0) {
-                if (side) fill_dense<BITS, TDT, DT, 1>(stg[j & 1], valid, rg, cg, kv);
-                else fill_dense<BITS, TDT, DT, 0>(stg[j & 1], valid, rg, cg, kv);
+                if (side) fill_dense<BITS, TDT, DT, 1, TDT>(stg[j & 1], valid, rg, cg, kv, nullptr);
+                else fill_dense<BITS, TDT, DT, 0, TDT>(stg[j & 1], valid, rg, cg, kv, nullptr);
             } else {
-                if (side) fill_dense<BITS, DT, DT, 1>(stg[j & 1], valid, rg, cg, kv);
-                else fill_dense<BITS, DT, DT, 0>(stg[j & 1], valid, rg, cg, kv);
+                uint16_t *app = nullptr;
+                if (app_ok)
+                    app = side ? p.va + (seqrow * p.v.tail_cap + ntail + cpos) * kDim
+                               : p.ka + (seqrow * p.k.tail_cap + ntail + cpos) * kDim;
+                if (side) fill_dense<BITS, DT, DT, 1, TDT>(stg[j & 1], valid, rg, cg, kv, app);
+                else fill_dense<BITS, DT, DT, 0, TDT>(stg[j & 1], valid, rg, cg, kv, app);
             }
         }
     };
@@ -617,6 +638,7 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     };
     if (!side_ok(a->k) || !side_ok(a->v)) return NSN_EINVAL;
     if (!a->k.blocks != !a->v.blocks) return NSN_EINVAL;
+    if (a->append && (!a->k.tail || !a->v.tail || a->k.tail_cap <= 0 || a->v.tail_cap <= 0)) return NSN_EINVAL;
     auto tail_ok = [](const nsn_kv_side &s) {
         return !s.tail || s.tail_dtype == NSN_DTYPE_F16 || s.tail_dtype == NSN_DTYPE_BF16;
     };
@@ -647,6 +669,10 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     p.vc = static_cast<const uint16_t *>(a->v_chunk);
     p.out = static_cast<uint16_t *>(a->out);
     p.status = a->status;
+    if (a->append) {   // the caller grants write access to the tails' rows past the context
+        p.ka = static_cast<uint16_t *>(const_cast<void *>(a->k.tail));
+        p.va = static_cast<uint16_t *>(const_cast<void *>(a->v.tail));
+    }
     const dim3 grid(static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch), static_cast<unsigned>(qt));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool bf = a->dtype == NSN_DTYPE_BF16;

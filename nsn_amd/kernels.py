@@ -230,7 +230,7 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
 
 
 def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, k_chunk, v_chunk, *, scale=SCALE,
-                      status=None, check=True, out=None):
+                      status=None, check=True, out=None, append=False):
     """Chunked-prefill attention over a packed context (C4's prefill step).
 
     q [B, Hq, n, 128]; k_chunk, v_chunk [B, Hkv, n, 128] (the chunk's own K/V;
@@ -240,7 +240,11 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     64*blocks[b]`` tail tokens of k/v (None: no context) -- and chunk tokens
     0..i.  Returns out [B, Hq, n, 128].  The reference materialises the
     packed blocks and runs dense attention instead
-    (loop_kv_pk01_cache.py:87-106).
+    (loop_kv_pk01_cache.py:87-106).  ``append=True`` also writes the
+    chunk's K/V into the tails right after each sequence's context tokens
+    (rounded to the tail dtype), in the same launch: the cache update
+    (loop_kv_pk01_cache.py:101-102) that otherwise follows as a separate
+    append; k and v must then carry tails with room for n more tokens.
     """
     _dev.require_gpu(q, k_chunk, v_chunk, ctx_len)
     require(q.ndim == 4 and q.shape[3] == DIM and q.is_contiguous(), "Query shape/type")
@@ -280,6 +284,13 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
         a.v = v.side()
     elif check:
         require(bool((ctx_len == 0).all()), "Context lengths without a context")
+    if append:
+        require(k is not None and k.tail is not None and v.tail is not None, "Append needs both tails")
+        if check:
+            L = ctx_len.cpu().numpy().astype(np.int64)
+            nb = k.blocks.cpu().numpy().astype(np.int64) if k.codes is not None else np.zeros_like(L)
+            require(np.all(L - BLOCK * nb + n <= min(k.tail.shape[2], v.tail.shape[2])),
+                    "Tail overflow: compress before appending more tokens")
     if out is None:
         out = torch.empty_like(q)
     st = status if status is not None else _dev.new_status(q.device)
@@ -293,12 +304,14 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     a.v_chunk = v_chunk.data_ptr()
     a.out = out.data_ptr()
     a.status = st.data_ptr()
+    a.append = 1 if append else 0
     rc = _lib.lib().nsn_prefill_attention(a, _dev.stream())
     _lib.check(rc, "nsn_prefill_attention")
     if check and status is None:
         s = _dev.read_status(st)
         if s & _lib.ST_CAPACITY:
-            raise IntegrityError("Inconsistent cache: K/V block counts differ or the tail exceeds its capacity")
+            raise IntegrityError("Inconsistent cache: K/V block counts differ, the tail exceeds its capacity "
+                                 "or lacks room for the append")
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_OUTPUT):
             raise NumericalFailure("Nonfinite prefill output")
     return out

@@ -307,9 +307,25 @@ class StreamingKVCache:
         return _attn().decode_attention(q, self.side(slot, "K"), self.side(slot, "V"), self.lengths(slot),
                                         max_seq_len=L, **kw)
 
-    def prefill(self, slot, q, k_chunk, v_chunk, **kw):
+    def prefill(self, slot, q, k_chunk, v_chunk, append=False, **kw):
         """Chunked-prefill attention of q [B, Hq, n, 128] over the slot's
-        context plus the chunk's own K/V (not yet appended)."""
+        context plus the chunk's own K/V (not yet appended).  ``append=True``
+        also appends the chunk to every sequence's tail in the same launch
+        (k_chunk / v_chunk in the compute dtype; the tail rows get them
+        rounded to the tail dtype, as ``append`` would)."""
+        if append:
+            n = k_chunk.shape[2]
+            L, C = self.seq_length[slot], self.seq_compressed[slot]
+            for b in range(self.batch):
+                if L[b] - C[b] + n > self.tail_cap:
+                    raise IntegrityError("Tail overflow: compress before appending more tokens")
+                if L[b] + n > self.block_cap * BLOCK + self.tail_cap:
+                    raise IntegrityError("Cache capacity exceeded")
+            out = _attn().prefill_attention(q, self.side(slot, "K"), self.side(slot, "V"), self.lengths(slot),
+                                            k_chunk, v_chunk, append=True, **kw)
+            for b in range(self.batch):
+                L[b] += n
+            return out
         has_ctx = max(self.seq_length[slot]) > 0
         return _attn().prefill_attention(q, self.side(slot, "K") if has_ctx else None,
                                          self.side(slot, "V") if has_ctx else None, self.lengths(slot),

@@ -252,3 +252,86 @@ def test_append_in_another_dtype_equals_append_of_converted_tokens():
             a, b = caches[0].side(0, name).tail, caches[1].side(0, name).tail
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (sdt, name)
         assert caches[0].seq_length == caches[1].seq_length
+
+
+F16, BF16 = torch.float16, torch.bfloat16
+
+
+def _state(cache, slot=0):
+    """The slot's meaningful state as raw bits: block counts, then per
+    sequence its packed blocks (codes, metadata, decode factors) and its
+    tail rows (storage past them is never read)."""
+    def raw(t):
+        t = t.contiguous()
+        return t if t.dtype == torch.uint8 else t.view(torch.int8)
+    out = []
+    for name in ("K", "V"):
+        kv = cache.side(slot, name)
+        out.append(raw(kv.blocks))
+        for b in range(cache.batch):
+            L, C = cache.seq_length[slot][b], cache.seq_compressed[slot][b]
+            for t in (kv.codes, kv.norm, kv.min, kv.scale, kv.factor):
+                out.append(raw(t[b, :, :C // 64]))
+            out.append(raw(kv.tail[b, :, :L - C]))
+    return out
+
+
+@pytest.mark.parametrize("dtype,tail_dtype", [(BF16, F16), (F16, F16), (BF16, BF16)])
+def test_prefill_with_append_equals_prefill_then_append(dtype, tail_dtype):
+    """prefill(append=True) writes the chunk to the tails inside the prefill
+    launch: its outputs, lengths, tails and packed state are bit-identical to
+    prefill() followed by append(), over three chunks of 300 (two query
+    tiles) with compression between them, ragged context lengths and GQA
+    2:1 (only one q-head's workgroup of each kv-head appends)."""
+    B, Hq, H, n = 3, 4, 2, 300
+    g = torch.Generator(device=DEV).manual_seed(31)
+    caches = [StreamingKVCache(1, B, H, 2048, bits=3, dtype=tail_dtype, max_append=n, device=DEV) for _ in range(2)]
+    first = torch.randn((B, H, 100, 128), generator=g, device=DEV).to(dtype)
+    for c in caches:
+        c.append(0, first, first * 0.5, counts=[7, 47, 87])
+    for step in range(3):
+        q = torch.randn((B, Hq, n, 128), generator=g, device=DEV).to(dtype)
+        k = torch.randn((B, H, n, 128), generator=g, device=DEV).to(dtype)
+        v = torch.randn((B, H, n, 128), generator=g, device=DEV).to(dtype)
+        want = caches[0].prefill(0, q, k, v)
+        caches[0].append(0, k, v)
+        got = caches[1].prefill(0, q, k, v, append=True)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        assert caches[0].seq_length == caches[1].seq_length
+        for a, b in zip(_state(caches[0]), _state(caches[1])):
+            assert torch.equal(a, b), step
+        for c in caches:
+            c.post_prefill()
+        assert caches[0].seq_compressed == caches[1].seq_compressed
+    for a, b in zip(_state(caches[0]), _state(caches[1])):
+        assert torch.equal(a, b)
+    for c in caches:
+        c.check_status()
+
+
+def test_prefill_append_without_room():
+    """A chunk that does not fit the tail: with check=True the host refuses it
+    before the launch (nothing changes); with check=False the kernel's own
+    bound raises the capacity flag, appends nothing and still computes the
+    attention."""
+    from nsn_amd import _dev, _lib, kernels
+    from nsn_amd.errors import IntegrityError
+    g = torch.Generator(device=DEV).manual_seed(32)
+    c = StreamingKVCache(1, 1, 1, 1024, bits=3, dtype=F16, max_append=32, device=DEV)   # tail_cap 160
+    x = torch.randn((1, 1, 150, 128), generator=g, device=DEV).to(F16)
+    c.append(0, x, x)
+    q, k, v = (torch.randn((1, 1, 64, 128), generator=g, device=DEV).to(F16) for _ in range(3))
+    before = _state(c)
+    with pytest.raises(IntegrityError):
+        c.prefill(0, q, k, v, append=True)
+    with pytest.raises(IntegrityError):
+        kernels.prefill_attention(q, c.side(0, "K"), c.side(0, "V"), c.lengths(0), k, v, append=True)
+    st = _dev.new_status(DEV)
+    out = kernels.prefill_attention(q, c.side(0, "K"), c.side(0, "V"), c.lengths(0), k, v, append=True,
+                                    check=False, status=st)
+    want = kernels.prefill_attention(q, c.side(0, "K"), c.side(0, "V"), c.lengths(0), k, v)
+    assert _dev.read_status(st) == _lib.ST_CAPACITY
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    for a, b in zip(before, _state(c)):
+        assert torch.equal(a, b)
+    assert c.seq_length[0] == [150]
