@@ -163,11 +163,12 @@ def test_native_arm_prefill_matches_unpatched_model(tail_dtype):
     assert err <= 1e-3 * ref.float().abs().max().item(), err
 
 
-def test_decode_graph_replays_match_eager_steps():
+@pytest.mark.parametrize("tail_dtype", [F16, BF16])
+def test_decode_graph_replays_match_eager_steps(tail_dtype):
     """The fused step captured as a HIP graph: every replay (with eager work
     and a synchronisation between replays) equals the same device-position
     step run eagerly, bit for bit, across a compression; both agree with the
-    host-position fused arm to the arms' tolerance."""
+    host-position fused arm to the arms' tolerance.  fp16 and bf16 tails."""
     m, cfg, ids = model()
     n = 80
     tokens = torch.randint(0, 256, (B, n), generator=torch.Generator().manual_seed(3)).to(DEV)
@@ -175,7 +176,8 @@ def test_decode_graph_replays_match_eager_steps():
     outs = {}
     try:
         for use_graph in (False, True):
-            cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P, strict=False)
+            cache = adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P, strict=False,
+                                          tail_dtype=tail_dtype)
             with torch.no_grad():
                 m(input_ids=ids, past_key_values=cache, use_cache=True)
             cache.post_prefill()
@@ -189,8 +191,8 @@ def test_decode_graph_replays_match_eager_steps():
             assert all(cache.connection_calls[s] == n for s in (0, 1))
             assert dg.replays == (n if use_graph else 0)
             outs[use_graph] = torch.stack(steps)
-        ref = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P), ids,
-                            tokens)
+        ref = forced_logits(m, adapter.PackedKVCache(cfg, B, 1024, arm="PACKED_KV_FUSED", max_prefill=P,
+                                                     tail_dtype=tail_dtype), ids, tokens)
     finally:
         restore()
     assert torch.equal(outs[True], outs[False])
