@@ -492,11 +492,11 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
 
-    // ---- prologue: raw block 0 staged and filled, raw block 1 in flight
+    // ---- prologue: raw blocks 0 and 1 staged together (one round trip), block 0 filled
     stage(0);
+    if (nblk > 1) stage(1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (nblk > 1) stage(1);
     fill(0);
 
     // ---- one barrier per block: compute block j from KV buffer j & 1 while
