@@ -279,10 +279,19 @@ class StreamingKVCache:
                 sel(kv.scale).data_ptr(), sel(sd.headers).data_ptr(), sel(kv.factor).data_ptr(), self.block_cap,
                 start // BLOCK, start, None, self.status.data_ptr(), _dev.stream())
             _lib.check(rc, "nsn_encode_blocks")
-            # re-base the surviving tail tokens (source and target may overlap)
-            tail = sel(kv.tail)
-            src = tail[..., n:n + rest, :]
-            tail[..., :rest, :] = src.clone() if rest > n else src
+        # re-base the surviving tail tokens [n, n + rest) of every row to [0, rest)
+        if rest <= 0:
+            return
+        kt, vt = sel(self._sides[(slot, "K")].kv.tail), sel(self._sides[(slot, "V")].kv.tail)
+        if rest <= n:   # disjoint: one copy launch for both sides
+            step = n * DIM * kt.element_size()
+            rc = lib.nsn_tail_append(kt.data_ptr() + step, vt.data_ptr() + step, rows, rest, self.tail_cap,
+                                     kt.data_ptr(), vt.data_ptr(), self.tail_cap, 0, _dev.dtype_code(self.dtype),
+                                     _dev.stream())
+            _lib.check(rc, "nsn_tail_append")
+        else:           # overlapping rows: through a copy of the source
+            for tail in (kt, vt):
+                tail[..., :rest, :] = tail[..., n:n + rest, :].clone()
 
     def post_prefill(self):
         for s in range(self.slots):
