@@ -84,15 +84,18 @@ class StreamingKVCache:
         self.device = device
         nbytes = BLOCK * DIM * bits // 8
         self._sides = {}
+        # each slot's K and V packed-block counts: rows of one [2, batch]
+        # tensor, set by one launch (or one upload) per compression
+        self._blocks = [torch.zeros((2, batch), dtype=torch.int32, device=device) for _ in range(slots)]
         for s in range(slots):
-            for name in ("K", "V"):
+            for i, name in enumerate(("K", "V")):
                 kv = PackedKV(
                     codes=torch.empty((batch, heads, self.block_cap, nbytes), dtype=torch.uint8, device=device),
                     norm=torch.empty((batch, heads, self.block_cap, BLOCK), dtype=torch.float16, device=device),
                     min=torch.empty((batch, heads, self.block_cap, DIM), dtype=torch.float16, device=device),
                     scale=torch.empty((batch, heads, self.block_cap, DIM), dtype=torch.float16, device=device),
                     factor=torch.empty((batch, heads, self.block_cap, BLOCK), dtype=torch.float32, device=device),
-                    blocks=torch.zeros(batch, dtype=torch.int32, device=device),
+                    blocks=self._blocks[s][i],
                     tail=torch.zeros((batch, heads, self.tail_cap, DIM), dtype=dtype, device=device),
                     bits=bits)
                 hdr = torch.zeros((batch, heads, self.block_cap, 12), dtype=torch.uint8, device=device)
@@ -170,8 +173,7 @@ class StreamingKVCache:
         for b in range(self.batch):
             self.seq_length[slot][b] = 0
             self.seq_compressed[slot][b] = 0
-        for name in ("K", "V"):
-            self._sides[(slot, name)].kv.blocks.zero_()
+        self._blocks[slot].zero_()
         self.encoded_blocks[slot] = 0
 
     # ------------------------------------------------------------------ updates
@@ -253,12 +255,12 @@ class StreamingKVCache:
         for b in moving:
             C[b] = targets[b]
         nblocks = [c // BLOCK for c in C]
-        for name in ("K", "V"):
-            kv = self._sides[(slot, name)].kv
-            if len(set(nblocks)) == 1:
-                kv.blocks.fill_(nblocks[0])
-            else:
-                kv.blocks.copy_(torch.tensor(nblocks, dtype=torch.int32))
+        if len(set(nblocks)) == 1:
+            self._blocks[slot].fill_(nblocks[0])
+        else:   # from pinned memory without a host wait, like the lengths
+            gpu = self.device.type == "cuda"
+            self._blocks[slot].copy_(torch.tensor([nblocks, nblocks], dtype=torch.int32, pin_memory=gpu),
+                                     non_blocking=gpu)
 
     def _encode_rows(self, slot, b, start, target, length):
         """Encode tokens [start, target) of sequence b (or of every sequence,
