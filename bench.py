@@ -1162,8 +1162,9 @@ def stats_summary(d, workload):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
-              "described in DESIGN.md and no figure at several GPUs is produced.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the path would shard by sequence "
+              "and kv-head, each GPU running this kernel on its share; no figure at several GPUs is produced.",
+              file=sys.stderr)
         sys.exit(2)
     if args.summarize:
         summarize(args.summarize)
