@@ -276,8 +276,8 @@ def _state(cache, slot=0):
     return out
 
 
-@pytest.mark.parametrize("dtype,tail_dtype", [(BF16, F16), (F16, F16), (BF16, BF16)])
-def test_prefill_with_append_equals_prefill_then_append(dtype, tail_dtype):
+@pytest.mark.parametrize("dtype,tail_dtype,bits", [(BF16, F16, 3), (F16, F16, 3), (BF16, BF16, 3), (BF16, F16, 5)])
+def test_prefill_with_append_equals_prefill_then_append(dtype, tail_dtype, bits):
     """prefill(append=True) writes the chunk to the tails inside the prefill
     launch: its outputs, lengths, tails and packed state are bit-identical to
     prefill() followed by append(), over three chunks of 300 (two query
@@ -285,7 +285,8 @@ def test_prefill_with_append_equals_prefill_then_append(dtype, tail_dtype):
     2:1 (only one q-head's workgroup of each kv-head appends)."""
     B, Hq, H, n = 3, 4, 2, 300
     g = torch.Generator(device=DEV).manual_seed(31)
-    caches = [StreamingKVCache(1, B, H, 2048, bits=3, dtype=tail_dtype, max_append=n, device=DEV) for _ in range(2)]
+    caches = [StreamingKVCache(1, B, H, 2048, bits=bits, dtype=tail_dtype, max_append=n, device=DEV)
+              for _ in range(2)]
     first = torch.randn((B, H, 100, 128), generator=g, device=DEV).to(dtype)
     for c in caches:
         c.append(0, first, first * 0.5, counts=[7, 47, 87])

@@ -45,6 +45,18 @@ def test_library_rejects_bad_arguments_without_gpu_work():
     assert lib.nsn_attention_workspace_floats(16, 32, 8) == 16 * 32 * (8 * 132 + 1) == kernels.workspace_floats(16, 32, 8)
     # zero-size work is a no-op
     assert lib.nsn_pack_codes(None, 0, 3, None, None, None) == _lib.NSN_OK
+    # prefill: the chunk's append needs both tails (fake, aligned, never dereferenced addresses)
+    A = 1 << 20
+    pa = _lib.PrefillArgs()
+    pa.q, pa.ctx_len, pa.k_chunk, pa.v_chunk, pa.out = A, A, A, A, A
+    pa.dtype, pa.batch, pa.heads_q, pa.heads_kv, pa.n_q, pa.bits = _lib.DTYPE_BF16, 1, 1, 1, 0, 3
+    assert lib.nsn_prefill_attention(pa, None) == _lib.NSN_OK    # n_q = 0: nothing to do
+    pa.n_q, pa.bits = 64, 4
+    assert lib.nsn_prefill_attention(pa, None) == _lib.NSN_EINVAL
+    pa.bits, pa.append = 3, 1
+    assert lib.nsn_prefill_attention(pa, None) == _lib.NSN_EINVAL    # append without tails
+    pa.k.tail, pa.k.tail_cap, pa.k.tail_dtype = A, 128, _lib.DTYPE_F16
+    assert lib.nsn_prefill_attention(pa, None) == _lib.NSN_EINVAL    # the V tail is missing
 
 
 def test_device_position_appends_reject_bad_arguments_without_gpu_work():
