@@ -340,10 +340,11 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
 // Merge splits: one 256-thread block (4 waves) per (b, hq).  Wave w sums
 // splits w, w+4, ... (all its loads in flight together), lane c owns channels
 // 2c, 2c+1; the four wave partials are combined in LDS.
+constexpr int kMergeSlots = 16;   // partial slots per wave the merge holds in registers (64 per (b, hq))
 template <int ODT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, const int32_t *counts, int n_splits,
                                                          float *ctx, void *out, int32_t *status) {
-    __shared__ float red_z[4];
+    __shared__ float red_m[4], red_z[4];
     __shared__ float2 red_u[4][64];
     const int64_t bh = blockIdx.x;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -352,20 +353,56 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, 
     int used = counts[bh];
     used = used < 1 ? 1 : (used > n_splits ? n_splits : used);
     n_splits = used;
-    float L = -INFINITY;
-    for (int s = lane; s < n_splits; s += 64) L = fmaxf(L, base[static_cast<int64_t>(s) * kPartStride]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L = fmaxf(L, __shfl_xor(L, off));
     float z = 0.f, u0 = 0.f, u1 = 0.f;
+    if (n_splits <= 4 * kMergeSlots) {
+        // Wave w's slots w, w+4, ... all loaded at once (one round trip after
+        // the count), the maximum exchanged through LDS; then the same sums
+        // in the same order as the loop below.
+        float pm[kMergeSlots], pz[kMergeSlots];
+        float2 pu[kMergeSlots];
+#pragma unroll
+        for (int i = 0; i < kMergeSlots; ++i) {
+            const int s = w + 4 * i;
+            pm[i] = -INFINITY;
+            pz[i] = 0.f;
+            pu[i] = make_float2(0.f, 0.f);
+            if (s < n_splits) {
+                const float *ps = base + static_cast<int64_t>(s) * kPartStride;
+                pm[i] = ps[0];
+                pz[i] = ps[1];
+                pu[i] = *reinterpret_cast<const float2 *>(ps + 4 + 2 * lane);
+            }
+        }
+        float lw = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kMergeSlots; ++i) lw = fmaxf(lw, pm[i]);
+        if (lane == 0) red_m[w] = lw;
+        __syncthreads();
+        const float L = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+#pragma unroll
+        for (int i = 0; i < kMergeSlots; ++i) {
+            if (w + 4 * i < n_splits) {
+                const float a = (pm[i] == -INFINITY) ? 0.f : expf(pm[i] - L);
+                z = z + pz[i] * a;
+                u0 = u0 + pu[i].x * a;
+                u1 = u1 + pu[i].y * a;
+            }
+        }
+    } else {
+        float L = -INFINITY;
+        for (int s = lane; s < n_splits; s += 64) L = fmaxf(L, base[static_cast<int64_t>(s) * kPartStride]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L = fmaxf(L, __shfl_xor(L, off));
 #pragma unroll 4
-    for (int s = w; s < n_splits; s += 4) {
-        const float *ps = base + static_cast<int64_t>(s) * kPartStride;
-        const float m = ps[0];
-        const float a = (m == -INFINITY) ? 0.f : expf(m - L);
-        z = z + ps[1] * a;
-        const float2 u = *reinterpret_cast<const float2 *>(ps + 4 + 2 * lane);
-        u0 = u0 + u.x * a;
-        u1 = u1 + u.y * a;
+        for (int s = w; s < n_splits; s += 4) {
+            const float *ps = base + static_cast<int64_t>(s) * kPartStride;
+            const float m = ps[0];
+            const float a = (m == -INFINITY) ? 0.f : expf(m - L);
+            z = z + ps[1] * a;
+            const float2 u = *reinterpret_cast<const float2 *>(ps + 4 + 2 * lane);
+            u0 = u0 + u.x * a;
+            u1 = u1 + u.y * a;
+        }
     }
     if (lane == 0) red_z[w] = z;
     red_u[w][lane] = make_float2(u0, u1);
