@@ -124,6 +124,25 @@ def test_fast_stream_k_partition_many_sequences(split):
 
 
 @pytest.mark.parametrize("kernel", ["reference", "fast"])
+def test_merge_of_more_than_64_splits(kernel):
+    """79 partial slots per (sequence, q-head) at split 64 over 5000 tokens:
+    the merge's loop path (more than 64 slots) against the oracle, and
+    against the merge's register path (16 slots at split 320)."""
+    lengths = [5000, 300]
+    k, v, qb, kk, vv, seq = make_case(6, 2, 8, 2, lengths)
+    rnd = "float16" if kernel == "reference" else "float32"
+    outs = []
+    for split in (64, 320):
+        _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, seq, split_tokens=split, kv_round_dtype=torch.float16,
+                                          kernel=kernel)
+        ok, err = within(ctx.cpu().numpy(), oracle_ctx(k, v, qb, lengths, 3, rnd))
+        assert ok, (split, err)
+        outs.append(ctx.cpu().numpy())
+    atol, rtol = (1e-5, 1e-5) if kernel == "reference" else (2e-4, 2e-3)
+    assert np.allclose(outs[0], outs[1], atol=atol, rtol=rtol)
+
+
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
 def test_split_invariance(kernel):
     lengths = [1500, 900]
     k, v, qb, kk, vv, seq = make_case(5, 2, 8, 2, lengths)
