@@ -374,28 +374,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     const int64_t qw = q0 + 32 * wave;                     // this wave's first query
     const int64_t seqrow = static_cast<int64_t>(b) * p.heads_kv + kvh;
 
-    const int64_t T = p.ctx_len[b];
-    const int64_t nbk = p.k.blocks ? p.k.blocks[b] : 0;
-    const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
-    const int64_t nb = nbk;                                // (== nbv, checked below)
-    const int64_t ntail = T - nb * kBlockTok;
-    const int64_t qend = (q0 + kQTile < p.n_q) ? q0 + kQTile : p.n_q;   // chunk tokens this workgroup sees
-    const int64_t nt_blk = (ntail + kBlockTok - 1) / kBlockTok;
-    const int64_t nblk = nb + nt_blk + (qend + kBlockTok - 1) / kBlockTok;
-    if (nbk != nbv || nb < 0 || (nb > 0 && (nb > p.k.block_cap || nb > p.v.block_cap)) || ntail < 0 ||
-        ntail > p.k.tail_cap || ntail > p.v.tail_cap) {
-        if (tid == 0) raise_status(p.status, NSN_ST_CAPACITY);   // inconsistent cache (host checks first)
-        return;
-    }
-    // append: the workgroup of the last query tile (it stages every chunk
-    // block) of each kv-head's first q-head writes the chunk's K/V to tail
-    // rows ntail .. ntail + n_q - 1 as it fills them; no room: flag, no append
-    const bool app_wg = p.ka && blockIdx.z == 0 && hq % p.group == 0;
-    const bool app_ok = app_wg && ntail + p.n_q <= p.k.tail_cap && ntail + p.n_q <= p.v.tail_cap;
-    if (app_wg && !app_ok && tid == 0) raise_status(p.status, NSN_ST_CAPACITY);
-
     // ---- Q fragments (B operand of S^T = K' Q^T): query qw + 16*qt + row,
-    // channels 32*ks + 8*g + chE[e] (fp16: times scale*log2(e))
+    // channels 32*ks + 8*g + chE[e] (fp16: times scale*log2(e)); loaded
+    // before the context lengths are needed, so the two round trips overlap
     u32x4 qf[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -420,6 +401,26 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                                pk<DT>(x[O::chE[4]], x[O::chE[5]]), pk<DT>(x[O::chE[6]], x[O::chE[7]])};
         }
     }
+
+    const int64_t T = p.ctx_len[b];
+    const int64_t nbk = p.k.blocks ? p.k.blocks[b] : 0;
+    const int64_t nbv = p.v.blocks ? p.v.blocks[b] : 0;
+    const int64_t nb = nbk;                                // (== nbv, checked below)
+    const int64_t ntail = T - nb * kBlockTok;
+    const int64_t qend = (q0 + kQTile < p.n_q) ? q0 + kQTile : p.n_q;   // chunk tokens this workgroup sees
+    const int64_t nt_blk = (ntail + kBlockTok - 1) / kBlockTok;
+    const int64_t nblk = nb + nt_blk + (qend + kBlockTok - 1) / kBlockTok;
+    if (nbk != nbv || nb < 0 || (nb > 0 && (nb > p.k.block_cap || nb > p.v.block_cap)) || ntail < 0 ||
+        ntail > p.k.tail_cap || ntail > p.v.tail_cap) {
+        if (tid == 0) raise_status(p.status, NSN_ST_CAPACITY);   // inconsistent cache (host checks first)
+        return;
+    }
+    // append: the workgroup of the last query tile (it stages every chunk
+    // block) of each kv-head's first q-head writes the chunk's K/V to tail
+    // rows ntail .. ntail + n_q - 1 as it fills them; no room: flag, no append
+    const bool app_wg = p.ka && blockIdx.z == 0 && hq % p.group == 0;
+    const bool app_ok = app_wg && ntail + p.n_q <= p.k.tail_cap && ntail + p.n_q <= p.v.tail_cap;
+    if (app_wg && !app_ok && tid == 0) raise_status(p.status, NSN_ST_CAPACITY);
 
     f32x4 acc[8][2];   // O^T tiles [channel tile ct][query tile qt]
 #pragma unroll
