@@ -105,6 +105,7 @@ class StreamingKVCache:
         self._len_dev = {}               # cached int32 length tensors
         self.status = _dev.new_status(device)
         self.encoded_blocks = [0] * slots
+        self._side = None                # second stream of the compressions
 
     # ------------------------------------------------------------------ views
     def side(self, slot, name) -> PackedKV:
@@ -271,7 +272,8 @@ class StreamingKVCache:
         rest = length - target
         rows = self.heads if b is not None else self.batch * self.heads
         sel = (lambda t: t[b]) if b is not None else (lambda t: t)
-        for name in ("K", "V"):
+
+        def encode(name, stream):
             sd = self._sides[(slot, name)]
             kv = sd.kv
             rc = lib.nsn_encode_blocks(
@@ -279,8 +281,18 @@ class StreamingKVCache:
                 self.tail_cap * DIM, 0, self.bits, _lib.NORM_LANES8, 1,
                 sel(kv.codes).data_ptr(), sel(kv.norm).data_ptr(), sel(kv.min).data_ptr(),
                 sel(kv.scale).data_ptr(), sel(sd.headers).data_ptr(), sel(kv.factor).data_ptr(), self.block_cap,
-                start // BLOCK, start, None, self.status.data_ptr(), _dev.stream())
+                start // BLOCK, start, None, self.status.data_ptr(), stream)
             _lib.check(rc, "nsn_encode_blocks")
+        # K and V are encoded side by side: V on a second stream forked from
+        # and joined back into the current one (each launch alone is too
+        # small to fill the GPU)
+        cur = torch.cuda.current_stream(self.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)
+        self._side.wait_stream(cur)
+        encode("K", cur.cuda_stream)
+        encode("V", self._side.cuda_stream)
+        cur.wait_stream(self._side)
         # re-base the surviving tail tokens [n, n + rest) of every row to [0, rest)
         if rest <= 0:
             return
