@@ -129,13 +129,30 @@ def algorithmic_bytes(lengths, bits):
 
 
 def _cpu_model():
+    """The host CPU as `lscpu` names it: model name, vendor, family / model /
+    stepping, sockets x cores x threads (a VM may report a generic model
+    name; the family / model numbers still identify the part)."""
+    import subprocess
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in text.splitlines():
+            if ":" in line:
+                key, val = line.split(":", 1)
+                info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    if not info.get("Model name"):
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    info["Model name"] = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    keys = ("Model name", "Vendor ID", "CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket",
+            "Thread(s) per core", "CPU(s)", "Hypervisor vendor")
+    return "lscpu: " + "; ".join(f"{k} {info[k]}" for k in keys if info.get(k)) if info else "unknown"
 
 
 def _median_time(fn, reps, warm=3):
@@ -206,6 +223,20 @@ def cpu_baseline(kk, vv, q, lengths, sample_tokens=8192, reps=10):
                        f"{res['single']['c2'] * 1e3:.1f} ms on 1), scaled by total/sample tokens = {scale:.2f}",
                 c0_int3_qdq_us=round(res["all"]["c0"] * 1e6, 1), c0_int3_qdq_us_single=round(res["single"]["c0"] * 1e6, 1),
                 c1_readout_us=round(res["all"]["c1"] * 1e6, 1), c1_readout_us_single=round(res["single"]["c1"] * 1e6, 1))
+
+
+ROTATE = 3         # copies of the packed C2 cache, used in turn by consecutive steps
+BATCH = 24         # launches per timed batch of the per-kernel rounds (fixed, whatever --steps)
+ROUNDS = 5         # interleaved rounds of batches
+WARM_STEPS = 200   # steps before the per-kernel rounds
+
+
+def clone_packed(kv):
+    """A copy of one side of a packed cache at new addresses (every tensor cloned)."""
+    import dataclasses
+    import torch
+    return dataclasses.replace(kv, **{f.name: getattr(kv, f.name).clone() for f in dataclasses.fields(kv)
+                                      if isinstance(getattr(kv, f.name), torch.Tensor)})
 
 
 PROFILE_JSON = ROOT / "profiles" / "attn_fast_c2.json"
@@ -518,12 +549,202 @@ def profile_run(args):
     kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
     vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
     del k, v
+    caches = [(kk, vv)] + [(clone_packed(kk), clone_packed(vv)) for _ in range(ROTATE - 1)]
     max_len = max(lengths)
     steps = max(args.steps, PROFILE_STEPS)
-    for i in range(steps):
-        kernels.decode_attention(q, kk, vv, seq, kernel=args.kernel, max_seq_len=max_len, check=(i == 0))
+    for i in range(steps):   # the ROTATE copies in turn, as in the timed steps
+        ck, cv = caches[i % ROTATE]
+        kernels.decode_attention(q, ck, cv, seq, kernel=args.kernel, max_seq_len=max_len, check=(i == 0))
     torch.cuda.synchronize()
-    log(f"[bench] profile run done: {steps} steps")
+    log(f"[bench] profile run done: {steps} steps over {ROTATE} cache copies")
+
+
+def _arm_timing(fn, calls):
+    """loop_kv_vf01.py:105-117's timing of one arm: HIP events around `calls`
+    back-to-back calls (each allocates its own outputs and runs its host checks,
+    status reads included); extra device memory = allocated peak during the
+    calls - allocated before them.  Returns (ms per call, extra bytes)."""
+    import torch
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    out = None
+    for _ in range(calls):
+        if out is not None:
+            del out
+        out = fn()
+    b.record()
+    b.synchronize()
+    peak = torch.cuda.max_memory_allocated()
+    del out
+    return a.elapsed_time(b) / calls, peak - before
+
+
+def _paired(times, rounds, arms, num, den):
+    """Median over rounds of the per-round ratio num / den of per-call times."""
+    r = sorted(times[num][i] / times[den][i] for i in range(rounds))
+    return r[len(r) // 2]
+
+
+def readout_arms(dev, rounds=5, calls=20, warm=20):
+    """GPU timings of the reference's two published readout comparisons.
+
+    c1: the score-input V readout of one decode
+    query (AF01 FULL=False, experiments/ac08/source/loop_kv_af01_kernel.py:52-54),
+    B=1, 32 q / 8 kv heads, 4096 packed + 37 fp16 tail tokens, logits
+    N(0,1)*4, V from the config-0 generator (numpy rng 1): FUSED = the fast
+    kernel reading packed V; BRIDGE = V restored to HBM
+    (loop_kv_vf01_kernel.py:120-126) then the same kernel over dense V.
+    Kernel level: batches of back-to-back launches into preallocated buffers
+    (HIP events); call level: each call allocating its outputs and checking
+    its status, as below.
+
+    vf01: the shape of the reference's only published timings
+    (reports/vf01-results-v0.1-2026-10-02.md:27-35,68-69), B=1, 16 MHA heads,
+    896 packed + 127 bf16 tail tokens, packed K and V, through
+    kernels.pipeline's three arms on the fast kernel: V_FUSED, TILE_MATERIALIZE
+    (bridge) and RF01_MATERIALIZE.  Timed as loop_kv_vf01.py:105-117 times
+    them (_arm_timing, `calls` calls), `rounds` rounds with the arms
+    interleaved after `warm` warm-up calls each; per-arm medians, the median
+    of the per-round paired ratios, and the extra device memory per call.
+    """
+    import numpy as np
+    import torch
+    from nsn_amd import _dev, _lib, cache, codec, kernels, synthetic
+    stream = torch.cuda.current_stream()
+    res = {}
+
+    # ---- c1
+    rng = np.random.default_rng(1)
+    T1 = 4096 + 37
+    v1 = synthetic.kv_tokens(rng, (1, 8), T1)
+    sc1 = torch.from_numpy((rng.standard_normal((1, 32, T1)) * 4).astype(np.float32)).to(dev)
+    vv, seq = cache.pack_sequences(torch.from_numpy(v1).to(dev), [T1])
+    q1 = torch.zeros(1, 32, 128, dtype=torch.bfloat16, device=dev)
+    vden = torch.empty((1, 8, T1, 128), dtype=torch.float16, device=dev)
+    vd = kernels.PackedKV(None, None, None, None, None, None, vden, 3)
+    split, n_splits = kernels.default_split(1, 8, T1)
+    n_splits = max(2, n_splits)
+    ws = torch.empty(kernels.workspace_floats(1, 32, n_splits), dtype=torch.float32, device=dev)
+    out1 = torch.empty((1, 32, 128), dtype=torch.bfloat16, device=dev)
+    ctx1 = torch.empty((1, 32, 128), dtype=torch.float32, device=dev)
+    st = _dev.new_status(dev)
+    lib = _lib.lib()
+    nb1 = T1 // 64
+
+    def restore1():
+        rc = lib.nsn_restore_blocks(vv.codes.data_ptr(), 0, vv.norm.data_ptr(), vv.min.data_ptr(),
+                                    vv.scale.data_ptr(), 8, nb1, vv.codes.shape[2], 3, vden.data_ptr(),
+                                    _lib.DTYPE_F16, T1, vv.tail.data_ptr(), _lib.DTYPE_F16, T1 - nb1 * 64,
+                                    vv.tail.shape[2], st.data_ptr(), stream.cuda_stream)
+        assert rc == 0
+
+    def readout(vside):
+        kernels.decode_attention(q1, None, vside, seq, max_seq_len=T1, scores=sc1, kernel="fast",
+                                 split_tokens=split, workspace=ws, out=out1, ctx=ctx1, status=st, check=False)
+
+    def fused_k():
+        readout(vv)
+
+    def bridge_k():
+        restore1()
+        readout(vd)
+
+    def fused_call():
+        return kernels.decode_attention(q1, None, vv, seq, max_seq_len=T1, scores=sc1, kernel="fast")[0]
+
+    def bridge_call():
+        v = codec.restore(vv.codes[0], (vv.norm[0], vv.min[0], vv.scale[0]), 3, torch.float16,
+                          tail=vv.tail[0, :, :T1 - nb1 * 64])
+        side = kernels.PackedKV(None, None, None, None, None, None, v[None], 3)
+        return kernels.decode_attention(q1, None, side, seq, max_seq_len=T1, scores=sc1, kernel="fast")[0]
+    bridge_k()
+    torch.cuda.synchronize()
+    fused_out = fused_call().clone()
+    assert torch.allclose(fused_out.float(), bridge_call().float(), atol=2e-3, rtol=1e-2)
+    kt = {"fused": [], "bridge": []}
+    ct = {"fused": [], "bridge": []}
+    mem = {}
+    for _ in range(warm):
+        fused_k(), bridge_k(), fused_call(), bridge_call()
+    for _ in range(rounds):
+        kt["fused"].append(timed(fused_k, 50, 0, stream))
+        kt["bridge"].append(timed(bridge_k, 50, 0, stream))
+        for arm, fn in (("fused", fused_call), ("bridge", bridge_call)):
+            ms, extra = _arm_timing(fn, calls)
+            ct[arm].append(ms)
+            mem[arm] = max(mem.get(arm, 0), extra)
+    assert _dev.read_status(st) == 0
+    med = lambda xs: sorted(xs)[len(xs) // 2]
+    res["c1"] = {
+        "workload": "C1: score-input V readout, B=1, 32q/8kv, d=128, 4096 packed INT3 + 37 fp16 tail, logits N(0,1)*4",
+        "fused_kernel_us": round(med(kt["fused"]) * 1e3, 2), "bridge_kernel_us": round(med(kt["bridge"]) * 1e3, 2),
+        "kernel_ratio_fused_over_bridge": round(_paired(kt, rounds, None, "fused", "bridge"), 4),
+        "fused_call_us": round(med(ct["fused"]) * 1e3, 2), "bridge_call_us": round(med(ct["bridge"]) * 1e3, 2),
+        "call_ratio_fused_over_bridge": round(_paired(ct, rounds, None, "fused", "bridge"), 4),
+        "extra_device_bytes_per_call": mem,
+        "timing": f"kernel: median of {rounds} rounds of 50 back-to-back launches into preallocated buffers; call: "
+                  f"median of {rounds} rounds of {calls} calls allocating their outputs, status read each call",
+    }
+    log(f"[bench] C1 readout: fused {res['c1']['fused_kernel_us']} us, bridge {res['c1']['bridge_kernel_us']} us "
+        f"(kernel level); per call {res['c1']['fused_call_us']} / {res['c1']['bridge_call_us']} us; "
+        f"extra memory {mem}")
+    del vv, vden, ws
+
+    # ---- vf01
+    rng = np.random.default_rng(5)
+    H, NP, NT = 16, 896, 127
+    kx = synthetic.kv_tokens(rng, (1, H), NP + NT)
+    vx = synthetic.kv_tokens(rng, (1, H), NP + NT)
+
+    def group(x):
+        blocks = torch.from_numpy(x[:, :, :NP]).to(dev).reshape(1, H, NP // 64, 64, 128)
+        return codec.encode_group(blocks, 0)
+    g, vg = group(kx), group(vx)
+    kt_ = torch.from_numpy(kx[:, :, NP:]).to(dev).to(torch.bfloat16).contiguous()
+    vt_ = torch.from_numpy(vx[:, :, NP:]).to(dev).to(torch.bfloat16).contiguous()
+    qv = torch.from_numpy(rng.standard_normal((1, H, 1, 128)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    data = (g, kt_, qv, vg, vt_)
+    arms = ("V_FUSED", "TILE_MATERIALIZE", "RF01_MATERIALIZE")
+    outs = [kernels.pipeline(arm, data, kernel="fast").float() for arm in arms]
+    for o in outs[1:]:
+        assert torch.allclose(o, outs[0], atol=2e-3, rtol=1e-2)
+    for arm in arms:
+        for _ in range(warm):
+            kernels.pipeline(arm, data, kernel="fast")
+    vt = {arm: [] for arm in arms}
+    vmem = {}
+    for _ in range(rounds):
+        for arm in arms:
+            ms, extra = _arm_timing(lambda: kernels.pipeline(arm, data, kernel="fast"), calls)
+            vt[arm].append(ms)
+            vmem[arm] = max(vmem.get(arm, 0), extra)
+    res["vf01"] = {
+        "workload": "VF01 published shape: B=1, 16 MHA heads, d=128, 896 packed INT3 + 127 bf16 tail tokens, "
+                    "packed K and V, one decode query; kernels.pipeline arms on the fast kernel",
+        "ms_per_call": {arm: round(med(vt[arm]), 6) for arm in arms},
+        "paired_ratio_fused_over_bridge": round(_paired(vt, rounds, None, "V_FUSED", "TILE_MATERIALIZE"), 4),
+        "paired_ratio_fused_over_rf01": round(_paired(vt, rounds, None, "V_FUSED", "RF01_MATERIALIZE"), 4),
+        "extra_device_bytes_per_call": vmem,
+        "reference_published_rtx_pro_6000": {"ms_per_call": {"V_FUSED": 0.174514, "TILE_MATERIALIZE": 0.243244,
+                                                             "RF01_MATERIALIZE": 0.299447},
+                                             "paired_ratio_fused_over_bridge": 0.717196,
+                                             "paired_ratio_fused_over_rf01": 0.582795,
+                                             "extra_device_bytes_per_call": {"V_FUSED": 551424,
+                                                                             "TILE_MATERIALIZE": 14665728,
+                                                                             "RF01_MATERIALIZE": 21028864},
+                                             "source": "reports/vf01-results-v0.1-2026-10-02.md:27-35,68-69 "
+                                                       "(context only: other hardware and host stack)"},
+        "timing": f"loop_kv_vf01.py:105-117 protocol: {rounds} rounds, arms interleaved, {calls} checked calls "
+                  f"per arm and round between HIP events after {warm} warm-up calls; medians",
+    }
+    log(f"[bench] VF01 shape, ms per call {res['vf01']['ms_per_call']}, fused/bridge "
+        f"{res['vf01']['paired_ratio_fused_over_bridge']}, fused/RF01 {res['vf01']['paired_ratio_fused_over_rf01']}, "
+        f"extra memory {vmem}")
+    return res
 
 
 C3 = dict(B=64, HQ=16, HKV=4, L=8192, bits=5)
@@ -1224,9 +1445,13 @@ def main():
         f"{enc_tok_s / 1e9:.2f} G tok/s, {enc_gbs:.0f} GB/s algorithmic (314 B/token)")
     del encode_all, enc_bufs
 
-    # ---- packed ragged caches (setup, untimed)
+    # ---- packed ragged caches (setup, untimed).  ROTATE copies of the packed
+    # cache at separate addresses (3 x 365 MB, beyond the 256 MB Infinity
+    # Cache); consecutive steps use them in turn, so that no step re-reads what
+    # the previous one left in a cache level below HBM.
     kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
     vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+    caches = [(kk, vv)] + [(clone_packed(kk), clone_packed(vv)) for _ in range(ROTATE - 1)]
     max_len = max(lengths)
     split, n_splits = kernels.default_split(B, HKV, max_len)
     n_splits = max(2, n_splits) if args.kernel == "fast" else n_splits
@@ -1234,12 +1459,21 @@ def main():
     out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
     ctx = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
     status = _dev.new_status(dev)
-    # validated, checked call first (syncs, raises on any error)
-    kernels.decode_attention(q, kk, vv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
-                             workspace=ws, out=out, ctx=ctx)
+    # validated, checked calls first (sync, raise on any error); the copies give bitwise the same output
+    ref_out = None
+    for ck, cv in caches:
+        kernels.decode_attention(q, ck, cv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+                                 workspace=ws, out=out, ctx=ctx)
+        if ref_out is None:
+            ref_out = ctx.clone()
+        assert torch.equal(ctx, ref_out), "the cache copies give different outputs"
+    turn = [0]
 
-    def split_kernel():
-        kernels.decode_attention(q, kk, vv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
+    def split_kernel(rotate=True):
+        ck, cv = caches[turn[0]]
+        if rotate:
+            turn[0] = (turn[0] + 1) % ROTATE
+        kernels.decode_attention(q, ck, cv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
                                  workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=False)
     lib = _lib.lib()
     merge_args = (ws.data_ptr(), B, HQ, n_splits, ctx.data_ptr(), out.data_ptr(), _lib.DTYPE_BF16, status.data_ptr())
@@ -1247,12 +1481,16 @@ def main():
     def merge_kernel():
         _lib.check(lib.nsn_attention_merge(*merge_args, stream.cuda_stream), "nsn_attention_merge")
 
-    def step():   # one decode step: split kernel + merge
+    def step():   # one decode step: split kernel + merge, over the next cache copy
         split_kernel()
         merge_kernel()
 
+    def step_single():   # the same over copy 0 only (every step re-reads the same 365 MB)
+        split_kernel(rotate=False)
+        merge_kernel()
+
     log(f"[bench] decode: kernel={args.kernel} split={split} tokens x {n_splits} splits, "
-        f"{B * HKV * n_splits} work units; warmup {args.warmup}, steps {args.steps}")
+        f"{B * HKV * n_splits} work units; {ROTATE} cache copies in turn; warmup {args.warmup}, steps {args.steps}")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -1265,31 +1503,46 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
-    # Per-kernel durations in the same warm state: rounds of back-to-back
-    # batches -- steps, split-only launches, merge-only launches -- each batch
-    # bracketed by HIP events on the launch stream.  A batch of split launches
-    # has no merge between them, so its per-launch time is the split kernel's
-    # own duration plus the dispatch gap, and the interleaving keeps all three
-    # at one clock.
-    rounds = 5
-    per = max(4, args.steps // rounds)
-    round_step, round_split, round_merge = [], [], []
-    for _ in range(rounds):
-        round_step.append(timed(step, per, 0, stream))
-        round_split.append(timed(split_kernel, per, 0, stream))
-        round_merge.append(timed(merge_kernel, per, 0, stream))
-    split_ts = sorted(round_split)
-    ms_split = sum(round_split) / rounds
-    ms_merge = sum(round_merge) / rounds
-    ms_step_rounds = sum(round_step) / rounds
+    # Per-kernel durations, independent of --steps: after a fixed warm-up,
+    # ROUNDS rounds of back-to-back batches of BATCH launches each -- steps,
+    # split-only launches, merge-only launches, and steps over one cache copy
+    # -- all enqueued without a host synchronisation, with a HIP event on the
+    # launch stream between consecutive batches.  A split-only batch has no
+    # merge between its launches, so its per-launch time is the split
+    # kernel's own duration plus the dispatch gap; the interleaving keeps all
+    # four at one clock.
+    for _ in range(WARM_STEPS):
+        step()
+    kinds = (("step", step), ("split", split_kernel), ("merge", merge_kernel), ("single", step_single))
+    marks = []
+    for _ in range(ROUNDS):
+        for name, fn in kinds:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(stream)
+            marks.append((name, ev))
+            for _ in range(BATCH):
+                fn()
+    end = torch.cuda.Event(enable_timing=True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    per = {name: [] for name, _ in kinds}
+    for i, (name, ev) in enumerate(marks):
+        nxt = marks[i + 1][1] if i + 1 < len(marks) else end
+        per[name].append(ev.elapsed_time(nxt) / BATCH)
+    mean = lambda xs: sum(xs) / len(xs)
+    ms_split, ms_merge = mean(per["split"]), mean(per["merge"])
+    ms_step_rounds, ms_single = mean(per["step"]), mean(per["single"])
+    split_ts = sorted(per["split"])
+    consistent = ms_split + ms_merge <= ms_step_rounds * 1.02
     st_val = _dev.read_status(status)
     assert st_val == 0, f"status word {st_val:#x}"
     nbytes = algorithmic_bytes(lengths, 3)
     achieved = nbytes / (ms_split * 1e-3) / 1e9
-    log(f"[bench] step {ms_step * 1e3:.1f} us; interleaved rounds: step {ms_step_rounds * 1e3:.1f} us, "
-        f"split {ms_split * 1e3:.1f} us (median of rounds {split_ts[len(split_ts) // 2] * 1e3:.1f}), "
-        f"merge {ms_merge * 1e3:.1f} us; {nbytes / 1e6:.1f} MB algorithmic -> {achieved:.0f} GB/s "
-        f"({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    log(f"[bench] step {ms_step * 1e3:.1f} us (timed region, {ROTATE} copies in turn); rounds of {BATCH}: "
+        f"step {ms_step_rounds * 1e3:.1f} us, split {ms_split * 1e3:.1f} us (median of rounds "
+        f"{split_ts[len(split_ts) // 2] * 1e3:.1f}), merge {ms_merge * 1e3:.1f} us, one-copy step "
+        f"{ms_single * 1e3:.1f} us; split + merge <= step: {consistent}; {nbytes / 1e6:.1f} MB algorithmic -> "
+        f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     # parity spot check of this step against the exact-order kernel (untimed)
     if args.kernel != "reference":
@@ -1304,7 +1557,7 @@ def main():
         "metric": METRIC, "value": round(ms_step * 1e3, 2), "unit": "µs/step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16x2/f32",
-        "data": "synthetic (GPU torch.Generator seed 2; lengths numpy rng 2)",
+        "data": "synthetic (GPU torch.Generator seed 2; lengths numpy rng 2); 3 copies of the packed cache used in turn",
         "config": {"workload": "C2: fused packed-INT3 K+V decode attention, B=16, 32q/8kv heads, d=128, "
                                "ragged ctx U[16K,32K], fp16 tail < 64", "batch": B, "heads_q": HQ, "heads_kv": HKV,
                    "head_dim": D, "ctx_min": LMIN, "ctx_max": LMAX, "bits": 3, "kernel": args.kernel,
@@ -1318,8 +1571,15 @@ def main():
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
                      "kernel_us": round(ms_split * 1e3, 2), "kernel_us_median": round(split_ts[len(split_ts) // 2] * 1e3, 2),
                      "merge_us": round(ms_merge * 1e3, 2), "step_us_same_rounds": round(ms_step_rounds * 1e3, 2),
-                     "timing": f"{rounds} interleaved rounds of {per} steps / {per} split-only / {per} merge-only "
-                               "launches, HIP events around each batch on the launch stream"},
+                     "split_plus_merge_le_step": consistent,
+                     "timing": f"{WARM_STEPS} warm-up steps, then {ROUNDS} rounds of back-to-back batches of {BATCH} "
+                               "steps / split-only / merge-only / one-copy steps, enqueued without a host sync, HIP "
+                               f"events between batches on the launch stream; every batch but the one-copy one "
+                               f"turns over {ROTATE} copies of the packed cache"},
+        "cache_rotation": {"copies": ROTATE, "bytes_per_copy": nbytes,
+                           "note": "value and roofline turn over the copies (no step re-reads the previous step's "
+                                   "bytes); single_copy_step_us re-reads one copy every step"},
+        "single_copy_step_us": round(ms_single * 1e3, 2),
         "encode_roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(enc_gbs / HBM_PEAK_GBS, 4), "traffic": measured_encode_traffic(),
                             "kernel": "encode (C2 K, fp16 -> INT3 + fp16 metadata + fp32 decode factors)",
@@ -1348,7 +1608,7 @@ def main():
             restore_all()
             kernels.decode_attention(q, kk, vd, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
                                      workspace=ws, out=out, ctx=ctx, status=status, check=False)
-        ms_bridge = timed(bridge, max(3, args.steps // 4), 1, stream)
+        ms_bridge = timed(bridge, 10, 2, stream)
         del vfull
         # fp16-KV decode: the same kernel over dense fp16 K and V
         kd = kernels.PackedKV(None, None, None, None, None, None, k, 3)
@@ -1357,9 +1617,10 @@ def main():
         def dense():
             kernels.decode_attention(q, kd, vdn, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
                                      workspace=ws, out=out, ctx=ctx, status=status, check=False)
-        ms_dense = timed(dense, max(3, args.steps // 4), 1, stream)
+        ms_dense = timed(dense, 20, 3, stream)
         result["comparators"] = {"bridge_us": round(ms_bridge * 1e3, 1), "fp16_kv_us": round(ms_dense * 1e3, 1)}
         log(f"[bench] bridge {ms_bridge * 1e3:.1f} us/step, fp16-KV {ms_dense * 1e3:.1f} us/step")
+        result.update(readout_arms(dev))
 
     if not args.no_cpu:
         log("[bench] CPU baseline (PyTorch-CPU restatement, all threads and one) ...")
@@ -1368,7 +1629,7 @@ def main():
     if not args.c2_only:
         # the other BASELINE.json configs at their own shapes, reduced repeat counts
         # (C3: 60 steps; C4: one slot, 32 decode steps), as sub-objects of this line
-        del kk, vv, q, ws, k, v
+        del kk, vv, q, ws, k, v, caches
         torch.cuda.empty_cache()
         sub = argparse.Namespace(**vars(args))
         sub.steps, sub.warmup, sub.slots, sub.decode_steps = 60, 500, 1, 32

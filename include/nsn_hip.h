@@ -51,8 +51,10 @@ enum { NSN_NORM_LANES8 = 0, NSN_NORM_SEQUENTIAL = 1 };
                                              (q, tail tokens; block metadata in the REFERENCE kernel) */
 #define NSN_ST_WORKSPACE 0x400  /* attention: the partial slots (n_splits) are too few for the FAST kernel's partition */
 #define NSN_ST_CAPACITY 0x800   /* attention: a sequence's blocks or tail lie past the cache's capacity
-                                   (blocks > block_cap or seq_len - 64*blocks > tail_cap); the FAST
-                                   kernel reads nothing of that sequence */
+                                   (blocks > block_cap or seq_len - 64*blocks > tail_cap); neither
+                                   decode kernel reads anything of that sequence */
+#define NSN_ST_EMPTY 0x1000     /* attention merge: a (sequence, q-head) attended no token (length 0,
+                                   or a length refused by NSN_ST_CAPACITY); its output is zero */
 
 /* Return codes. */
 #define NSN_OK 0
@@ -243,8 +245,11 @@ int64_t nsn_attention_workspace_floats(int64_t batch, int64_t heads_q, int n_spl
  * before anything is launched.  Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU (concurrent streams, or another
  * launch before this one's merge has finished) race; calls in stream order
- * are safe.  Nothing in the array needs to start at zero: every partial and
- * partial count the merge reads is written by the same call.
+ * are safe.  Nothing in the array needs to start at zero: every partial
+ * count the merge reads is written by the same call (0 for a (sequence,
+ * q-head) with no usable token, whose output the merge sets to zero under
+ * NSN_ST_EMPTY), and so is every partial slot below that count -- except
+ * where the call raises NSN_ST_WORKSPACE, whose outputs are not valid.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).

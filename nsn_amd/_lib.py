@@ -29,6 +29,7 @@ ST_NONFINITE_ATTN_INPUT = 0x100
 ST_TAIL_RANGE = 0x200
 ST_WORKSPACE = 0x400
 ST_CAPACITY = 0x800
+ST_EMPTY = 0x1000
 
 NSN_OK, NSN_EINVAL, NSN_ELAUNCH, NSN_ENOSPC = 0, -1, -2, -3
 STATIC_SCRATCH_FLOATS = 4 * 1024 * 1024   # NSN_STATIC_SCRATCH_FLOATS

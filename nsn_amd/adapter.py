@@ -341,6 +341,8 @@ class PackedKVCache(Cache):
             raise IntegrityError("Tail append position out of range")
         if s & _lib.ST_CAPACITY:
             raise IntegrityError("Sequence length past the cache's block / tail capacity")
+        if s & _lib.ST_EMPTY:
+            raise IntegrityError("A sequence attended no token (zero length)")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s:

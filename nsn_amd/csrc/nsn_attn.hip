@@ -194,7 +194,26 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int G = p.group;
     const int64_t row = static_cast<int64_t>(b) * p.heads_kv + kvh;
-    const int64_t T = p.seq_len[b];
+    // The usable length.  One whose blocks or tail lie past the cache's
+    // capacity, or past the splits' reach, is possible only with the host
+    // checks skipped (device lengths): nothing of that sequence is read, the
+    // status word says why, and the merge sees a partial count of 0.
+    int64_t T = p.seq_len[b];
+    {
+        auto fits = [&](const SideParams &sd) {
+            const int64_t nb = sd.blocks ? sd.blocks[b] : 0;
+            if (nb < 0 || nb > (sd.blocks ? sd.block_cap : 0)) return false;
+            const int64_t rest = T - nb * kBlockTok;
+            return rest <= 0 || (sd.tail != nullptr && rest <= sd.tail_cap);
+        };
+        const bool cap_ok = T >= 0 && (SCORES ? T <= p.scores_cap : fits(p.k)) && fits(p.v);
+        const bool ws_ok = T <= static_cast<int64_t>(p.n_splits) * p.split_tokens;
+        if (!cap_ok || !ws_ok) {
+            if (tid == 0 && split == 0 && kvh == 0)
+                raise_status(p.status, !cap_ok ? NSN_ST_CAPACITY : NSN_ST_WORKSPACE);
+            T = 0;
+        }
+    }
     const int64_t t_begin = static_cast<int64_t>(split) * p.split_tokens;
     const int64_t t_end = t_begin + p.split_tokens < T ? t_begin + p.split_tokens : T;
     const int64_t hq0 = static_cast<int64_t>(kvh) * G;
@@ -322,9 +341,9 @@ __global__ __launch_bounds__(256) void attn_reference_kernel(AttnParams p) {
             float *dst = p.partials + ((static_cast<int64_t>(b) * p.heads_q + hq0 + h) * p.n_splits + split) * kPartStride;
             if (lane == 0) {
                 dst[0] = run_m[h]; dst[1] = run_l[h]; dst[2] = 0.f; dst[3] = 0.f;
-                if (split == 0)   // every split writes a slot: the merge reads all n_splits
+                if (split == 0)   // every split writes a slot: the merge reads all n_splits (none: no token)
                     reinterpret_cast<int32_t *>(p.partials + p.batch * p.heads_q * p.n_splits * kPartStride)
-                        [static_cast<int64_t>(b) * p.heads_q + hq0 + h] = p.n_splits;
+                        [static_cast<int64_t>(b) * p.heads_q + hq0 + h] = (T > 0) ? p.n_splits : 0;
             }
             *reinterpret_cast<float2 *>(dst + 4 + 2 * lane) = make_float2(acc[k][0], acc[k][1]);
             bad_attn |= !finite(acc[k][0]) || !finite(acc[k][1]);
@@ -349,9 +368,20 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *partials, 
     const int64_t bh = blockIdx.x;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const float *base = partials + bh * n_splits * kPartStride;
-    // partial slots written for this (b, hq); clamped so that a stale count stays in bounds
+    // partial slots written for this (b, hq): both decode kernels write the
+    // count, 0 for a (b, hq) that attended no token -- zero output, flagged
     int used = counts[bh];
-    used = used < 1 ? 1 : (used > n_splits ? n_splits : used);
+    if (used <= 0) {   // (uniform across the block)
+        if (w == 0) {
+            const int64_t c = bh * kDim + 2 * lane;
+            if (ctx) ctx[c] = ctx[c + 1] = 0.f;
+            static_cast<typename Elem<ODT>::T *>(out)[c] = Elem<ODT>::store(0.f);
+            static_cast<typename Elem<ODT>::T *>(out)[c + 1] = Elem<ODT>::store(0.f);
+            if (lane == 0) raise_status(status, NSN_ST_EMPTY);
+        }
+        return;
+    }
+    used = used > n_splits ? n_splits : used;   // (in bounds whatever the count)
     n_splits = used;
     float z = 0.f, u0 = 0.f, u1 = 0.f;
     if (n_splits <= 4 * kMergeSlots) {

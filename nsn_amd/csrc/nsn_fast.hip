@@ -934,12 +934,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
         fields(c0 + l, t, nk, nv);
         take_chunk(t, nk, nv);
     };
+    // A sequence with no usable token gets no segment: wave 0 writes partial
+    // count 0 for its q-heads, so that the merge never reads a stale slot.
+    auto mark_empty = [&](int64_t c, int32_t t) {
+        if (blockIdx.x != 0 || c + l >= p.batch || t != 0) return;
+        int32_t *cnt = reinterpret_cast<int32_t *>(p.partials + p.batch * p.heads_q * p.n_splits * kPartStride) +
+                       (c + l) * p.heads_q;
+        for (int64_t h = 0; h < p.heads_q; ++h) cnt[h] = 0;
+    };
     take_chunk(t_0, nk_0, nv_0);
+    mark_empty(0, t_l);
     int64_t N = lane_get(incl, 63);
     for (int64_t c = 64; c < p.batch; c += 64) {   // sequences past the first 64
         int32_t tr, nk, nv;
         fields(c + l, tr, nk, nv);
         const int32_t t = usable(tr, nk, nv);
+        mark_empty(c, t);
         const int32_t nbt = static_cast<int32_t>((static_cast<int64_t>(t) + kBlockTok - 1) / kBlockTok);
         N += H * static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(wave_incl_scan32(nbt), 63)));
     }

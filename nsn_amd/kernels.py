@@ -222,6 +222,8 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
             raise IntegrityError("Sequence length past the cache's block / tail capacity")
         if s & _lib.ST_WORKSPACE:
             raise IntegrityError("Decode workspace too small: n_splits below the fast kernel's partial slots")
+        if s & _lib.ST_EMPTY:
+            raise IntegrityError("A sequence attended no token (zero length)")
         if s & _lib.ST_NONFINITE_ATTN_INPUT:
             raise NumericalFailure("Nonfinite raw attention input (q, tail or block metadata)")
         if s & (_lib.ST_NONFINITE_ATTN | _lib.ST_NONFINITE_RESTORE | _lib.ST_NONFINITE_OUTPUT):

@@ -428,6 +428,36 @@ def test_capacity_guard_with_device_lengths():
     assert _dev.read_status(st) & _lib.ST_CAPACITY
 
 
+@pytest.mark.parametrize("kernel", ["fast", "reference"])
+def test_empty_and_over_capacity_sequences_with_device_lengths(kernel):
+    """check=False: a sequence of length 0, and one whose length lies past the
+    cache's capacity, attend nothing -- both kernels write partial count 0,
+    the merge writes a zero output and raises NSN_ST_EMPTY (the latter also
+    NSN_ST_CAPACITY) -- while the other sequences still match the oracle.
+    The merge never reads a slot the call did not write: the workspace is
+    filled with NaN first, so a stale read would show as a nonfinite output."""
+    from nsn_amd import _dev, _lib
+    lengths = [700, 300, 130, 64]
+    k, v, qb, kk, vv, seq = make_case(8, 4, 8, 2, lengths)
+    split, n_splits = kernels.default_split(4, 2, 700)
+    n_splits = max(2, n_splits)
+    ws = torch.full((kernels.workspace_floats(4, 8, n_splits),), float("nan"), dtype=torch.float32, device=DEV)
+    dev_len = torch.tensor([700, 0, 130, 64 * int(kk.blocks[3]) + kk.tail.shape[2] + 1], dtype=torch.int32,
+                           device=DEV)
+    print(f"empty/over-capacity case: kernel {kernel}, lengths {dev_len.tolist()}", flush=True)
+    st = _dev.new_status(DEV)
+    _, ctx = kernels.decode_attention(qb.to(DEV), kk, vv, dev_len, max_seq_len=700, kernel=kernel, check=False,
+                                      status=st, split_tokens=split, workspace=ws)
+    s = _dev.read_status(st)
+    assert s & _lib.ST_EMPTY and s & _lib.ST_CAPACITY, hex(s)
+    assert not s & (_lib.ST_NONFINITE_OUTPUT | _lib.ST_NONFINITE_ATTN), hex(s)
+    got = ctx.cpu().numpy()
+    assert np.all(got[1] == 0) and np.all(got[3] == 0)
+    ref = oracle_ctx(k[[0, 2]], v[[0, 2]], qb[[0, 2]], [700, 130], 3, "float32" if kernel == "fast" else "float16")
+    ok, err = within(got[[0, 2]], ref)
+    assert ok, err
+
+
 @pytest.mark.parametrize("Hq,Hkv,bits", [(8, 2, 3), (32, 4, 3), (8, 2, 5), (16, 8, 5)])
 def test_fast_bf16_tails_vs_oracle(Hq, Hkv, bits):
     """bf16 tails (the reference's dtype, loop_kv_qk01_kernel.py:66-69) on the

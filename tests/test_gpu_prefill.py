@@ -5,11 +5,10 @@ nsn_encode + nsn_decode: fp32 reconstructions for fp16 data, rounded to bf16
 for bf16 data as the reference's restore returns them), the tail and the
 chunk K/V as stored, then the oracle's float64 chunked-prefill attention
 (oracle.prefill_attention64, pinned row by row against the decode oracle).
-Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise, on
-top of the output's own rounding (bf16/fp16).  K/V and queries are N(0,1)
-activations, as in the chunked-prefill configuration.  The MFMA operands
-have the data's dtype (fp16: 11-bit, bf16: 8-bit significands), so the
-absolute error grows with the largest |v| a query attends to.
+Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise, plus
+the output's own rounding (bf16: 2^-8, fp16: 2^-11 relative) and nothing
+else.  K/V and queries are N(0,1) activations, as in the chunked-prefill
+configuration, except where a test scales them.
 """
 import numpy as np
 import pytest
@@ -48,8 +47,10 @@ def restore_ctx(x16, length, bits, dtype, packed_dtype=None):
     return np.concatenate(parts, axis=1) if parts else np.zeros((H, 0, 128), np.float32)
 
 
-def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chunk_scale=None):
-    """chunk_scale: optional [n] multipliers of the chunk's V rows (values past fp16's range)."""
+def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chunk_scale=None, weighted=0.0):
+    """chunk_scale: optional [n] multipliers of the chunk's V rows (values past
+    fp16's range).  weighted: a term added to the bound, times the attention
+    over |V| (only the out-of-fp16-range case uses it; see there)."""
     rng = np.random.default_rng(seed)
     tail_dtype = tail_dtype or dtype
     T = max(max(ctx_lengths), 1)
@@ -73,18 +74,16 @@ def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chu
         kc = restore_ctx(kx[b], L, bits, tail_dtype, dtype)
         vc = restore_ctx(vx[b], L, bits, tail_dtype, dtype)
         ref = O.prefill_attention64(q[b].float().numpy(), kc, vc, kch[b].float().numpy(), vch[b].float().numpy())
-        ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11      # output rounding
+        ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11      # the output's own rounding
         err = np.abs(got[b] - ref)
         bound = ATOL + (RTOL + ulp) * np.abs(ref)
-        if dtype == torch.bfloat16:
-            # bf16 softmax weights carry a 2^-9 relative rounding each, so the
-            # output may move by 2^-9 of the attention-weighted |v| (computed
-            # exactly: the same attention over |V|); 2^-8 leaves room for the
-            # K and V rounding
-            wabs = O.prefill_attention64(q[b].float().numpy(), kc, np.abs(vc), kch[b].float().numpy(),
-                                         np.abs(vch[b].float().numpy()))
-            bound = bound + 2.0 ** -8 * wabs
-        assert np.all(err <= bound), (b, float(err.max()), float((err / bound).max()))
+        if weighted:
+            bound = bound + weighted * O.prefill_attention64(q[b].float().numpy(), kc, np.abs(vc),
+                                                             kch[b].float().numpy(), np.abs(vch[b].float().numpy()))
+        ratio = float((err / bound).max())
+        print(f"prefill case seed {seed} sequence {b}: max err {float(err.max()):.2e}, max err/bound {ratio:.3f}",
+              flush=True)
+        assert ratio <= 1.0, (b, float(err.max()), ratio)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -126,7 +125,12 @@ def test_prefill_bf16_products_with_an_fp16_tail():
 
 def test_prefill_bf16_values_beyond_fp16_range():
     """bf16 chunk values of order 1e6 compute on the bf16 products (fp16 would
-    overflow); the error stays within 2^-8 of the attention-weighted |v|."""
+    overflow).  This is a range test, not a precision test: with values of
+    order 1e6 of both signs the output cancels to far below them, and no fp32
+    computation meets an absolute 2e-3 there (fp32 softmax weights alone carry
+    2^-24 of the attention-weighted |v|, ~0.06).  The bound therefore adds
+    2^-8 of the attention-weighted |v| (the bf16 weights' rounding); every
+    N(0,1) case above is held to the north-star bound alone."""
     scale = np.ones(200)
     scale[3::11] = 1e6
-    run_case(28, 1, 2, 2, [130], 200, 3, torch.bfloat16, chunk_scale=scale)
+    run_case(28, 1, 2, 2, [130], 200, 3, torch.bfloat16, chunk_scale=scale, weighted=2.0 ** -8)
