@@ -25,7 +25,8 @@ Profiling (the commands behind the committed summaries under profiles/):
 
 ``--profile`` runs one 1 GiB device-to-device copy (the counter calibration:
 a plain copy kernel of known size), 10 launches of the C2 encode, and then
-``--steps`` decode steps.  The
+the C2 decode steps as the benchmark issues them (C2Decode: back to back over
+three cache copies in turn): a 200-step warm-up and 100 measured steps.  The
 HBM traffic per split-kernel launch is FETCH_SIZE and WRITE_SIZE (KiB per
 dispatch) scaled by bytes-moved / counter-reading of that copy.  The normal
 run reports it as ``roofline.traffic`` when profiles/attn_fast_c2.json was
@@ -239,6 +240,65 @@ def clone_packed(kv):
                                       if isinstance(getattr(kv, f.name), torch.Tensor)})
 
 
+class C2Decode:
+    """The C2 decode step as the benchmark runs it: ROTATE copies of the packed
+    cache at separate addresses (3 x 365 MB, beyond the 256 MB Infinity
+    Cache), consecutive steps using them in turn, preallocated workspace and
+    outputs, launches with the host checks off (the first, checked call per
+    copy validates the cache).  split() is the split kernel alone, merge()
+    the merge alone, step() both over the next copy, step_single() both over
+    copy 0."""
+
+    def __init__(self, dev, lengths, k, v, q, kernel="fast"):
+        import torch
+        from nsn_amd import _dev, _lib, cache, kernels
+        kk, self.seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
+        vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+        self.kk, self.vv, self.q, self.kernel = kk, vv, q, kernel
+        self.caches = [(kk, vv)] + [(clone_packed(kk), clone_packed(vv)) for _ in range(ROTATE - 1)]
+        self.max_len = max(lengths)
+        split, n_splits = kernels.default_split(B, HKV, self.max_len)
+        self.split_tokens = split
+        self.n_splits = max(2, n_splits) if kernel == "fast" else n_splits
+        self.ws = torch.empty(kernels.workspace_floats(B, HQ, self.n_splits), dtype=torch.float32, device=dev)
+        self.out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
+        self.ctx = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+        self.status = _dev.new_status(dev)
+        self.stream = torch.cuda.current_stream()
+        ref = None
+        for ck, cv in self.caches:   # validated, checked calls (sync, raise on any error)
+            kernels.decode_attention(q, ck, cv, self.seq, max_seq_len=self.max_len, kernel=kernel, split_tokens=split,
+                                     workspace=self.ws, out=self.out, ctx=self.ctx)
+            if ref is None:
+                ref = self.ctx.clone()
+            assert torch.equal(self.ctx, ref), "the cache copies give different outputs"
+        self.turn = 0
+        self._kernels = kernels
+        self._lib = _lib
+        self._merge_args = (self.ws.data_ptr(), B, HQ, self.n_splits, self.ctx.data_ptr(), self.out.data_ptr(),
+                            _lib.DTYPE_BF16, self.status.data_ptr())
+
+    def split(self, rotate=True):
+        ck, cv = self.caches[self.turn]
+        if rotate:
+            self.turn = (self.turn + 1) % ROTATE
+        self._kernels.decode_attention(self.q, ck, cv, self.seq, max_seq_len=self.max_len, kernel=self.kernel,
+                                       split_tokens=self.split_tokens, workspace=self.ws, out=self.out, ctx=self.ctx,
+                                       status=self.status, check=False, merge=False)
+
+    def merge(self):
+        self._lib.check(self._lib.lib().nsn_attention_merge(*self._merge_args, self.stream.cuda_stream),
+                        "nsn_attention_merge")
+
+    def step(self):
+        self.split()
+        self.merge()
+
+    def step_single(self):
+        self.split(rotate=False)
+        self.merge()
+
+
 PROFILE_JSON = ROOT / "profiles" / "attn_fast_c2.json"
 PROFILE_MD = ROOT / "profiles" / "attn_fast_c2.md"
 FAST_SOURCE = ROOT / "nsn_amd" / "csrc" / "nsn_fast.hip"
@@ -268,12 +328,12 @@ def _rows(path_glob):
 
 def _counter(dirname, counter):
     """Per-dispatch readings (KiB) of one counter for the split kernel, the
-    merge kernel, the calibration copy (the only copy dispatch with a grid
-    of 64K threads or more; the other copies in the run move a few bytes) and
+    merge kernel, the calibration copy (the first copy dispatch with a grid
+    of 64K threads or more; the later ones copy the packed cache) and
     the C2 encode launches (the first ENCODE_PROFILE_STEPS encoder dispatches:
     `--profile` runs them before it packs the cache with the same kernel)."""
     out = {"split": [], "merge": [], "calib": [], "encode": []}
-    enc = []
+    enc, calib = [], []
     for r in _rows((dirname, "**/*counter_collection.csv")):
         if r["Counter_Name"] != counter:
             continue
@@ -285,8 +345,9 @@ def _counter(dirname, counter):
         elif ENCODE_KERNEL in name:
             enc.append((int(r["Dispatch_Id"]), val))
         elif name.startswith(CALIB_KERNEL) and int(r["Grid_Size"]) >= 65536:
-            out["calib"].append(val)
+            calib.append((int(r["Dispatch_Id"]), val))
     out["encode"] = [v for _, v in sorted(enc)[:ENCODE_PROFILE_STEPS]]
+    out["calib"] = [min(calib)[1]] if calib else []   # the run's first large copy (the later ones copy the cache)
     return out
 
 
@@ -379,12 +440,17 @@ def summarize(d):
     alg = algorithmic_bytes(lens, 3)
     top = sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]
     top += [r for r in stats if (SPLIT_KERNEL in r["Name"] or MERGE_KERNEL in r["Name"]) and r not in top]
-    split_avg = next(float(r["AverageNs"]) for r in stats if SPLIT_KERNEL in r["Name"]) / 1e3
-    durs = sorted((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-                  for r in _rows((d / "kt", "**/*kernel_trace.csv")) if SPLIT_KERNEL in r["Kernel_Name"])
+    all_avg = next(float(r["AverageNs"]) for r in stats if SPLIT_KERNEL in r["Name"]) / 1e3
+    # the measured launches: the last PROFILE_STEPS, after the WARM_STEPS warm-up the benchmark also runs
+    seq = [dur for _, dur in sorted((int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                                    for r in _rows((d / "kt", "**/*kernel_trace.csv")) if SPLIT_KERNEL in r["Kernel_Name"])]
+    last = seq[-PROFILE_STEPS:]
+    split_avg = sum(last) / len(last)
+    durs = sorted(last)
     split_med = durs[len(durs) // 2]
     fig = {"kernel": SPLIT_KERNEL, "source_sha256": source_sha(), "workload": "C2",
            "split_avg_us": round(split_avg, 2), "split_median_us": round(split_med, 2),
+           "split_avg_us_all_launches": round(all_avg, 2), "launches": len(seq), "measured_launches": len(last),
            "fetch_kib": round(mean(fetch["split"]), 1),
            "write_kib": round(mean(write["split"]), 1), "fetch_scale": round(f_scale, 4),
            "write_scale": round(w_scale, 4), "read_bytes": int(split_read), "write_bytes": int(split_write),
@@ -412,9 +478,13 @@ def summarize(d):
           f"writes x{w_scale:.3f}.", "",
           f"Split kernel: {split_read / 1e6:.1f} MB read + {split_write / 1e6:.1f} MB written = "
           f"**{fig['traffic'] / 1e6:.1f} MB** per launch, against {alg / 1e6:.1f} MB algorithmic "
-          f"(ratio {fig['traffic'] / alg:.3f}); duration under the profiler: mean {split_avg:.1f} us "
-          f"-> {alg / split_avg / 1e3:.0f} GB/s algorithmic, median {split_med:.1f} us "
-          f"-> {alg / split_med / 1e3:.0f} GB/s (the mean includes the cold first launch).", "",
+          f"(ratio {fig['traffic'] / alg:.3f}).", "",
+          f"Duration under the profiler, over the last {len(last)} of the {len(seq)} split launches (the "
+          f"{len(seq) - len(last)} before them are the warm-up the benchmark also runs, {WARM_STEPS} steps, plus "
+          f"the checked calls): mean **{split_avg:.1f} us** -> {alg / split_avg / 1e3:.0f} GB/s algorithmic = "
+          f"{alg / split_avg / 1e3 / HBM_PEAK_GBS:.1%} of 8 TB/s; median {split_med:.1f} us; min {durs[0]:.1f} us, "
+          f"max {durs[-1]:.1f} us.  Over all {len(seq)} launches the mean is {all_avg:.1f} us: during the "
+          "warm-up the engine clock dips for a stretch of launches before it settles.", "",
           f"Kernel source sha256: `{fig['source_sha256']}`", ""]
     sq = _sq(d, SPLIT_KERNEL)
     if sq:
@@ -529,10 +599,10 @@ def c2_encoder(dev, k):
 
 
 def profile_run(args):
-    """Calibration copy, the C2 encode launches, then `steps` decode steps of
-    the C2 workload."""
+    """Calibration copy, the C2 encode launches, then WARM_STEPS + `steps`
+    decode steps of the C2 workload, issued as the benchmark's timed batches
+    issue them (C2Decode.step: back to back, the cache copies in turn)."""
     import torch
-    from nsn_amd import cache, kernels
     dev = torch.device("cuda:0")
     lengths, k, v, q = make_workload(dev)
     src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
@@ -546,17 +616,13 @@ def profile_run(args):
         encode_all()
     torch.cuda.synchronize()
     del encode_all, enc_bufs
-    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
-    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
+    dec = C2Decode(dev, lengths, k, v, q, kernel=args.kernel)
     del k, v
-    caches = [(kk, vv)] + [(clone_packed(kk), clone_packed(vv)) for _ in range(ROTATE - 1)]
-    max_len = max(lengths)
     steps = max(args.steps, PROFILE_STEPS)
-    for i in range(steps):   # the ROTATE copies in turn, as in the timed steps
-        ck, cv = caches[i % ROTATE]
-        kernels.decode_attention(q, ck, cv, seq, kernel=args.kernel, max_seq_len=max_len, check=(i == 0))
+    for _ in range(WARM_STEPS + steps):   # as the timed steps: back to back, the copies in turn, no host sync
+        dec.step()
     torch.cuda.synchronize()
-    log(f"[bench] profile run done: {steps} steps over {ROTATE} cache copies")
+    log(f"[bench] profile run done: {WARM_STEPS} + {steps} steps over {ROTATE} cache copies")
 
 
 def _arm_timing(fn, calls):
@@ -1445,49 +1511,11 @@ def main():
         f"{enc_tok_s / 1e9:.2f} G tok/s, {enc_gbs:.0f} GB/s algorithmic (314 B/token)")
     del encode_all, enc_bufs
 
-    # ---- packed ragged caches (setup, untimed).  ROTATE copies of the packed
-    # cache at separate addresses (3 x 365 MB, beyond the 256 MB Infinity
-    # Cache); consecutive steps use them in turn, so that no step re-reads what
-    # the previous one left in a cache level below HBM.
-    kk, seq = cache.pack_sequences(k, lengths, bits=3, tail_dtype=torch.float16)
-    vv, _ = cache.pack_sequences(v, lengths, bits=3, tail_dtype=torch.float16)
-    caches = [(kk, vv)] + [(clone_packed(kk), clone_packed(vv)) for _ in range(ROTATE - 1)]
-    max_len = max(lengths)
-    split, n_splits = kernels.default_split(B, HKV, max_len)
-    n_splits = max(2, n_splits) if args.kernel == "fast" else n_splits
-    ws = torch.empty(kernels.workspace_floats(B, HQ, n_splits), dtype=torch.float32, device=dev)
-    out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
-    ctx = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
-    status = _dev.new_status(dev)
-    # validated, checked calls first (sync, raise on any error); the copies give bitwise the same output
-    ref_out = None
-    for ck, cv in caches:
-        kernels.decode_attention(q, ck, cv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
-                                 workspace=ws, out=out, ctx=ctx)
-        if ref_out is None:
-            ref_out = ctx.clone()
-        assert torch.equal(ctx, ref_out), "the cache copies give different outputs"
-    turn = [0]
-
-    def split_kernel(rotate=True):
-        ck, cv = caches[turn[0]]
-        if rotate:
-            turn[0] = (turn[0] + 1) % ROTATE
-        kernels.decode_attention(q, ck, cv, seq, max_seq_len=max_len, kernel=args.kernel, split_tokens=split,
-                                 workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=False)
-    lib = _lib.lib()
-    merge_args = (ws.data_ptr(), B, HQ, n_splits, ctx.data_ptr(), out.data_ptr(), _lib.DTYPE_BF16, status.data_ptr())
-
-    def merge_kernel():
-        _lib.check(lib.nsn_attention_merge(*merge_args, stream.cuda_stream), "nsn_attention_merge")
-
-    def step():   # one decode step: split kernel + merge, over the next cache copy
-        split_kernel()
-        merge_kernel()
-
-    def step_single():   # the same over copy 0 only (every step re-reads the same 365 MB)
-        split_kernel(rotate=False)
-        merge_kernel()
+    # ---- packed ragged caches (setup, untimed): see C2Decode
+    dec = C2Decode(dev, lengths, k, v, q, kernel=args.kernel)
+    kk, vv, seq, max_len = dec.kk, dec.vv, dec.seq, dec.max_len
+    split, n_splits, ws, out, ctx, status = dec.split_tokens, dec.n_splits, dec.ws, dec.out, dec.ctx, dec.status
+    split_kernel, merge_kernel, step, step_single = dec.split, dec.merge, dec.step, dec.step_single
 
     log(f"[bench] decode: kernel={args.kernel} split={split} tokens x {n_splits} splits, "
         f"{B * HKV * n_splits} work units; {ROTATE} cache copies in turn; warmup {args.warmup}, steps {args.steps}")
@@ -1629,7 +1657,7 @@ def main():
     if not args.c2_only:
         # the other BASELINE.json configs at their own shapes, reduced repeat counts
         # (C3: 60 steps; C4: one slot, 32 decode steps), as sub-objects of this line
-        del kk, vv, q, ws, k, v, caches
+        del kk, vv, q, ws, k, v, dec
         torch.cuda.empty_cache()
         sub = argparse.Namespace(**vars(args))
         sub.steps, sub.warmup, sub.slots, sub.decode_steps = 60, 500, 1, 32

@@ -293,6 +293,10 @@ typedef struct {
     void *out;              /* [B, Hq, n_q, 128] dtype */
     int32_t *status;        /* NSN_ST_NONFINITE_OUTPUT; NSN_ST_CAPACITY on an inconsistent cache or no room to append */
     int append;             /* 1: also append the chunk's K/V to the tails (see above) */
+    int precise_weights;    /* bf16 only: 1 = the softmax weights enter the PV product as bf16 hi + lo
+                               (~2^-17 relative) instead of one bf16 rounding (2^-9), at ~24 % more
+                               time per block; for chunks with little or no context, whose first
+                               queries attend a handful of tokens.  Ignored for fp16. */
 } nsn_prefill_args;
 
 int nsn_prefill_attention(const nsn_prefill_args *args, nsn_stream_t stream);

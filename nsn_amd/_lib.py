@@ -56,7 +56,8 @@ class AttnArgs(ctypes.Structure):
 class PrefillArgs(ctypes.Structure):
     _fields_ = [("q", P), ("dtype", I32), ("batch", I64), ("heads_q", I64), ("heads_kv", I64), ("n_q", I64),
                 ("scale", ctypes.c_float), ("ctx_len", P), ("bits", I32), ("k", KVSide), ("v", KVSide),
-                ("k_chunk", P), ("v_chunk", P), ("out", P), ("status", P), ("append", I32)]
+                ("k_chunk", P), ("v_chunk", P), ("out", P), ("status", P), ("append", I32),
+                ("precise_weights", I32)]
 
 
 class KScoreArgs(ctypes.Structure):

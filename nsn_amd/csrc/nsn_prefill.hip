@@ -29,6 +29,8 @@
 // Softmax runs in the log2 domain: fp16 queries are pre-scaled by
 // scale*log2(e); bf16 queries enter the product exactly and the scores are
 // scaled after it.
+#include <type_traits>
+
 #include "nsn_common.hpp"
 
 namespace nsn {
@@ -80,6 +82,12 @@ __device__ __forceinline__ float rows4_max(float x) {
     x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// fp32 pair -> bf16 hi (round to nearest even) + bf16 lo = rn(x - hi): the
+// pair to ~2^-17 relative.
+__device__ __forceinline__ void split_bf16(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = pk<NSN_DTYPE_BF16>(a, b);
+    lo = pk<NSN_DTYPE_BF16>(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 __device__ __forceinline__ float h16(uint32_t w, int hi) {
     return static_cast<float>(__builtin_bit_cast(half2v, w)[hi]);
@@ -345,12 +353,18 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, c
 }
 
 // DT: dtype of the queries, the chunk K/V, the output and the products; TDT:
-// dtype of the context tail.
-template <int BITS, int DT, int TDT>
+// dtype of the context tail.  LO (bf16 only): the softmax weights enter the
+// PV product and the row sums as bf16 hi + lo (~2^-17 relative) instead of
+// one bf16 rounding (2^-9) -- for chunks with little or no context, whose
+// first queries attend a handful of tokens, where one weight's bf16 rounding
+// moves the output by up to 2^-9 of |v|.  It costs ~24 % more time per
+// block (36 more MFMA and ~80 more VALU per wave), so the caller asks for it.
+template <int BITS, int DT, int TDT, bool LO>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
     using S = Stage<BITS>;
     using O = Order<BITS>;
     constexpr bool QPRE = DT == NSN_DTYPE_F16;   // fp16 queries carry scale*log2(e); bf16 ones stay exact
+    static_assert(!LO || DT == NSN_DTYPE_BF16, "hi + lo weights are a bf16 form");
     __shared__ __align__(16) uint16_t kt[2][kBlockTok * kKP];
     __shared__ __align__(16) uint16_t vt[2][kDim * kVP];
     __shared__ __align__(16) uint8_t stg[2][S::BYTES > kDenseStage ? S::BYTES : kDenseStage];
@@ -510,7 +524,6 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         if (j + 2 < nblk) stage(j + 2);
         if (j + 1 < nblk) fill(j + 1);
         if (qw >= p.n_q) continue;   // (a wave past the chunk end only helps fill)
-        const bool packed = j < nb;
         int valid;
         int64_t cpos;
         block_rows(j, valid, cpos);
@@ -534,7 +547,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         // running maximum (and the state's rescale) only moves when some
         // lane's block maximum exceeds it.
         const bool masked = valid < kBlockTok || cpos >= 0;   // (uniform) partial or causal block
-        u32x4 pb[2][2];   // P''^T B operands [ks2][qt]
+        u32x4 pb[2][2];   // P''^T B operands [ks2][qt] (LO: the bf16 hi parts)
+        u32x4 pl[2][2];   // LO: the bf16 lo parts
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
             if (masked) {
@@ -570,10 +584,21 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                     pw[tt][i] = __builtin_amdgcn_exp2f(QPRE ? s[tt][qt][i] - msafe
                                                             : __builtin_fmaf(s[tt][qt][i], p.qscale, -msafe));
 #pragma unroll
-            for (int ks2 = 0; ks2 < 2; ++ks2)
-                pb[ks2][qt] = u32x4{pk<DT>(pw[2 * ks2][0], pw[2 * ks2][1]), pk<DT>(pw[2 * ks2][2], pw[2 * ks2][3]),
-                                    pk<DT>(pw[2 * ks2 + 1][0], pw[2 * ks2 + 1][1]),
-                                    pk<DT>(pw[2 * ks2 + 1][2], pw[2 * ks2 + 1][3])};
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                if constexpr (LO) {
+                    uint32_t h[4], lo[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        split_bf16(pw[2 * ks2 + (e >> 1)][2 * (e & 1)], pw[2 * ks2 + (e >> 1)][2 * (e & 1) + 1], h[e],
+                                   lo[e]);
+                    pb[ks2][qt] = u32x4{h[0], h[1], h[2], h[3]};
+                    pl[ks2][qt] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                } else {
+                    pb[ks2][qt] = u32x4{pk<DT>(pw[2 * ks2][0], pw[2 * ks2][1]), pk<DT>(pw[2 * ks2][2], pw[2 * ks2][3]),
+                                        pk<DT>(pw[2 * ks2 + 1][0], pw[2 * ks2 + 1][1]),
+                                        pk<DT>(pw[2 * ks2 + 1][2], pw[2 * ks2 + 1][3])};
+                }
+            }
         }
         // ---- O^T[channel][query] += V'^T P''^T (k order: tokens 4g..4g+3 of both 16-token tiles)
 #pragma unroll
@@ -582,13 +607,19 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             for (int ks2 = 0; ks2 < 2; ++ks2) {
                 const u32x4 a = *reinterpret_cast<const u32x4 *>(vtj + (16 * ct + row) * kVP + 32 * ks2 + 8 * g);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[ct][qt] = mfma<DT>(a, pb[ks2][qt], acc[ct][qt]);
+                for (int qt = 0; qt < 2; ++qt) {
+                    acc[ct][qt] = mfma<DT>(a, pb[ks2][qt], acc[ct][qt]);
+                    if constexpr (LO) acc[ct][qt] = mfma<DT>(a, pl[ks2][qt], acc[ct][qt]);
+                }
             }
         }
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) lsum[qt] = mfma<DT>(ones_a, pb[ks2][qt], lsum[qt]);
+            for (int qt = 0; qt < 2; ++qt) {
+                lsum[qt] = mfma<DT>(ones_a, pb[ks2][qt], lsum[qt]);
+                if constexpr (LO) lsum[qt] = mfma<DT>(ones_a, pl[ks2][qt], lsum[qt]);
+            }
     }
 
     // ---- output: O[q][c] = O^T / l, channels 16*ct + 4*g + i of query qw + 16*qt + row
@@ -677,17 +708,20 @@ extern "C" int nsn_prefill_attention(const nsn_prefill_args *a, nsn_stream_t str
     const dim3 grid(static_cast<unsigned>(a->heads_q), static_cast<unsigned>(a->batch), static_cast<unsigned>(qt));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool bf = a->dtype == NSN_DTYPE_BF16;
-#define NSN_PREFILL_LAUNCH(B_, D_)                                                                              \
-    do {                                                                                                        \
-        if (tbf) hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_BF16>), grid, dim3(64 * kWaves), 0, st, p); \
-        else hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_F16>), grid, dim3(64 * kWaves), 0, st, p);      \
+#define NSN_PREFILL_LAUNCH(B_, D_, L_)                                                                              \
+    do {                                                                                                            \
+        if (tbf) hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_BF16, L_>), grid, dim3(64 * kWaves), 0, st, p); \
+        else hipLaunchKernelGGL((prefill_kernel<B_, D_, NSN_DTYPE_F16, L_>), grid, dim3(64 * kWaves), 0, st, p);      \
     } while (0)
+    const bool lo = bf && a->precise_weights;
     if (a->bits == 3) {
-        if (bf) NSN_PREFILL_LAUNCH(3, NSN_DTYPE_BF16);
-        else NSN_PREFILL_LAUNCH(3, NSN_DTYPE_F16);
+        if (lo) NSN_PREFILL_LAUNCH(3, NSN_DTYPE_BF16, true);
+        else if (bf) NSN_PREFILL_LAUNCH(3, NSN_DTYPE_BF16, false);
+        else NSN_PREFILL_LAUNCH(3, NSN_DTYPE_F16, false);
     } else {
-        if (bf) NSN_PREFILL_LAUNCH(5, NSN_DTYPE_BF16);
-        else NSN_PREFILL_LAUNCH(5, NSN_DTYPE_F16);
+        if (lo) NSN_PREFILL_LAUNCH(5, NSN_DTYPE_BF16, true);
+        else if (bf) NSN_PREFILL_LAUNCH(5, NSN_DTYPE_BF16, false);
+        else NSN_PREFILL_LAUNCH(5, NSN_DTYPE_F16, false);
     }
 #undef NSN_PREFILL_LAUNCH
     return hipGetLastError() == hipSuccess ? NSN_OK : NSN_ELAUNCH;

@@ -232,7 +232,7 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
 
 
 def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, k_chunk, v_chunk, *, scale=SCALE,
-                      status=None, check=True, out=None, append=False):
+                      status=None, check=True, out=None, append=False, precise_weights=None):
     """Chunked-prefill attention over a packed context (C4's prefill step).
 
     q [B, Hq, n, 128]; k_chunk, v_chunk [B, Hkv, n, 128] (the chunk's own K/V;
@@ -247,6 +247,10 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     (rounded to the tail dtype), in the same launch: the cache update
     (loop_kv_pk01_cache.py:101-102) that otherwise follows as a separate
     append; k and v must then carry tails with room for n more tokens.
+    ``precise_weights`` (bf16 only): the softmax weights enter the PV product
+    as bf16 hi + lo (~2^-17 relative) instead of one bf16 rounding, at ~24 %
+    more kernel time; None = only when there is no context (k is None), where
+    the first queries attend a handful of tokens.
     """
     _dev.require_gpu(q, k_chunk, v_chunk, ctx_len)
     require(q.ndim == 4 and q.shape[3] == DIM and q.is_contiguous(), "Query shape/type")
@@ -307,6 +311,7 @@ def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, 
     a.out = out.data_ptr()
     a.status = st.data_ptr()
     a.append = 1 if append else 0
+    a.precise_weights = 1 if (k is None if precise_weights is None else precise_weights) else 0
     rc = _lib.lib().nsn_prefill_attention(a, _dev.stream())
     _lib.check(rc, "nsn_prefill_attention")
     if check and status is None:

@@ -335,7 +335,11 @@ class StreamingKVCache:
         context plus the chunk's own K/V (not yet appended).  ``append=True``
         also appends the chunk to every sequence's tail in the same launch
         (k_chunk / v_chunk in the compute dtype; the tail rows get them
-        rounded to the tail dtype, as ``append`` would)."""
+        rounded to the tail dtype, as ``append`` would).  bf16 chunks carry
+        their softmax weights as bf16 hi + lo (``precise_weights``) while some
+        sequence of the slot has less than one block of context: its first
+        queries attend a handful of tokens."""
+        kw.setdefault("precise_weights", min(self.seq_length[slot]) < BLOCK)
         if append:
             n = k_chunk.shape[2]
             L, C = self.seq_length[slot], self.seq_compressed[slot]

@@ -47,7 +47,8 @@ def restore_ctx(x16, length, bits, dtype, packed_dtype=None):
     return np.concatenate(parts, axis=1) if parts else np.zeros((H, 0, 128), np.float32)
 
 
-def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chunk_scale=None, weighted=0.0):
+def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chunk_scale=None, weighted=0.0,
+             precise=None):
     """chunk_scale: optional [n] multipliers of the chunk's V rows (values past
     fp16's range).  weighted: a term added to the bound, times the attention
     over |V| (only the out-of-fp16-range case uses it; see there)."""
@@ -67,7 +68,7 @@ def run_case(seed, B, Hq, Hkv, ctx_lengths, n, bits, dtype, tail_dtype=None, chu
     else:
         kk = vv = None
         seq = torch.zeros(B, dtype=torch.int32, device=DEV)
-    out = kernels.prefill_attention(q.to(DEV), kk, vv, seq, kch.to(DEV), vch.to(DEV))
+    out = kernels.prefill_attention(q.to(DEV), kk, vv, seq, kch.to(DEV), vch.to(DEV), precise_weights=precise)
     got = out.float().cpu().numpy()
     for b in range(B):
         L = ctx_lengths[b]
@@ -105,8 +106,11 @@ def test_prefill_c4_chunk_of_512():
     run_case(26, 2, 4, 2, [1000, 130], 512, 3, torch.float16)
 
 
-def test_prefill_no_context_is_causal_attention():
-    run_case(22, 1, 2, 2, [0], 200, 3, torch.bfloat16)
+@pytest.mark.parametrize("precise", [None, False])
+def test_prefill_no_context_is_causal_attention(precise):
+    """No context: by default (None) the bf16 weights carry their lo parts; the
+    single-rounded form (False) is held to the same bound."""
+    run_case(22, 1, 2, 2, [0], 200, 3, torch.bfloat16, precise=precise)
 
 
 def test_prefill_block_aligned_context_gqa8():
@@ -118,9 +122,12 @@ def test_prefill_5bit():
     run_case(24, 2, 2, 2, [192, 100], 70, 5, torch.float16)
 
 
-def test_prefill_bf16_products_with_an_fp16_tail():
-    """C4's mix: bf16 queries and chunk on the bf16 MFMA over an fp16 tail."""
-    run_case(27, 2, 4, 2, [300, 77], 150, 3, torch.bfloat16, tail_dtype=torch.float16)
+@pytest.mark.parametrize("precise", [None, True])
+def test_prefill_bf16_products_with_an_fp16_tail(precise):
+    """C4's mix: bf16 queries and chunk on the bf16 MFMA over an fp16 tail,
+    with single-rounded weights (the default over a context) and with the
+    weights as bf16 hi + lo (precise_weights=True)."""
+    run_case(27, 2, 4, 2, [300, 77], 150, 3, torch.bfloat16, tail_dtype=torch.float16, precise=precise)
 
 
 def test_prefill_bf16_values_beyond_fp16_range():
