@@ -1396,7 +1396,7 @@ def _r(x, nd=3):
 
 
 ADAPTER_DOC = ("rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- "
-               "python3 bench.py --workload adapter --adapter-arms graph")
+               "python3 bench.py --workload adapter --adapter-arms graph --steps 20 --warmup 5")
 
 
 def adapter_summary(d):
