@@ -29,8 +29,6 @@
 // Softmax runs in the log2 domain: fp16 queries are pre-scaled by
 // scale*log2(e); bf16 queries enter the product exactly and the scores are
 // scaled after it.
-#include <type_traits>
-
 #include "nsn_common.hpp"
 
 namespace nsn {
