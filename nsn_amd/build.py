@@ -1,6 +1,7 @@
 """Build libnsn_hip.so (gfx950) in-tree with hipcc.
 
     python -m nsn_amd.build
+    python -m nsn_amd.build --resource-usage [source.hip ...]   # compiler's per-kernel resource report
 
 Flags: -O3; -ffp-contract=off (the codec must not contract multiply-adds that
 torch rounds separately; fma is written explicitly where torch fuses); packed
@@ -59,5 +60,57 @@ def build(verbose=False, jobs=None):
     return LIB
 
 
+_RES_KEYS = (("VGPRs", "vgpr"), ("AGPRs", "agpr"), ("TotalSGPRs", "sgpr"), ("ScratchSize [bytes/lane]", "scratch"),
+             ("Occupancy [waves/SIMD]", "occupancy"), ("SGPRs Spill", "sgpr_spill"), ("VGPRs Spill", "vgpr_spill"),
+             ("LDS Size [bytes/block]", "lds"))
+
+
+def resource_usage(source):
+    """Per-kernel register, spill, scratch, LDS and occupancy figures of one
+    source as the compiler reports them (-Rpass-analysis=kernel-resource-usage,
+    device code only, same flags as the build).  Returns {mangled name: {key: int}}."""
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *FLAGS, "--cuda-device-only", "-c", str(SRC / source), "-o", os.devnull,
+           "-Rpass-analysis=kernel-resource-usage"]
+    out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, check=True).stdout
+    kernels, cur = {}, None
+    for ln in out.splitlines():
+        if "remark:" not in ln:
+            continue
+        msg = ln.split("remark:", 1)[1].split("[-Rpass", 1)[0].strip()
+        if msg.startswith("Function Name:"):
+            cur = kernels.setdefault(msg.split(":", 1)[1].strip(), {})
+            continue
+        for label, key in _RES_KEYS:
+            if cur is not None and msg.startswith(label + ":"):
+                cur[key] = int(msg.split(":", 1)[1].strip())
+    return kernels
+
+
+def _demangle(names):
+    try:
+        out = subprocess.run(["c++filt"], input="\n".join(names), stdout=subprocess.PIPE, text=True, check=True).stdout
+        return out.splitlines()
+    except (OSError, subprocess.CalledProcessError):
+        return list(names)
+
+
+def resource_table(sources=None):
+    """Markdown table of resource_usage() over the given (default: all) sources."""
+    rows = ["| kernel | VGPR | AGPR | SGPR | SGPR spill | VGPR spill | scratch B/lane | LDS B/workgroup | waves/SIMD |",
+            "|---|---|---|---|---|---|---|---|---|"]
+    for s in sources or SOURCES:
+        ks = resource_usage(s)
+        for name, pretty in zip(ks, _demangle(list(ks))):
+            r = ks[name]
+            short = pretty.replace("nsn::", "").split("(")[0]
+            rows.append(f"| `{short}` ({s}) | " + " | ".join(
+                str(r.get(k, "?")) for k in ("vgpr", "agpr", "sgpr", "sgpr_spill", "vgpr_spill", "scratch", "lds",
+                                             "occupancy")) + " |")
+    return "\n".join(rows)
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if len(sys.argv) > 1 and sys.argv[1] == "--resource-usage":
+        print(resource_table(sys.argv[2:] or None))
+    else:
+        print(build(verbose=True))
