@@ -60,7 +60,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1000)
     p.add_argument("--kernel", default="fast", choices=["fast", "reference"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    p.add_argument("--no-baselines", action="store_true", help="skip the bridge / fp16 comparators")
+    p.add_argument("--no-baselines", action="store_true", help="skip the bridge / fp16 / dense SDPA comparators")
     p.add_argument("--c2-only", action="store_true", help="default run: skip the C3 and C4 figures")
     p.add_argument("--profile", action="store_true", help="calibration copy + --steps decode steps only")
     p.add_argument("--summarize", metavar="DIR", help="turn rocprofv3 CSV output under DIR into profiles/")
@@ -1059,6 +1059,40 @@ def k1c_summary(d):
 C4 = dict(B=32, H=16, T=8192, chunk=512, steps=256)
 
 
+def dense_sdpa_comparator(qc, T, stream):
+    """torch's own flash attention on the last C4 chunk's shape with DENSE
+    bf16 K/V: the chunk's 512 queries against all T keys, no mask (the
+    packed prefill's causal last chunk computes ~3 % fewer pairs), each
+    backend torch offers on this build (aotriton flash and memory-efficient).
+    TFLOP/s on the pairs each computes.  A comparator only: it reads
+    materialised K/V the packed path never holds."""
+    import torch
+    import torch.nn.functional as Fn
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    b_, h, nq, d = qc.shape
+    gen = torch.Generator(device=qc.device).manual_seed(5)
+    k = torch.randn((b_, h, T, d), generator=gen, device=qc.device, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn((b_, h, T, d), generator=gen, device=qc.device, dtype=torch.bfloat16)
+    flops = 4.0 * b_ * h * nq * T * d
+    out = {"shape": f"B={b_} H={h} q={nq} keys={T} d={d} bf16, no mask", "flops": flops,
+           "fa_library": str(torch.backends.cuda.preferred_rocm_fa_library())}
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(be):
+                ms = timed(lambda: Fn.scaled_dot_product_attention(qc, k, v), 5, 2, stream)
+        except RuntimeError as e:   # backend not built for this device
+            out[name] = {"error": str(e)[:120]}
+            continue
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1), "frac": round(tf / 2500, 4)}
+        log(f"[bench] C4 dense comparator: torch SDPA {name} ({out['fa_library']}) on dense bf16 K/V, "
+            f"{nq} queries x {T} keys: {ms * 1e3:.0f} us, {tf:.0f} TFLOP/s ({tf / 2500:.1%})")
+    del k, v
+    torch.cuda.empty_cache()
+    return out
+
+
 def main_c4(args, emit=True):
     """C4: a streaming packed cache of Ouro-like
     slots (MHA, 16 kv heads, d=128, batch 32, N(0,1) bf16 activations, GPU
@@ -1123,6 +1157,7 @@ def main_c4(args, emit=True):
     cache.seq_length[0], cache.seq_compressed[0] = saved
     for name in ("K", "V"):
         cache.side(0, name).blocks.fill_(cache.compressed[0] // 64)
+    dense = None if args.no_baselines else dense_sdpa_comparator(qc, T, stream)
 
     # ---- decode steps: append, attend (fast kernel), compress every 64 tokens
     qd = torch.randn((b_, h, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
@@ -1175,6 +1210,8 @@ def main_c4(args, emit=True):
         "prefill_roofline": {"bound": "mfma", "achieved": round(mfma, 1), "peak": 2500.0, "unit": "TFLOP/s",
                              "frac": round(mfma / 2500, 4), "flops_per_slot": flops},
         "prefill_kernel_last_chunk_us": round(pk_ms * 1e3, 1),
+        "prefill_kernel_last_chunk_tflops": round(last_flops / (pk_ms * 1e-3) / 1e12, 1),
+        "dense_sdpa_comparator": dense,
         "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "decode step (append + fast decode + merge + policy)", "algorithmic_bytes": dec_bytes},
@@ -1686,6 +1723,8 @@ def main():
         result["c4"] = {"workload": r4["config"]["workload"], "prefill_ms_per_slot": r4["prefill_ms_per_slot"],
                         "prefill_mfma_frac": r4["prefill_roofline"]["frac"],
                         "prefill_kernel_last_chunk_us": r4["prefill_kernel_last_chunk_us"],
+                        "prefill_kernel_last_chunk_tflops": r4["prefill_kernel_last_chunk_tflops"],
+                        "dense_sdpa_comparator": r4["dense_sdpa_comparator"],
                         "decode_us_per_slot_step": r4["value"], "decode_hbm_frac": r4["roofline"]["frac"]}
     print(json.dumps(result), flush=True)
 

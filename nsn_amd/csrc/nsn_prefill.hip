@@ -47,6 +47,7 @@ constexpr int kQTile = 32 * kWaves;      // chunk queries per workgroup
 constexpr int kKP = 136;      // K' row pitch (halves): 272 B rows
 constexpr int kVP = 72;       // V'^T row pitch (halves): 144 B rows
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.f;  // running-maximum slack (log2 units): weights < 2^8
 
 // D = A B + C on the compute dtype CT (NSN_DTYPE_F16 or NSN_DTYPE_BF16).
 template <int CT>
@@ -72,14 +73,30 @@ __device__ __forceinline__ uint32_t pk(float a, float b) {
         return __builtin_bit_cast(uint32_t, h);
     }
 }
+// Maxima of scores as single v_max3_f32 / v_max_f32 instructions.  fmaxf
+// compiles to the same instructions plus a self-max per operand that the
+// compiler cannot prove canonical (MFMA results, lane swaps): the quieting of
+// signalling NaNs, which a score never is (a NaN score is a quiet NaN out of
+// the MFMA, ignored by the maximum as fmaxf ignores it, and it still reaches
+// the output through its weight).  Half the maximum's instructions were those.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max2f(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 // Maximum over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48),
 // on every lane, without LDS: v_permlane16_swap gives rows (0,0,2,2) and
 // (1,1,3,3), v_permlane32_swap the halves (lo,lo) and (hi,hi).
 __device__ __forceinline__ float rows4_max(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max2f(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max2f(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 // fp32 pair -> bf16 hi (round to nearest even) + bf16 lo = rn(x - hi): the
 // pair to ~2^-17 relative.
@@ -559,13 +576,17 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                     for (int i = 0; i < 4; ++i)
                         if (16 * tt + 4 * g + i > lim) s[tt][qt][i] = -INFINITY;
             }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
-                mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qt][0], s[tt][qt][1]), fmaxf(s[tt][qt][2], s[tt][qt][3])));
+            const f32x4 *v = &s[0][qt];   // (stride 2: s[tt][qt] = v[2 * tt])
+            const float a0 = max3f(v[0][0], v[0][1], v[0][2]), a1 = max3f(v[0][3], v[2][0], v[2][1]);
+            const float a2 = max3f(v[2][2], v[2][3], v[4][0]), a3 = max3f(v[4][1], v[4][2], v[4][3]);
+            const float a4 = max3f(v[6][0], v[6][1], v[6][2]);
+            float mx = max2f(max3f(a0, a1, a2), max3f(a3, a4, v[6][3]));
             mx = rows4_max(mx);
             if (!QPRE) mx *= p.qscale;   // (bf16: the scores scale inside the exponent below)
-            if (__builtin_amdgcn_ballot_w64(mx > m_run[qt])) {
+            // The running maximum moves only when a score passes it by more
+            // than kLazy (log2 units): weights then stay below 2^kLazy, which
+            // every weight form holds exactly as well as weights below 1.
+            if (__builtin_amdgcn_ballot_w64(mx > m_run[qt] + kLazy)) {
                 const float mnew = fmaxf(m_run[qt], mx);
                 const float alpha = (m_run[qt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qt] - mnew);
                 lsum[qt] *= alpha;
