@@ -214,6 +214,11 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     float (*const pmax)[kDim] = reinterpret_cast<float (*)[kDim]>(xraw + 8192);    // [16][128]
     __shared__ float nrm_s[kBlockTok], den_s[kBlockTok], rcp_s[kBlockTok];
     __shared__ double rden_s[DT == NSN_DTYPE_F16 ? 1 : kBlockTok];   // fp16 input divides by den and rcp
+    // Per-channel constants, channel c at [chx(c)] = 16 * (c % 8) + c / 8: the
+    // code pass reads channel 8*cg + e in lanes cg = 0..15 at once, which this
+    // order puts on 16 consecutive words (channel-order storage put them 8
+    // words apart: 4 lanes on each bank).
+    auto chx = [](int c) { return 16 * (c & 7) + (c >> 3); };
     __shared__ float m_s[kDim];
     __shared__ double rs_s[kDim];
     __shared__ float yh_s[kDim], yl_s[kDim];
@@ -361,17 +366,17 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
                 hi = fmaxf(hi, pmax[w][tid]);
             }
             const float s = div_by_recip(hi - lo, recip_rn(kLevels));
-            m_s[tid] = lo;
+            m_s[chx(tid)] = lo;
             // 1/s; for s == 0 the reference divides by 1 (every d - m is 0 then),
             // or zeroes the codes when zero_flat_scale is set: a factor of 0
             const double rs = (s == 0.f) ? (p.zero_flat_scale ? 0.0 : 1.0) : recip_rn(s);
-            rs_s[tid] = rs;
+            rs_s[chx(tid)] = rs;
             // 1/s as yh + yl: yh = RN32(1/s) (= RN32(RN64(1/s)): 1/s is never
             // within 2^-48 of an fp32 midpoint), yl = RN32(RN64(1/s) - yh).  s == 0
             // multiplies by 1 (or by 0 under zero_flat_scale) with yl = 0: exact.
             const float yh = static_cast<float>(rs);
-            yh_s[tid] = yh;
-            yl_s[tid] = static_cast<float>(rs - static_cast<double>(yh));
+            yh_s[chx(tid)] = yh;
+            yl_s[chx(tid)] = static_cast<float>(rs - static_cast<double>(yh));
             // A nonzero s below 2^-64 takes the fp64 loop: the low product could
             // leave the normal range, and with a subnormal s the quotient
             // (d - m) / s can pass the top level (s then also underflows fp16,
@@ -380,8 +385,8 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
             const uint16_t hm = f32_to_f16_bits(lo), hs = f32_to_f16_bits(s);
             p.mins[ob * kDim + tid] = hm;
             p.scales[ob * kDim + tid] = hs;
-            mh_s[tid] = f16_bits_to_f32(hm);
-            sh_s[tid] = f16_bits_to_f32(hs);
+            mh_s[chx(tid)] = f16_bits_to_f32(hm);
+            sh_s[chx(tid)] = f16_bits_to_f32(hs);
             if ((hm & 0x7c00u) == 0x7c00u || (hs & 0x7c00u) == 0x7c00u) status_acc |= NSN_ST_META_NONFINITE;
             if (s != 0.f && (hs & 0x7fffu) == 0) status_acc |= NSN_ST_META_UNDERFLOW;
         } else if (tid < kDim + kBlockTok) {
@@ -426,16 +431,16 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
                 float yh = 0.f, yl = 0.f, mh = 0.f, sh = 0.f;
                 double rs = 0.0;
                 if (CLAMP) {
-                    rs = rs_s[c];
+                    rs = rs_s[chx(c)];
                 } else {
-                    yh = yh_s[c];
-                    yl = yl_s[c];
+                    yh = yh_s[chx(c)];
+                    yl = yl_s[chx(c)];
                 }
                 if (FAC) {
-                    mh = mh_s[c];
-                    sh = sh_s[c];
+                    mh = mh_s[chx(c)];
+                    sh = sh_s[chx(c)];
                 }
-                const float m = m_s[c];
+                const float m = m_s[chx(c)];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float t = d[j][e] - m;
@@ -502,9 +507,9 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int c = 8 * cg + e;
-                    const float t = d[j][e] - m_s[c];
-                    const float q = clamp ? fminf(static_cast<float>(static_cast<double>(t) * rs_s[c]), kLevels)
-                                          : __builtin_fmaf(t, yh_s[c], t * yl_s[c]);
+                    const float t = d[j][e] - m_s[chx(c)];
+                    const float q = clamp ? fminf(static_cast<float>(static_cast<double>(t) * rs_s[chx(c)]), kLevels)
+                                          : __builtin_fmaf(t, yh_s[chx(c)], t * yl_s[chx(c)]);
                     w[e >> 2] |= (__float_as_uint(q + kRoundMagic) & 0xffu) << (8 * (e & 3));
                 }
                 udst[256 * j] = make_uint2(w[0], w[1]);
