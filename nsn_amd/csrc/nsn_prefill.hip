@@ -248,6 +248,13 @@ __device__ __forceinline__ int vpos(int t) {
     return (t & 32) | ((t & 12) << 1) | ((t & 16) >> 2) | (t & 3);
 }
 
+// V'^T row `r` keeps its 16-byte chunk c at position c ^ ((r / 8) % 4): the
+// fill writes channels 8*cg + e of four channel groups cg at once, rows 8
+// apart, which land on the same banks in plain order (4-way conflicts); the
+// PV operand reads (rows 16*ct + 0..15, one chunk) stay conflict-free.
+__device__ __forceinline__ int vchunk(int r, int c) { return c ^ ((r >> 3) & 3); }
+__device__ __forceinline__ int vcol_at(int r, int t) { return 8 * vchunk(r, vpos(t) >> 3) + (vpos(t) & 7); }
+
 // The block buffer compute reads: K' [64 tok][kKP], V'^T [128 ch][kVP].
 struct KV {
     uint16_t *kt, *vt;
@@ -300,7 +307,8 @@ __device__ __forceinline__ void fill_dense(const uint8_t *st, int valid, int rg,
     if constexpr (side == 1) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + e) * kVP + vpos(4 * rg)) = u32x2{vcol[e][0], vcol[e][1]};
+            *reinterpret_cast<u32x2 *>(kv.vt + (8 * cg + e) * kVP + vcol_at(8 * cg + e, 4 * rg)) =
+                u32x2{vcol[e][0], vcol[e][1]};
     }
 }
 
@@ -360,7 +368,7 @@ __device__ __forceinline__ void fill_packed(const uint8_t *st, int rg, int cg, c
     if constexpr (side == 1) {
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-            uint16_t *dst = kv.vt + (8 * cg + O::chE[p]) * kVP + vpos(4 * rg);
+            uint16_t *dst = kv.vt + (8 * cg + O::chE[p]) * kVP + vcol_at(8 * cg + O::chE[p], 4 * rg);
             *reinterpret_cast<uint32_t *>(dst + 2 * pfirst) = vcol[p][0];
             *reinterpret_cast<uint32_t *>(dst + 2 * (pfirst ^ 1)) = vcol[p][1];
         }
@@ -624,7 +632,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(vtj + (16 * ct + row) * kVP + 32 * ks2 + 8 * g);
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(vtj + (16 * ct + row) * kVP +
+                                                                 8 * vchunk(16 * ct + row, 4 * ks2 + g));
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
                     acc[ct][qt] = mfma<DT>(a, pb[ks2][qt], acc[ct][qt]);
