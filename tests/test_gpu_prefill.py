@@ -122,6 +122,15 @@ def test_prefill_5bit():
     run_case(24, 2, 2, 2, [192, 100], 70, 5, torch.float16)
 
 
+@pytest.mark.parametrize("tail_dtype,precise", [(torch.bfloat16, None), (torch.float16, None),
+                                                (torch.float16, True)])
+def test_prefill_5bit_bf16_products(tail_dtype, precise):
+    """5-bit packed context under bf16 queries and chunk (the bf16 MFMA form of
+    the 5-bit kernel): over a bf16 or an fp16 tail, single-rounded or hi + lo
+    weights, across two query tiles with a ragged second one."""
+    run_case(29, 2, 4, 2, [300, 77], 300, 5, torch.bfloat16, tail_dtype=tail_dtype, precise=precise)
+
+
 @pytest.mark.parametrize("precise", [None, True])
 def test_prefill_bf16_products_with_an_fp16_tail(precise):
     """C4's mix: bf16 queries and chunk on the bf16 MFMA over an fp16 tail,
