@@ -107,6 +107,23 @@ def test_5bit_decode_vs_oracle(kernel):
     assert ok, err
 
 
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+@pytest.mark.parametrize("bits,Hq,Hkv", [(3, 8, 2), (3, 16, 2), (5, 16, 2)])
+def test_decode_fp16_queries_vs_oracle(kernel, bits, Hq, Hkv):
+    """fp16 queries (the fp16 query instantiations of both kernels; the fast
+    kernel splits them hi + lo as it does bf16 ones), GQA 4:1 and 8:1, 3 and
+    5 bits, fp16 tails."""
+    lengths = [700, 130]
+    k, v, _, kk, vv, seq = make_case(5, 2, Hq, Hkv, lengths, bits=bits)
+    rng = np.random.default_rng(55)
+    qh = torch.from_numpy(rng.standard_normal((2, Hq, 128)).astype(np.float32)).to(torch.float16)
+    out, ctx = kernels.decode_attention(qh.to(DEV), kk, vv, seq, kernel=kernel, kv_round_dtype=torch.float16)
+    ref = oracle_ctx(k, v, qh, lengths, bits, "float16" if kernel == "reference" else "float32")
+    ok, err = within(ctx.cpu().numpy(), ref)
+    assert ok, err
+    assert torch.equal(out.cpu(), ctx.cpu().to(torch.bfloat16))
+
+
 @pytest.mark.parametrize("split", [None, 512])
 def test_fast_stream_k_partition_many_sequences(split):
     """More than 64 sequences: the fast kernel cuts the blocks of all streams,
@@ -458,7 +475,7 @@ def test_empty_and_over_capacity_sequences_with_device_lengths(kernel):
     assert ok, err
 
 
-@pytest.mark.parametrize("Hq,Hkv,bits", [(8, 2, 3), (32, 4, 3), (8, 2, 5), (16, 8, 5)])
+@pytest.mark.parametrize("Hq,Hkv,bits", [(8, 2, 3), (32, 4, 3), (8, 2, 5), (16, 8, 5), (16, 2, 5)])
 def test_fast_bf16_tails_vs_oracle(Hq, Hkv, bits):
     """bf16 tails (the reference's dtype, loop_kv_qk01_kernel.py:66-69) on the
     fast kernel's bf16 MFMA path; packed tokens keep fp32 reconstructions."""
