@@ -322,6 +322,31 @@ def test_score_input_readout_config1(kernel):
         assert ok, err
 
 
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+@pytest.mark.parametrize("bits,Hq,Hkv,tail", [(5, 8, 2, "float16"), (3, 16, 2, "bfloat16"),
+                                               (5, 16, 2, "bfloat16")])
+def test_score_input_readout_ragged(kernel, bits, Hq, Hkv, tail):
+    """Score-input readout beyond C1: two ragged sequences, 5-bit V, GQA 8:1,
+    bf16 tails (the kernels' score-input instantiations past the C1 one)."""
+    rng = np.random.default_rng(31)
+    from nsn_amd import synthetic
+    lengths = [700, 130]
+    T = max(lengths)
+    v = synthetic.kv_tokens(rng, (2, Hkv), T)
+    scores = (rng.standard_normal((2, Hq, T)) * 4).astype(np.float32)
+    tdt = torch.bfloat16 if tail == "bfloat16" else torch.float16
+    vv, seq = cache.pack_sequences(torch.from_numpy(v).to(DEV), lengths, bits=bits, tail_dtype=tdt)
+    qdummy = torch.zeros(2, Hq, 128, dtype=torch.bfloat16, device=DEV)
+    _, ctx = kernels.decode_attention(qdummy, None, vv, seq, scores=torch.from_numpy(scores).to(DEV),
+                                      kv_round_dtype=tdt, kernel=kernel)
+    got = ctx.cpu().numpy()
+    for b, L in enumerate(lengths):
+        vr = oracle_restore(v[b], L, bits, tail if kernel == "reference" else "float32", tail)
+        ref = O.readout64(scores[b:b + 1, :, :L], vr[None], groups=Hq // Hkv)
+        ok, err = within(got[b:b + 1], ref)
+        assert ok, (b, err)
+
+
 @pytest.mark.parametrize("mode", ["dense", "bridge"])
 def test_fast_dense_and_bridge_vs_oracle(mode):
     """fp16-KV baseline (no packed blocks) and the bridge (packed K, restored V)."""
