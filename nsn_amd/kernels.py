@@ -114,7 +114,7 @@ def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
 def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
                      kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
                      scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True,
-                     static_workspace=False, trace_scores=None, trace_v=None):
+                     static_workspace=False, trace_scores=None, trace_v=None, validate_lengths=None):
     """Batched single-query decode attention.
 
     q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
@@ -128,6 +128,9 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     cap >= max_seq_len; reference kernel only) receive what the kernel itself
     computed for every token t < seq_len[b]: its scores and the V rows it
     multiplied (the TRACE stores of loop_kv_vf01_kernel.py:104,113).
+    ``validate_lengths`` (default: with ``check`` or without ``max_seq_len``)
+    copies the lengths and block counts to the host and checks them against
+    the buffers; callers that built them from tensor shapes pass False.
     """
     _dev.require_gpu(q, seq_len)
     require(q.ndim == 3 and q.shape[2] == DIM and q.is_contiguous(), "Query shape/type")
@@ -149,7 +152,9 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
     else:
         require(scores.dtype == torch.float32 and scores.is_contiguous() and scores.ndim == 3
                 and tuple(scores.shape[:2]) == (B, Hq), "Score shape/type")
-    if max_seq_len is None or check:
+    if validate_lengths is None:
+        validate_lengths = max_seq_len is None or check
+    if validate_lengths:
         _validate_lengths(seq_len, k if scores is None else None, v, scores, max_seq_len)
     if max_seq_len is None:
         max_seq_len = int(seq_len.max().item())
@@ -375,15 +380,15 @@ def _group_side(g, tail, bits=None, factors=False, status=None):
     f = None
     if factors:
         f = block_factors(codes.reshape(b_ * h, n, nbytes), *g["metas"], b, status=status).reshape(b_, h, n, BLOCK)
-    return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2], f,
-                    torch.full((1,), n, dtype=torch.int32, device=dev), tail.contiguous(), b)
+    return PackedKV(codes, g["metas"][0], g["metas"][1], g["metas"][2], f, _length_tensor(n, dev),
+                    tail.contiguous(), b)
 
 
 @functools.lru_cache(maxsize=256)
 def _length_tensor(T, device):
     """A [1] int32 device tensor holding T, made once per (T, device): the
-    batch-1 routes read it and never write it, so one fill per length serves
-    every call."""
+    batch-1 routes read it (as a length or a block count) and never write
+    it, so one fill per value serves every call."""
     return torch.full((1,), T, dtype=torch.int32, device=device)
 
 
@@ -475,6 +480,10 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
     """
     Hq = q.shape[1]
     T = _length(g, kt)
+    # the lengths and block counts below are built from these shapes, so the
+    # consistency check needs no device round trip
+    require(T > 0, "Empty sequence")
+    require(_length(vg, vt) == T, "K/V lengths differ")
     fast = kernel == "fast"
     ks, vs = _fast_sides(((g, kt), (vg, vt)), fast, status, q.device)
     seq = _length_tensor(T, q.device)
@@ -484,7 +493,8 @@ def launch(g, kt, q, vg, vt, trace=False, kernel="reference", status=None):
         tr_s = torch.empty((1, Hq, T), dtype=torch.float32, device=q.device)
         tr_v = torch.empty((1, Hkv, T, DIM), dtype=torch.float32, device=q.device)
     out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
-                                kv_round_dtype=kt.dtype, status=status, trace_scores=tr_s, trace_v=tr_v)
+                                kv_round_dtype=kt.dtype, status=status, trace_scores=tr_s, trace_v=tr_v,
+                                validate_lengths=False)
     score = vtr = None
     if trace and not fast:   # what the exact-order kernel itself computed
         score, vtr = tr_s, tr_v.to(vt.dtype)
@@ -561,16 +571,19 @@ def af_launch(g, tail, q, v, score=None, full=False, kernel="reference"):
     """
     Hq = q.shape[1]
     T = v.shape[2]
+    require(T > 0, "Empty sequence")
     vs = PackedKV(None, None, None, None, None, None, v.contiguous(), 3)
     seq = _length_tensor(T, v.device)
+    # lengths and block counts from the shapes: checked here, on the host
     if full:
+        require(_length(g, tail) == T, "K/V lengths differ")
         ks, = _fast_sides(((g, tail),), kernel == "fast", None, v.device)
         out, ctx = decode_attention(q.reshape(1, Hq, DIM), ks, vs, seq, max_seq_len=T, kernel=kernel,
-                                    kv_round_dtype=v.dtype)
+                                    kv_round_dtype=v.dtype, validate_lengths=False)
     else:
         require(score is not None and tuple(score.shape) == (1, Hq, T), "Score shape/type")
         out, ctx = decode_attention(q.reshape(1, Hq, DIM), None, vs, seq, max_seq_len=T, scores=score.contiguous(),
-                                    kernel=kernel, kv_round_dtype=v.dtype)
+                                    kernel=kernel, kv_round_dtype=v.dtype, validate_lengths=False)
     return out.reshape(1, 1, Hq, DIM), ctx.reshape(1, Hq, 1, DIM)
 
 
