@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from nsn_amd import cache, codec, kernels
-from nsn_amd.errors import NumericalFailure
+from nsn_amd.errors import IntegrityError, NumericalFailure
 from oracle import oracle as O
 from tests.golden import inputs as gi
 
@@ -395,6 +395,37 @@ def test_fast_matches_reference_launch_surface():
     _, c_fast, _, _ = kernels.launch(g, kt, q, vg, vt, kernel="fast")
     ok, err = within(c_fast.cpu().numpy(), c_ref.cpu().numpy().astype(np.float64))
     assert ok, err
+
+
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+def test_batch1_routes_check_lengths_on_the_host(kernel):
+    """launch() and af_launch() build the sequence length and block counts
+    from the tensor shapes and check them on the host: K and V of different
+    lengths, or an empty sequence, raise IntegrityError before any launch,
+    and a consistent call still matches the checked general entry."""
+    rng = np.random.default_rng(13)
+    from nsn_amd import synthetic
+    x = synthetic.kv_tokens(rng, (2, 4), 64 * 3 + 10)
+    k16 = torch.from_numpy(x[0]).to(DEV)[None]
+    v16 = torch.from_numpy(x[1]).to(DEV)[None]
+    g = codec.encode_group(k16[:, :, :192].reshape(1, 4, 3, 64, 128).contiguous(), 0)
+    vg = codec.encode_group(v16[:, :, :192].reshape(1, 4, 3, 64, 128).contiguous(), 0)
+    kt, vt = k16[:, :, 192:].contiguous(), v16[:, :, 192:].contiguous()
+    q = torch.from_numpy(rng.standard_normal((1, 8, 1, 128)).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    with pytest.raises(IntegrityError, match="K/V lengths differ"):
+        kernels.launch(g, kt, q, vg, vt[:, :, :9].contiguous(), kernel=kernel)
+    with pytest.raises(IntegrityError, match="Empty sequence"):
+        kernels.launch(None, kt[:, :, :0].contiguous(), q, None, vt[:, :, :0].contiguous(), kernel=kernel)
+    vdense = kernels.restore_v(vg, vt)
+    with pytest.raises(IntegrityError, match="K/V lengths differ"):
+        kernels.af_launch(g, kt, q, vdense[:, :, :200].contiguous(), full=True, kernel=kernel)
+    # consistent: the same context as the general entry with its device-side length check
+    _, c1, _, _ = kernels.launch(g, kt, q, vg, vt, kernel=kernel)
+    ks, vs = kernels._fast_sides(((g, kt), (vg, vt)), kernel == "fast", None, DEV)
+    seq = torch.full((1,), 202, dtype=torch.int32, device=DEV)
+    _, c2 = kernels.decode_attention(q.reshape(1, 8, 128), ks, vs, seq, max_seq_len=202, kernel=kernel,
+                                     kv_round_dtype=kt.dtype)
+    assert torch.equal(c1.reshape(1, 8, 128), c2)
 
 
 @pytest.mark.parametrize("fused", [True, False])
