@@ -287,18 +287,21 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // any LDS read (it cannot tell the stages apart), which serialises the
 // prefetch.  The kernel waits for its DMAs itself (vmcnt(0) at the top of each
 // block); an untracked VMEM operation can only make the compiler's own vmcnt
-// waits stricter, never looser.  M0 carries the LDS address.
+// waits stricter, never looser.  M0 carries the LDS address.  The loads carry
+// the non-temporal hint (`nt`): a step reads each packed block once, and
+// without the hint the streamed blocks are kept in the caches at the expense
+// of the step's own traffic (C2 split kernel 73.9 -> 67.1-67.7 us).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void *src, uint32_t *dst) {
     const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 // The same with a uniform 64-bit base (SGPRs) and a 32-bit lane offset: the
 // per-block address update is scalar and the lane offset loop-invariant.
 __device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t *dst) {
     const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
