@@ -233,7 +233,9 @@ def cpu_baseline(kk, vv, q, lengths, sample_tokens=8192, reps=10):
 ROTATE = 3         # copies of the packed C2 cache, used in turn by consecutive steps
 BATCH = 24         # launches per timed batch of the per-kernel rounds (fixed, whatever --steps)
 ROUNDS = 5         # interleaved rounds of batches
-WARM_STEPS = 200   # steps before the per-kernel rounds
+WARM_STEPS = 200   # steps before the measured launches of --profile
+SETTLE_STEPS = 1000   # steps before the per-kernel rounds and the timed region (the first few hundred
+                      # steps after the set-up run several us slower)
 
 
 def clone_packed(kv):
@@ -1571,18 +1573,6 @@ def main():
 
     log(f"[bench] decode: kernel={args.kernel} split={split} tokens x {n_splits} splits, "
         f"{B * HKV * n_splits} work units; {ROTATE} cache copies in turn; warmup {args.warmup}, steps {args.steps}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # the timed region: exactly `steps` steps, nothing else on the stream
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
     # Per-kernel durations, independent of --steps: after a fixed warm-up,
     # ROUNDS rounds of back-to-back batches of BATCH launches each -- steps,
     # split-only launches, merge-only launches, and steps over one cache copy
@@ -1591,7 +1581,7 @@ def main():
     # merge between its launches, so its per-launch time is the split
     # kernel's own duration plus the dispatch gap; the interleaving keeps all
     # four at one clock.
-    for _ in range(WARM_STEPS):
+    for _ in range(SETTLE_STEPS):
         step()
     kinds = (("step", step), ("split", split_kernel), ("merge", merge_kernel), ("single", step_single))
     marks = []
@@ -1609,6 +1599,22 @@ def main():
     for i, (name, ev) in enumerate(marks):
         nxt = marks[i + 1][1] if i + 1 < len(marks) else end
         per[name].append(ev.elapsed_time(nxt) / BATCH)
+    # The timed region follows the rounds, so that it measures a decode loop
+    # in service rather than the first steps after the set-up (5 warm-up
+    # steps right after it measured 76 us per step against 70 in the
+    # rounds): `warmup` steps, a synchronisation, then exactly `steps` steps,
+    # nothing else on the stream.
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
     mean = lambda xs: sum(xs) / len(xs)
     ms_split, ms_merge = mean(per["split"]), mean(per["merge"])
     ms_step_rounds, ms_single = mean(per["step"]), mean(per["single"])
@@ -1652,10 +1658,12 @@ def main():
                      "kernel_us": round(ms_split * 1e3, 2), "kernel_us_median": round(split_ts[len(split_ts) // 2] * 1e3, 2),
                      "merge_us": round(ms_merge * 1e3, 2), "step_us_same_rounds": round(ms_step_rounds * 1e3, 2),
                      "split_plus_merge_le_step": consistent,
-                     "timing": f"{WARM_STEPS} warm-up steps, then {ROUNDS} rounds of back-to-back batches of {BATCH} "
+                     "timing": f"{SETTLE_STEPS} warm-up steps, then {ROUNDS} rounds of back-to-back batches of {BATCH} "
                                "steps / split-only / merge-only / one-copy steps, enqueued without a host sync, HIP "
                                f"events between batches on the launch stream; every batch but the one-copy one "
                                f"turns over {ROTATE} copies of the packed cache"},
+        "value_timing": f"after the roofline rounds: {args.warmup} warm-up steps, a host synchronisation, then "
+                        f"{args.steps} steps between HIP events on the launch stream, nothing else on it",
         "cache_rotation": {"copies": ROTATE, "bytes_per_copy": nbytes,
                            "note": "value and roofline turn over the copies (no step re-reads the previous step's "
                                    "bytes); single_copy_step_us re-reads one copy every step"},
