@@ -251,9 +251,10 @@ class C2Decode:
     cache at separate addresses (3 x 365 MB, beyond the 256 MB Infinity
     Cache), consecutive steps using them in turn, preallocated workspace and
     outputs, launches with the host checks off (the first, checked call per
-    copy validates the cache).  split() is the split kernel alone, merge()
-    the merge alone, step() both over the next copy, step_single() both over
-    copy 0."""
+    copy validates the cache) from argument blocks built once per copy
+    (kernels.prepare_decode), as a serving loop would.  split() is the split
+    kernel alone, merge() the merge alone, step() both over the next copy,
+    step_single() both over copy 0."""
 
     def __init__(self, dev, lengths, k, v, q, kernel="fast"):
         import torch
@@ -279,18 +280,19 @@ class C2Decode:
                 ref = self.ctx.clone()
             assert torch.equal(self.ctx, ref), "the cache copies give different outputs"
         self.turn = 0
-        self._kernels = kernels
+        self._split_launch = [kernels.prepare_decode(q, ck, cv, self.seq, max_seq_len=self.max_len, kernel=kernel,
+                                                     split_tokens=split, workspace=self.ws, out=self.out,
+                                                     ctx=self.ctx, status=self.status, merge=False)
+                              for ck, cv in self.caches]
         self._lib = _lib
         self._merge_args = (self.ws.data_ptr(), B, HQ, self.n_splits, self.ctx.data_ptr(), self.out.data_ptr(),
                             _lib.DTYPE_BF16, self.status.data_ptr())
 
     def split(self, rotate=True):
-        ck, cv = self.caches[self.turn]
+        launch = self._split_launch[self.turn]
         if rotate:
             self.turn = (self.turn + 1) % ROTATE
-        self._kernels.decode_attention(self.q, ck, cv, self.seq, max_seq_len=self.max_len, kernel=self.kernel,
-                                       split_tokens=self.split_tokens, workspace=self.ws, out=self.out, ctx=self.ctx,
-                                       status=self.status, check=False, merge=False)
+        launch()
 
     def merge(self):
         self._lib.check(self._lib.lib().nsn_attention_merge(*self._merge_args, self.stream.cuda_stream),

@@ -111,27 +111,12 @@ def default_split(batch, heads_kv, max_len, target_units=4096, min_split=256):
     return max(BLOCK, split), max(1, math.ceil(max_len / max(BLOCK, split)))
 
 
-def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
+def _decode_args(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
                      kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
                      scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True,
                      static_workspace=False, trace_scores=None, trace_v=None, validate_lengths=None):
-    """Batched single-query decode attention.
-
-    q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
-    ctx [B,Hq,128] fp32).  ``scores`` [B, Hq, cap] fp32 replaces K (the AF01
-    FULL=False readout).  ``check`` syncs and raises NumericalFailure on any
-    nonfinite intermediate/output.  ``static_workspace`` runs through
-    nsn_decode_attention_static: the partials live in the library's per-device
-    scratch array (at most ``_lib.STATIC_SCRATCH_FLOATS`` floats), so with
-    ``out``, ``ctx`` and ``status`` given the call allocates nothing.
-    ``trace_scores`` [B, Hq, cap] and ``trace_v`` [B, Hkv, cap, 128] (fp32,
-    cap >= max_seq_len; reference kernel only) receive what the kernel itself
-    computed for every token t < seq_len[b]: its scores and the V rows it
-    multiplied (the TRACE stores of loop_kv_vf01_kernel.py:104,113).
-    ``validate_lengths`` (default: with ``check`` or without ``max_seq_len``)
-    copies the lengths and block counts to the host and checks them against
-    the buffers; callers that built them from tensor shapes pass False.
-    """
+    """decode_attention's checks and argument block: (entry point, args,
+    status, out, ctx, workspace)."""
     _dev.require_gpu(q, seq_len)
     require(q.ndim == 3 and q.shape[2] == DIM and q.is_contiguous(), "Query shape/type")
     B, Hq = q.shape[:2]
@@ -220,6 +205,35 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
         require(cap >= max_seq_len, "Trace capacity below max_seq_len")
         a.trace_cap = cap
     entry = "nsn_decode_attention_static" if static_workspace else "nsn_decode_attention"
+    return entry, a, st, out, ctx, workspace
+
+
+def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len=None, scores=None,
+                     kernel="reference", kv_round_dtype=None, split_tokens=None, out_dtype=torch.bfloat16,
+                     scale=SCALE, status=None, check=True, workspace=None, out=None, ctx=None, merge=True,
+                     static_workspace=False, trace_scores=None, trace_v=None, validate_lengths=None):
+    """Batched single-query decode attention.
+
+    q [B, Hq, 128]; seq_len i32 [B] (device); returns (out [B,Hq,128] out_dtype,
+    ctx [B,Hq,128] fp32).  ``scores`` [B, Hq, cap] fp32 replaces K (the AF01
+    FULL=False readout).  ``check`` syncs and raises NumericalFailure on any
+    nonfinite intermediate/output.  ``static_workspace`` runs through
+    nsn_decode_attention_static: the partials live in the library's per-device
+    scratch array (at most ``_lib.STATIC_SCRATCH_FLOATS`` floats), so with
+    ``out``, ``ctx`` and ``status`` given the call allocates nothing.
+    ``trace_scores`` [B, Hq, cap] and ``trace_v`` [B, Hkv, cap, 128] (fp32,
+    cap >= max_seq_len; reference kernel only) receive what the kernel itself
+    computed for every token t < seq_len[b]: its scores and the V rows it
+    multiplied (the TRACE stores of loop_kv_vf01_kernel.py:104,113).
+    ``validate_lengths`` (default: with ``check`` or without ``max_seq_len``)
+    copies the lengths and block counts to the host and checks them against
+    the buffers; callers that built them from tensor shapes pass False.
+    """
+    entry, a, st, out, ctx, _ = _decode_args(
+        q, k, v, seq_len, max_seq_len=max_seq_len, scores=scores, kernel=kernel, kv_round_dtype=kv_round_dtype,
+        split_tokens=split_tokens, out_dtype=out_dtype, scale=scale, status=status, check=check,
+        workspace=workspace, out=out, ctx=ctx, merge=merge, static_workspace=static_workspace,
+        trace_scores=trace_scores, trace_v=trace_v, validate_lengths=validate_lengths)
     rc = getattr(_lib.lib(), entry)(a, _dev.stream())
     _lib.check(rc, entry)
     if check and status is None:
@@ -236,6 +250,34 @@ def decode_attention(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_
             raise NumericalFailure("Nonfinite fused attention intermediate/output")
     return out, ctx
 
+
+def prepare_decode(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_len, **kwargs):
+    """decode_attention's checks and argument block, done once, for a loop
+    that decodes over the same buffers again and again (a serving loop's
+    fixed-shape steps; the C2 bench).  Takes decode_attention's arguments
+    (``max_seq_len`` required, ``check`` off) and returns ``launch()``, which
+    enqueues the same kernel launch(es) on the current stream with no other
+    host work, and whose return value is (out, ctx).  Each launch reads the
+    buffers' current contents (q, caches, lengths), so they may change
+    between launches, but not their storage or shapes; nonfinite and
+    capacity flags accumulate in ``status``, which the caller reads.
+    """
+    require(not kwargs.get("check", False), "prepare_decode launches without the host status check")
+    require(kwargs.get("trace_scores") is None and kwargs.get("trace_v") is None, "No trace outputs in prepared launches")
+    kwargs["check"] = False
+    kwargs.setdefault("validate_lengths", True)
+    if kwargs.get("status") is None:
+        kwargs["status"] = _dev.new_status(q.device)
+    entry, a, st, out, ctx, workspace = _decode_args(q, k, v, seq_len, max_seq_len=max_seq_len, **kwargs)
+    fn = getattr(_lib.lib(), entry)
+    keep = (q, k, v, seq_len, st, out, ctx, workspace)   # the storage the argument block points at
+
+    def launch():
+        _lib.check(fn(a, _dev.stream()), entry)
+        return keep[5], keep[6]
+
+    launch.status = st
+    return launch
 
 def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, k_chunk, v_chunk, *, scale=SCALE,
                       status=None, check=True, out=None, append=False, precise_weights=None):

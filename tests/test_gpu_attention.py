@@ -177,6 +177,30 @@ def test_split_invariance(kernel):
         assert np.allclose(o, outs[0], atol=atol, rtol=rtol)
 
 
+
+@pytest.mark.parametrize("kernel", ["reference", "fast"])
+def test_prepared_decode_equals_decode_attention(kernel):
+    """prepare_decode's launcher (argument block built once, as the C2 bench
+    and a serving loop use it) gives decode_attention's outputs bitwise, and
+    reads the buffers' current contents at every launch."""
+    lengths = [1500, 900, 64]
+    k, v, qb, kk, vv, seq = make_case(8, 3, 8, 2, lengths)
+    q = qb.to(DEV)
+    kw = dict(max_seq_len=max(lengths), kernel=kernel, split_tokens=256)
+    launch = kernels.prepare_decode(q, kk, vv, seq, **kw)
+    for it in range(3):
+        out, ctx = launch()
+        torch.cuda.synchronize()
+        got_out, got_ctx = out.clone(), ctx.clone()
+        want_out, want_ctx = kernels.decode_attention(q, kk, vv, seq, **kw)
+        assert torch.equal(got_ctx, want_ctx) and torch.equal(got_out, want_out)
+        assert int(launch.status.item()) == 0
+        q.mul_(-0.5)   # (new query values in the same storage)
+    with pytest.raises(IntegrityError):
+        kernels.prepare_decode(q, kk, vv, seq, check=True, **kw)
+    with pytest.raises(TypeError):
+        kernels.prepare_decode(q, kk, vv, seq, kernel=kernel)   # max_seq_len is required
+
 def test_gqa_equals_repeated_mha():
     """Invariant: q-head h of a GQA call equals an MHA call on kv-head h // G."""
     lengths = [300]
