@@ -824,18 +824,35 @@ def readout_arms(dev, rounds=5, calls=20, warm=20):
 C3 = dict(B=64, HQ=16, HKV=4, L=8192, bits=5)
 
 
-def interleaved_rounds(step, split, merge, steps, stream, rounds=5):
+def interleaved_rounds(step, split, merge, stream, rounds=ROUNDS, batch=BATCH, settle=SETTLE_STEPS):
     """Mean per-launch ms of a decode step, its split kernel alone and its
-    merge alone, from `rounds` interleaved rounds of back-to-back batches
-    (HIP events around each batch on the launch stream), so that all three
-    run at one clock.  Also returns the per-round split times (sorted)."""
-    per = max(4, steps // rounds)
-    rs, rk, rm = [], [], []
+    merge alone, as C2's rounds measure them: after `settle` untimed steps,
+    `rounds` rounds of back-to-back batches of `batch` launches of each kind,
+    enqueued without a host synchronisation, with a HIP event between
+    consecutive batches on the launch stream (so that all three run at one
+    clock, and the figures do not depend on --steps).  Also returns the
+    per-round split times (sorted) and the batch size."""
+    import torch
+    for _ in range(settle):
+        step()
+    kinds = (("step", step), ("split", split), ("merge", merge))
+    marks = []
     for _ in range(rounds):
-        rs.append(timed(step, per, 0, stream))
-        rk.append(timed(split, per, 0, stream))
-        rm.append(timed(merge, per, 0, stream))
-    return sum(rs) / rounds, sum(rk) / rounds, sum(rm) / rounds, sorted(rk), per
+        for name, fn in kinds:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(stream)
+            marks.append((name, ev))
+            for _ in range(batch):
+                fn()
+    end = torch.cuda.Event(enable_timing=True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    per = {name: [] for name, _ in kinds}
+    for i, (name, ev) in enumerate(marks):
+        nxt = marks[i + 1][1] if i + 1 < len(marks) else end
+        per[name].append(ev.elapsed_time(nxt) / batch)
+    mean = lambda xs: sum(xs) / len(xs)
+    return mean(per["step"]), mean(per["split"]), mean(per["merge"]), sorted(per["split"]), batch
 
 
 def main_c3(args, emit=True):
@@ -891,16 +908,21 @@ def main_c3(args, emit=True):
     kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
                              workspace=ws, out=out, ctx=ctx)
 
+    # launches from argument blocks built once (kernels.prepare_decode), as in C2
+    launches = {m: kernels.prepare_decode(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
+                                          workspace=ws, out=out, ctx=ctx, status=status, merge=m)
+                for m in (True, False)}
+
     def step(merge=True):
-        kernels.decode_attention(q, kk, vv, seq, max_seq_len=L, kernel=args.kernel, split_tokens=split,
-                                 workspace=ws, out=out, ctx=ctx, status=status, check=False, merge=merge)
+        launches[merge]()
     lib = _lib.lib()
 
     def merge_kernel():
         _lib.check(lib.nsn_attention_merge(ws.data_ptr(), b_, hq, n_splits, ctx.data_ptr(), out.data_ptr(),
                                            _lib.DTYPE_BF16, status.data_ptr(), stream.cuda_stream), "nsn_attention_merge")
+    # per-kernel rounds first, then the timed steps (as in C2)
+    _, ms_split, ms_merge, _, _ = interleaved_rounds(step, lambda: step(merge=False), merge_kernel, stream)
     ms_step = timed(step, args.steps, args.warmup, stream)
-    _, ms_split, ms_merge, _, _ = interleaved_rounds(step, lambda: step(merge=False), merge_kernel, args.steps, stream)
     assert _dev.read_status(status) == 0
     nbytes = b_ * hkv * 2 * L * (bits * 16 + 10) + 2 * b_ * hq * D * 2
     achieved = nbytes / (ms_split * 1e-3) / 1e9
@@ -923,7 +945,11 @@ def main_c3(args, emit=True):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
-                     "kernel_us": round(ms_split * 1e3, 2)},
+                     "kernel_us": round(ms_split * 1e3, 2), "merge_us": round(ms_merge * 1e3, 2),
+                     "timing": f"{SETTLE_STEPS} warm-up steps, then {ROUNDS} rounds of back-to-back batches of "
+                               f"{BATCH} steps / split-only / merge-only launches, enqueued without a host sync, HIP "
+                               "events between batches on the launch stream; one cache copy (378 MB, beyond the "
+                               "256 MB Infinity Cache); value: the timed steps after the rounds"},
         "encode_roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(enc_gbs / HBM_PEAK_GBS, 4)},
         "parity_ok": ok,
