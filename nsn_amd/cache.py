@@ -10,8 +10,6 @@ launch straight into preallocated storage.
 """
 from __future__ import annotations
 
-import math
-
 import torch
 
 from . import _dev, _lib

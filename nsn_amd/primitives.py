@@ -14,7 +14,7 @@ import math
 import torch
 
 from . import _dev, _lib
-from .errors import IntegrityError, NumericalFailure, require
+from .errors import NumericalFailure, require
 
 BLOCK = 64
 DIM = 128
