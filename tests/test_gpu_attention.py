@@ -178,16 +178,18 @@ def test_split_invariance(kernel):
 
 
 
-@pytest.mark.parametrize("kernel", ["reference", "fast"])
-def test_prepared_decode_equals_decode_attention(kernel):
+@pytest.mark.parametrize("kernel,static", [("reference", False), ("fast", False), ("fast", True)])
+def test_prepared_decode_equals_decode_attention(kernel, static):
     """prepare_decode's launcher (argument block built once, as the C2 bench
-    and a serving loop use it) gives decode_attention's outputs bitwise, and
-    reads the buffers' current contents at every launch."""
+    and a serving loop use it; with static=True over the library's static
+    scratch, so that a launch allocates nothing) gives decode_attention's
+    outputs bitwise, and reads the buffers' current contents at every
+    launch."""
     lengths = [1500, 900, 64]
     k, v, qb, kk, vv, seq = make_case(8, 3, 8, 2, lengths)
     q = qb.to(DEV)
     kw = dict(max_seq_len=max(lengths), kernel=kernel, split_tokens=256)
-    launch = kernels.prepare_decode(q, kk, vv, seq, **kw)
+    launch = kernels.prepare_decode(q, kk, vv, seq, static_workspace=static, **kw)
     for it in range(3):
         out, ctx = launch()
         torch.cuda.synchronize()
