@@ -943,7 +943,8 @@ def main_c3(args, emit=True):
                    "kernel": args.kernel, "split_tokens": split, "n_splits": n_splits},
         "encode_us": round(enc_ms * 1e3, 1), "encode_gbs": round(enc_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_c3_traffic() if args.kernel == "fast" else None,
                      "kernel": f"attn split kernel ({args.kernel})", "algorithmic_bytes": nbytes,
                      "kernel_us": round(ms_split * 1e3, 2), "merge_us": round(ms_merge * 1e3, 2),
                      "timing": f"{SETTLE_STEPS} warm-up steps, then {ROUNDS} rounds of back-to-back batches of "
@@ -1253,7 +1254,9 @@ def main_c4(args, emit=True):
 
 STATS_DOC = {
     "c3": ("attn_fast_c3", "C3: 5-bit packed K/V, B=64, 16q/4kv, ctx 8192 -- encode of all blocks + decode steps",
-           "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c3 --no-cpu"),
+           "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c3 --no-cpu\n"
+           "rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o p -- python3 bench.py --workload c3 --no-cpu\n"
+           "rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o p -- python3 bench.py --workload c3 --no-cpu"),
     "c4": ("prefill_c4", "C4: streaming cache, MHA 16 kv-heads, batch 32 -- 8192-token chunked prefill + decode steps",
            "rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o kt -- python3 bench.py --workload c4 "
            "--slots 1 --decode-steps 16\n"
@@ -1504,6 +1507,61 @@ def adapter_summary(d):
     print("\n".join(L))
 
 
+C3_SPLIT_KERNEL = "nsn::fast::attn_fast_kernel<5, 1, false, 4, false>"
+C3_ENCODE_KERNEL = "nsn::encode_kernel<0, 5, 0>"
+C3_JSON = ROOT / "profiles" / "attn_fast_c3.json"
+
+
+def c3_traffic_lines(d):
+    """HBM traffic of the C3 split kernel and of the C3 encode launch (all K
+    and V blocks) from the FETCH_SIZE / WRITE_SIZE passes under OUT/fetch and
+    OUT/write, scaled by the factors the C2 profile's 1 GiB calibration copy
+    measured on this GPU type; also writes profiles/attn_fast_c3.json, which
+    the C3 line reads while the kernel source is unchanged."""
+    import statistics
+    c2 = json.loads(PROFILE_JSON.read_text())
+    fs, ws = c2["fetch_scale"], c2["write_scale"]
+
+    def per(counter, sub, kernel, largest=False):
+        vals = [float(r["Counter_Value"]) for r in _rows((Path(d) / sub, "**/*counter_collection.csv"))
+                if r["Counter_Name"] == counter and kernel in r["Kernel_Name"]]
+        return max(vals) if largest else statistics.median(vals), len(vals)
+
+    fk, n = per("FETCH_SIZE", "fetch", C3_SPLIT_KERNEL)
+    wk, _ = per("WRITE_SIZE", "write", C3_SPLIT_KERNEL)
+    efk, _ = per("FETCH_SIZE", "fetch", C3_ENCODE_KERNEL, largest=True)
+    ewk, _ = per("WRITE_SIZE", "write", C3_ENCODE_KERNEL, largest=True)
+    rd, wr = fk * 1024 * fs, wk * 1024 * ws
+    erd, ewr = efk * 1024 * fs, ewk * 1024 * ws
+    b_, hq, hkv, L, bits = C3["B"], C3["HQ"], C3["HKV"], C3["L"], C3["bits"]
+    alg = b_ * hkv * 2 * L * (bits * 16 + 10) + 2 * b_ * hq * D * 2
+    enc_alg = 2 * b_ * hkv * L * 346
+    fig = {"kernel": C3_SPLIT_KERNEL, "source_sha256": source_sha(), "workload": "C3", "dispatches": n,
+           "fetch_kib": fk, "write_kib": wk, "fetch_scale": fs, "write_scale": ws,
+           "read_bytes": int(rd), "write_bytes": int(wr), "traffic": int(rd + wr), "algorithmic_bytes": alg,
+           "encode_traffic": int(erd + ewr), "encode_algorithmic_bytes": enc_alg}
+    C3_JSON.write_text(json.dumps(fig, indent=1) + "\n")
+    return ["## HBM traffic per dispatch (the FETCH_SIZE and WRITE_SIZE passes above)", "",
+            f"Scaled by the factors of the calibration copy in `profiles/attn_fast_c2.md` (same GPU type): reads "
+            f"x{fs:.3f}, writes x{ws:.3f}.", "",
+            "| dispatch | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes | algorithmic | ratio |", "|---|---|---|---|---|---|",
+            f"| split kernel (median of {n}) | {fk:.0f} | {wk:.0f} | {(rd + wr) / 1e6:.1f} MB | {alg / 1e6:.1f} MB | "
+            f"{(rd + wr) / alg:.3f} |",
+            f"| encode of all K and V blocks (the largest encode dispatch) | {efk:.0f} | {ewk:.0f} | "
+            f"{(erd + ewr) / 1e6:.1f} MB | {enc_alg / 1e6:.1f} MB | {(erd + ewr) / enc_alg:.3f} |", "",
+            f"Kernel source sha256 (nsn_amd/csrc/nsn_fast.hip): `{source_sha()}`", ""]
+
+
+def measured_c3_traffic():
+    """HBM bytes per C3 split-kernel launch from the committed profile, if it
+    was measured on this kernel source; else None."""
+    try:
+        fig = json.loads(C3_JSON.read_text())
+    except (OSError, ValueError):
+        return None
+    return fig["traffic"] if fig.get("source_sha256") == source_sha() else None
+
+
 def stats_summary(d, workload):
     """profiles/<name>.md from the kernel statistics of one rocprofv3 run."""
     name, title, cmd = STATS_DOC[workload]
@@ -1518,6 +1576,8 @@ def stats_summary(d, workload):
                  f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
                  f"{float(r['TotalDurationNs']) / 1e6:.2f} |")
     L.append("")
+    if workload == "c3" and (Path(d) / "fetch").is_dir() and (Path(d) / "write").is_dir():
+        L += c3_traffic_lines(d)
     sq = _sq(d, PREFILL_KERNEL, last=PREFILL_LAST_CALLS) if workload == "c4" else {}
     if sq:
         L += ["## SQ counters of the prefill kernel on the last chunk (the sq1 and sq2 passes above)", "",
@@ -1752,6 +1812,7 @@ def main():
         r3 = main_c3(sub, emit=False)
         result["c3"] = {"workload": r3["config"]["workload"], "step_us": r3["value"],
                         "split_kernel_us": r3["roofline"]["kernel_us"], "hbm_frac": r3["roofline"]["frac"],
+                        "traffic": r3["roofline"]["traffic"],
                         "encode_us": r3["encode_us"], "encode_hbm_frac": r3["encode_roofline"]["frac"],
                         "parity_ok": r3["parity_ok"]}
         torch.cuda.empty_cache()
