@@ -204,3 +204,22 @@ def test_abi_struct_sizes_match_the_bindings():
     class Grown(ctypes.Structure):   # a layout with one more field than the library's
         _fields_ = _lib.AttnArgs._fields_ + [("extra", ctypes.c_void_p)]
     assert lib.nsn_abi_sizeof(1) != ctypes.sizeof(Grown)
+
+
+def test_integration_binding_stubs_match_the_bindings():
+    """The ctypes stubs INTEGRATION.md gives a maintainer (its python blocks'
+    struct classes) have the package's field names, offsets and sizes."""
+    import ctypes
+    doc = (Path(__file__).resolve().parent.parent / "INTEGRATION.md").read_text()
+    ns = {"ctypes": ctypes, "P": ctypes.c_void_p, "I32": ctypes.c_int, "I64": ctypes.c_int64}
+    for block in re.findall(r"```python\n(.*?)```", doc, re.S):
+        classes = re.findall(r"^class \w+\(ctypes\.Structure\):.*?\n(?:    .*\n)+", block, re.M)
+        for c in classes:
+            exec(c, ns)
+    for name in ("KVSide", "AttnArgs", "PrefillArgs", "KScoreArgs"):
+        assert name in ns, f"INTEGRATION.md has no {name} stub"
+        doc_st, pkg_st = ns[name], getattr(_lib, name)
+        assert [f[0] for f in doc_st._fields_] == [f[0] for f in pkg_st._fields_], name
+        assert ctypes.sizeof(doc_st) == ctypes.sizeof(pkg_st), name
+        for f, _ in doc_st._fields_:
+            assert getattr(doc_st, f).offset == getattr(pkg_st, f).offset, (name, f)
