@@ -279,6 +279,7 @@ def prepare_decode(q, k: Optional[PackedKV], v: PackedKV, seq_len, *, max_seq_le
     launch.status = st
     return launch
 
+
 def prefill_attention(q, k: Optional[PackedKV], v: Optional[PackedKV], ctx_len, k_chunk, v_chunk, *, scale=SCALE,
                       status=None, check=True, out=None, append=False, precise_weights=None):
     """Chunked-prefill attention over a packed context (C4's prefill step).
