@@ -429,6 +429,24 @@ def _sq_lines(sq, blocks_per_wave=None):
     return L
 
 
+def split_resource_lines():
+    """The split kernel's registers, spills, scratch, LDS and occupancy as
+    the compiler reports them for the current source (the build's flags)."""
+    from nsn_amd import build
+    ks = build.resource_usage("nsn_fast.hip")
+    name = next((n for n in ks if "attn_fast_kernelILi3ELi1ELb0ELi4ELb0E" in n), None)
+    if name is None:
+        return []
+    r = ks[name]
+    return ["## Compiler resources of the split kernel (`python -m nsn_amd.build --resource-usage`)", "",
+            "| VGPR | AGPR | SGPR | SGPR spill | VGPR spill | scratch B/lane | LDS B/workgroup | waves/SIMD |",
+            "|---|---|---|---|---|---|---|---|",
+            "| " + " | ".join(str(r.get(k, "?")) for k in ("vgpr", "agpr", "sgpr", "sgpr_spill", "vgpr_spill",
+                                                        "scratch", "lds", "occupancy")) + " |", "",
+            "Where the spills sit (outside the packed-block loop but for 6 SGPR reloads per two blocks): "
+            "profiles/resource_usage.md.", ""]
+
+
 def summarize(d):
     """Write profiles/attn_fast_c2.{md,json} from rocprofv3 CSV output under d
     (subdirectories kt/, fetch/, write/ made by the commands in the module docstring)."""
@@ -499,8 +517,10 @@ def summarize(d):
         L += ["## SQ counters (rocprofv3 --pmc, the sq1 and sq2 passes above)", ""]
         L += _sq_lines(sq, blocks_per_wave=sum((x + 63) // 64 for x in lens) * HKV / sq["SQ_WAVES"])
         L += ["", f"With 2 waves per SIMD the SIMD's VALU port is busy about twice the per-wave VALU-issue "
-              f"share while the waves live; the mean wave lifetime ({4 * sq['SQ_WAVE_CYCLES'] / sq['SQ_WAVES'] / (sq['GRBM_GUI_ACTIVE'] / 8) :.0%} of the "
-              f"dispatch's GPU-active cycles) shows the end-of-kernel imbalance.", ""]
+              f"share while the waves live; the mean wave lifetime is {4 * sq['SQ_WAVE_CYCLES'] / sq['SQ_WAVES'] / (sq['GRBM_GUI_ACTIVE'] / 8) :.0%} of the "
+              f"dispatch's GPU-active cycles (the dispatch ramp and the end-of-kernel imbalance; the same share "
+              f"in every profile of this kernel so far).", ""]
+    L += split_resource_lines()
     PROFILE_MD.write_text("\n".join(L))
     print("\n".join(L))
     if fetch["encode"] and write["encode"]:
