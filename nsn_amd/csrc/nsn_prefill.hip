@@ -182,10 +182,12 @@ struct PrefillParams {
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-// 16 bytes per lane from global memory straight into LDS at M0 + 16*lane.
+// 16 bytes per lane from global memory straight into LDS at M0 + 16*lane,
+// with the non-temporal hint: a workgroup streams each block of its context
+// once (C4 last chunk 1241-1242 -> 1222-1228 us).
 __device__ __forceinline__ void dma16(const void *src, void *dst) {
     const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
