@@ -150,6 +150,7 @@ __device__ __forceinline__ void block_factors_lds(const uint8_t *codes_s, const 
 constexpr float kRoundMagic = 12582912.f;   // 1.5 * 2^23: q + this rounds q half-even into the low mantissa bits
 
 typedef _Float16 enc_h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t enc_u4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float half_lo(uint32_t w) { return static_cast<float>(__builtin_bit_cast(enc_h2, w)[0]); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return static_cast<float>(__builtin_bit_cast(enc_h2, w)[1]); }
 
@@ -238,16 +239,19 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     }
     {
         // ---- load: the thread's 4 rows x 8 channels as raw dwords (16-byte
-        // loads; a wave reads 1 KiB of consecutive input per row group)
+        // loads; a wave reads 1 KiB of consecutive input per row group).  The
+        // input is read once, so the loads carry the non-temporal hint (C2
+        // encode 385.3 -> 377.8 us, mean of 4 alternating rounds).
         const T *x = static_cast<const T *>(p.x) + static_cast<int64_t>(o) * p.x_outer_stride +
                      (p.x_token_offset + static_cast<int64_t>(i) * kBlockTok) * kDim;
         uint32_t xw[4][NW];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint4 *src = reinterpret_cast<const uint4 *>(x + (r0 + 16 * j) * kDim + 8 * cg);
+            const enc_u4 *src = reinterpret_cast<const enc_u4 *>(x + (r0 + 16 * j) * kDim + 8 * cg);
 #pragma unroll
             for (int h = 0; h < NW / 4; ++h) {
-                const uint4 a = src[h];
+                const enc_u4 a4 = __builtin_nontemporal_load(src + h);
+                const uint4 a = make_uint4(a4[0], a4[1], a4[2], a4[3]);
                 xw[j][4 * h] = a.x; xw[j][4 * h + 1] = a.y; xw[j][4 * h + 2] = a.z; xw[j][4 * h + 3] = a.w;
             }
         }
